@@ -1,0 +1,159 @@
+/*
+ * hh_oracle.h -- CPU restatement of the reference HCT decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it.
+ * The product (haagenti_amd) never links or calls it.
+ *
+ * Every function restates a reference function (cited as file:line, paths
+ * relative to the reference repository root) in plain C11 so that the GPU
+ * path can be compared with it on identical inputs.
+ *
+ * Parity status of each function (how the restatement itself is pinned) is
+ * listed next to it; tests/test_oracle_*.py hold the checks.
+ */
+#ifndef HH_ORACLE_H
+#define HH_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error kinds, same meaning as haagenti_core::Error
+ * (crates/haagenti-core/src/error.rs:10-60). */
+enum {
+    HHO_OK = 0,
+    HHO_CORRUPTED_DATA = 1,
+    HHO_BUFFER_TOO_SMALL = 2,
+    HHO_UNEXPECTED_EOF = 3,
+    HHO_ALGORITHM = 6,   /* Error::Algorithm ("hct" read failures, tensor.rs:421-431,470-480) */
+};
+
+/* Sub-kinds of CorruptedData raised by decompress_block / the HCT parsers. */
+enum {
+    HHO_CORRUPT_NONE = 0,
+    HHO_CORRUPT_ZERO_OFFSET = 1,      /* block.rs:320-322 "invalid zero offset" */
+    HHO_CORRUPT_OFFSET_BEYOND = 2,    /* block.rs:323-325 "offset beyond output at offset N" */
+    HHO_CORRUPT_BITMAP_COUNT = 3,     /* compressive.rs:630-636 popcount != k */
+    HHO_CORRUPT_HEADER = 4,           /* tensor.rs:311-331 magic/version/algo/dtype */
+    HHO_CORRUPT_SIZE = 5,             /* size/shape inconsistencies in containers */
+};
+
+typedef struct hho_err {
+    int32_t kind;       /* HHO_* */
+    int32_t sub;        /* HHO_CORRUPT_* */
+    uint64_t position;  /* UnexpectedEof: bytes_read; OffsetBeyond: output_pos */
+    uint64_t required;  /* BufferTooSmall: required */
+    uint64_t provided;  /* BufferTooSmall: provided */
+} hho_err;
+
+/* ---------------- LZ4 raw block (crates/haagenti-lz4/src/block.rs) ------- */
+
+/* block.rs:370-373 */
+size_t hho_lz4_max_compressed_size(size_t input_len);
+
+/* block.rs:73-147 (+ write_sequence :150-209, write_last_literals :212-251).
+ * Returns HHO_OK and sets *written, or HHO_BUFFER_TOO_SMALL. */
+int hho_lz4_compress_block(const uint8_t *in, size_t in_len, uint8_t *out,
+                           size_t out_cap, size_t *written, hho_err *err);
+
+/* block.rs:261-366.  out_len is output.len(), output_size the expected size
+ * (they are equal in every reference caller, decompress.rs:59-68). */
+int hho_lz4_decompress_block(const uint8_t *in, size_t in_len, uint8_t *out,
+                             size_t out_len, size_t output_size,
+                             size_t *written, hho_err *err);
+
+/* Many independent blocks; nthreads workers (0 = all cores).  Per-block
+ * status in kinds[]/written[].  Mirrors the rayon par_iter structure of
+ * crates/haagenti/src/pipeline/turbo.rs:236-261 for the CPU baseline. */
+void hho_lz4_decompress_batch(const uint8_t *in, const uint64_t *in_off,
+                              const uint32_t *in_len, uint8_t *out,
+                              const uint64_t *out_off, const uint32_t *out_cap,
+                              size_t nblocks, int32_t *kinds, uint64_t *written,
+                              int nthreads);
+
+/* ---------------- INT4 (crates/haagenti/src/testing/quantization.rs) ------ */
+
+uint16_t hho_f32_to_f16_bits(float v);          /* :136-163 (truncating) */
+float hho_f16_bits_to_f32(uint16_t h);          /* :166-197 */
+/* Same over an array, returning raw f32 bit patterns (keeps NaN payloads). */
+void hho_f16_bits_to_f32_bits(const uint16_t *h, size_t n, uint32_t *out);
+size_t hho_int4_compressed_size(size_t n);      /* :202-210 */
+/* :30-70; returns bytes written (== hho_int4_compressed_size(n)). */
+size_t hho_quantize_int4(const float *w, size_t n, uint8_t *out);
+/* :82-131; returns the number of elements produced (may be < n). */
+size_t hho_dequantize_int4(const uint8_t *data, size_t data_len, size_t n,
+                           float *out);
+/* Same arithmetic over [begin, end) 32-element groups, threaded. */
+size_t hho_dequantize_int4_mt(const uint8_t *data, size_t data_len, size_t n,
+                              float *out, int nthreads);
+
+/* ---------------- DCT (crates/haagenti-core/src/dct.rs) ------------------- */
+
+void hho_dct_1d(const float *in, float *out, size_t n);        /* :79-129 */
+void hho_dct_1d_direct(const float *in, float *out, size_t n); /* :133-146 */
+void hho_idct_1d(const float *in, float *out, size_t n);       /* :154-259 */
+void hho_idct_1d_direct(const float *in, float *out, size_t n);/* :263-277 */
+void hho_dct_2d(const float *in, float *out, size_t width, size_t height);  /* :282-308 */
+void hho_idct_2d(const float *in, float *out, size_t width, size_t height); /* :311-337 */
+void hho_dct_1d_f64(const double *in, double *out, size_t n);  /* :342-361 */
+void hho_idct_1d_f64(const double *in, double *out, size_t n); /* :364-383 */
+void hho_dct_2d_f64(const double *in, double *out, size_t w, size_t h);  /* :386-412 */
+void hho_idct_2d_f64(const double *in, double *out, size_t w, size_t h); /* :415-441 */
+/* crates/haagenti/src/hct_test_vectors.rs:43-75 and :78-107 */
+void hho_reference_dct_2d(const float *in, float *out, size_t rows, size_t cols);
+void hho_reference_idct_2d(const float *in, float *out, size_t rows, size_t cols);
+
+/* ---------------- Spectral retention (crates/haagenti/src/compressive.rs) - */
+
+/* k = max(1, (n as f32 * clamp(rho, .05, 1)) as usize)   (:97, :152) */
+size_t hho_retain_count(size_t n, float rho);
+/* Top-k by |c| (stable descending sort, :144-149), LSB-first bitmap of the
+ * kept raster indices (:157-163); ascending kept indices into idx (:167-172).
+ * NaN magnitudes sort last (the reference's order with NaN depends on its
+ * sort algorithm; the decode path never sees it). */
+void hho_topk_bitmap(const float *c, size_t n, size_t k, uint8_t *bitmap,
+                     uint32_t *idx);
+/* Bitmap -> ascending index map (:620-627). Returns the number of set bits. */
+size_t hho_bitmap_index_map(const uint8_t *bitmap, size_t n, uint32_t *idx);
+
+/* ---------------- HCT-T tile format (64x64 tiles, INT4 coefficients) ------ */
+/* Tile bytes: [bitmap 512][ceil(k/32) f16 scales][ceil(k/2) nibble bytes]   */
+
+size_t hho_hctt_tile_bytes(size_t k);
+/* Encode one 64x64 tile: dct_2d -> top-k -> bitmap -> quantize_int4. */
+void hho_hctt_encode_tile(const float *tile, size_t k, uint8_t *out);
+/* Decode one tile: dequantize_int4 -> bitmap scatter -> idct_2d (f32).
+ * Returns HHO_OK or HHO_CORRUPTED_DATA (bitmap popcount != k). */
+int hho_hctt_decode_tile(const uint8_t *tile_bytes, size_t k, float *out64x64);
+/* Same but the IDCT in f64 (truth), output f64. */
+int hho_hctt_decode_tile_f64(const uint8_t *tile_bytes, size_t k, double *out);
+/* Whole row-major rows x cols tensor (multiples of 64), tiles in row-major
+ * tile order; threaded.  Output row-major f32. */
+void hho_hctt_encode_tensor(const float *w, size_t rows, size_t cols, size_t k,
+                            uint8_t *out, int nthreads);
+int hho_hctt_decode_tensor(const uint8_t *tiles, size_t rows, size_t cols,
+                           size_t k, float *out, int nthreads);
+
+/* ---------------- HCT container (crates/haagenti-hct/src/tensor.rs) ------ */
+
+/* Size of the v1 file HctWriter::finish writes for the given blocks. */
+size_t hho_hct_file_size(size_t nblocks, size_t total_compressed);
+/* HctWriter::compress_data + finish (:556-616) with the LZ4 compressor:
+ * chunks data by block_size, compresses each chunk, writes header + index +
+ * data into out (capacity out_cap).  Returns bytes written or 0 on error. */
+size_t hho_hct_write_lz4(const uint8_t *data, size_t len, uint32_t block_size,
+                         uint8_t dtype, const uint64_t *shape, int rank,
+                         uint8_t *out, size_t out_cap);
+/* HctReader::new + decompress_all (:417-515).  Writes the concatenated
+ * output into out (capacity out_cap) and *written. */
+int hho_hct_read_all_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
+                         size_t out_cap, size_t *written, hho_err *err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
