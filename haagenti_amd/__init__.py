@@ -1,0 +1,313 @@
+"""haagenti_amd -- MI355X (gfx950) HCT decode path behind a C ABI.
+
+Python mirror of the reference's decode interfaces, calling
+libhaagenti_hip.so through ctypes:
+
+  Lz4Decompressor   haagenti_core::Decompressor for raw LZ4 blocks
+                    (crates/haagenti-core/src/traits.rs:56-91,
+                    crates/haagenti-lz4/src/decompress.rs:28-68), decoded on GPU
+  Lz4Compressor     Compressor side (crates/haagenti-lz4/src/compress.rs:59-99)
+  HipContext        GpuContext / GpuDecompressor (crates/haagenti-cuda/src/lib.rs:89-230)
+  HaagentiError     haagenti_core::Error (crates/haagenti-core/src/error.rs:10-135)
+
+Device entry points take torch tensors (or raw device addresses) for
+device memory; torch is only the allocator and stream provider.  There is
+no CPU fallback: importing without the built library raises.
+"""
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhaagenti_hip.so")
+
+OK = 0
+CORRUPTED_DATA = 1
+BUFFER_TOO_SMALL = 2
+UNEXPECTED_EOF = 3
+CHECKSUM_MISMATCH = 4
+UNSUPPORTED = 5
+ALGORITHM = 6
+INVALID_ARGUMENT = 7
+OUT_OF_MEMORY = 8
+DEVICE = 9
+KERNEL_LAUNCH = 10
+DEVICE_NOT_FOUND = 11
+
+CORRUPT_ZERO_OFFSET = 1
+CORRUPT_OFFSET_BEYOND = 2
+CORRUPT_BITMAP_COUNT = 3
+
+F32, F16, BF16 = 0, 1, 2
+
+
+class BlockStatus(C.Structure):
+    _fields_ = [("code", C.c_int32), ("detail", C.c_int32), ("position", C.c_uint64),
+                ("required", C.c_uint64), ("written", C.c_uint64)]
+
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python haagenti_amd/build.py` "
+        "(the HIP extension is required, there is no CPU fallback)")
+
+_lib = C.CDLL(LIB_PATH)
+_vp, _sz, _i32, _u32 = C.c_void_p, C.c_size_t, C.c_int32, C.c_uint32
+
+
+def _sig(name, res, args):
+    f = getattr(_lib, name)
+    f.restype = res
+    f.argtypes = args
+    return f
+
+
+_sig("hh_status_category", C.c_char_p, [_i32])
+_sig("hh_status_is_recoverable", _i32, [_i32])
+_sig("hh_version", C.c_char_p, [])
+_sig("hh_device_count", _i32, [])
+_sig("hh_context_create", _i32, [_i32, C.POINTER(_vp)])
+_sig("hh_context_destroy", None, [_vp])
+_sig("hh_context_stream", _vp, [_vp])
+_sig("hh_context_synchronize", _i32, [_vp])
+_sig("hh_lz4_decompress_batch", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp])
+_sig("hh_lz4_decompress_to", _i32, [_vp, _vp, _sz, _vp, _sz, C.POINTER(_sz), C.POINTER(BlockStatus)])
+_sig("hh_lz4_compress_block", _i32, [_vp, _sz, _vp, _sz, C.POINTER(_sz)])
+_sig("hh_lz4_max_compressed_size", _sz, [_sz])
+_sig("hh_dequant_int4", _i32, [_vp, _vp, _sz, _sz, _i32, _vp, C.POINTER(_sz), _vp])
+_sig("hh_quantize_int4", _sz, [_vp, _sz, _vp])
+_sig("hh_int4_compressed_size", _sz, [_sz])
+_sig("hh_hctt_tile_bytes", _sz, [_u32])
+_sig("hh_hctt_retain_count", _u32, [C.c_float])
+_sig("hh_hctt_decode", _i32, [_vp, _vp, _sz, _u32, _u32, _u32, _i32, _vp, _vp, _vp])
+_sig("hh_hctt_encode", _i32, [_vp, _u32, _u32, _u32, _vp, _i32])
+
+
+class HcttTensor(C.Structure):
+    """hh_hctt_tensor: one tensor of a batched tile decode."""
+    _fields_ = [("d_tiles", _vp), ("tiles_len", _sz), ("rows", _u32), ("cols", _u32),
+                ("k", _u32), ("d_out", _vp), ("d_tile_status", _vp)]
+
+
+_sig("hh_hctt_decode_batch", _i32, [_vp, C.POINTER(HcttTensor), _u32, _i32, _vp])
+
+# Every symbol include/haagenti_hip.h declares (checked by the tests).
+EXPORTS = [
+    "hh_status_category", "hh_status_is_recoverable", "hh_version", "hh_device_count",
+    "hh_context_create", "hh_context_destroy", "hh_context_stream", "hh_context_synchronize",
+    "hh_lz4_decompress_batch", "hh_lz4_decompress_to", "hh_lz4_compress_block",
+    "hh_lz4_max_compressed_size", "hh_dequant_int4", "hh_quantize_int4",
+    "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
+    "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_encode",
+]
+
+
+def lib():
+    return _lib
+
+
+class HaagentiError(Exception):
+    """haagenti_core::Error mirror: .code, .category, plus the record fields."""
+
+    def __init__(self, code, message="", status=None):
+        self.code = int(code)
+        self.category = category(code)
+        self.status = status
+        super().__init__(f"{self.category}: {message}" if message else self.category)
+
+    def is_recoverable(self):
+        return bool(_lib.hh_status_is_recoverable(self.code))
+
+
+def category(code):
+    return _lib.hh_status_category(int(code)).decode()
+
+
+def version():
+    return _lib.hh_version().decode()
+
+
+def device_count():
+    return int(_lib.hh_device_count())
+
+
+def _check(code, what=""):
+    if code != OK:
+        raise HaagentiError(code, what)
+
+
+def _addr(x):
+    """Device address of a torch tensor, or an int address."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _host_buf(data):
+    b = bytes(data)
+    return b, C.cast(C.c_char_p(b), _vp) if b else None
+
+
+class HipContext:
+    """One device context (device id, stream, IDCT basis table).  Not
+    thread-safe; use one per host thread, like GpuDctContext."""
+
+    def __init__(self, device=0):
+        p = _vp()
+        _check(_lib.hh_context_create(int(device), C.byref(p)), "hh_context_create")
+        self._p = p
+        self.device = device
+
+    @property
+    def handle(self):
+        return self._p
+
+    @property
+    def stream(self):
+        return _lib.hh_context_stream(self._p)
+
+    def synchronize(self):
+        _check(_lib.hh_context_synchronize(self._p))
+
+    def close(self):
+        if getattr(self, "_p", None):
+            _lib.hh_context_destroy(self._p)
+            self._p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---------------------------------------------------------- device API
+    def lz4_decompress_batch(self, d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
+                             d_out_cap, nblocks, d_status, stream=None):
+        """Raw device-pointer batch decode (hh_lz4_decompress_batch)."""
+        return _lib.hh_lz4_decompress_batch(
+            self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), _addr(d_out),
+            _addr(d_out_off), _addr(d_out_cap), int(nblocks), _addr(d_status), stream)
+
+    def dequant_int4(self, d_q, q_len, n, d_out, dtype=F32, stream=None):
+        produced = _sz(0)
+        _check(_lib.hh_dequant_int4(self._p, _addr(d_q), int(q_len), int(n), int(dtype),
+                                    _addr(d_out), C.byref(produced), stream), "hh_dequant_int4")
+        return produced.value
+
+    def hctt_decode(self, d_tiles, tiles_len, rows, cols, k, d_out, dtype=F32,
+                    d_tile_status=None, stream=None):
+        _check(_lib.hh_hctt_decode(self._p, _addr(d_tiles), int(tiles_len), int(rows), int(cols),
+                                   int(k), int(dtype), _addr(d_out), _addr(d_tile_status),
+                                   stream), "hh_hctt_decode")
+
+    def hctt_decode_batch(self, tensors, dtype=F32, stream=None):
+        """tensors: list of (d_tiles, tiles_len, rows, cols, k, d_out[, d_status])."""
+        arr = (HcttTensor * len(tensors))()
+        for i, t in enumerate(tensors):
+            st = t[6] if len(t) > 6 else None
+            arr[i] = HcttTensor(_addr(t[0]), int(t[1]), int(t[2]), int(t[3]), int(t[4]),
+                                _addr(t[5]), _addr(st))
+        _check(_lib.hh_hctt_decode_batch(self._p, arr, len(tensors), int(dtype), stream),
+               "hh_hctt_decode_batch")
+
+    # ---------------------------------------------------------- host API
+    def lz4_decompress_to(self, data, out_cap):
+        """Decompressor::decompress_to on host buffers.  Returns
+        (bytes, BlockStatus); raises HaagentiError on failure."""
+        b, pin = _host_buf(data)
+        out = C.create_string_buffer(max(int(out_cap), 1))
+        written = _sz(0)
+        st = BlockStatus()
+        rc = _lib.hh_lz4_decompress_to(self._p, pin, len(b), out, int(out_cap), C.byref(written),
+                                       C.byref(st))
+        if rc != OK:
+            raise HaagentiError(rc, "lz4 decompress", st)
+        return out.raw[:written.value], st
+
+
+class Lz4Decompressor:
+    """haagenti_core::Decompressor for raw LZ4 blocks, decoded on the GPU.
+
+    Methods mirror crates/haagenti-lz4/src/decompress.rs:28-68."""
+
+    def __init__(self, ctx=None):
+        self.ctx = ctx if ctx is not None else HipContext(0)
+
+    def algorithm(self):
+        return "lz4"
+
+    def decompress_to(self, data, out_cap):
+        out, st = self.ctx.lz4_decompress_to(data, out_cap)
+        return out
+
+    def decompress_with_size(self, data, output_size):
+        return self.decompress_to(data, output_size)
+
+    def decompress(self, data):
+        """Size unknown: start at 4x the input and grow on BufferTooSmall up
+        to 256 MiB (decompress.rs:33-57)."""
+        size = len(data) * 4
+        while True:
+            try:
+                return self.decompress_to(data, size)
+            except HaagentiError as e:
+                if e.code != BUFFER_TOO_SMALL:
+                    raise
+                size = max(int(e.status.required), size * 2)
+                if size > 256 * 1024 * 1024:
+                    raise HaagentiError(CORRUPTED_DATA, "decompressed size exceeds limit")
+
+
+class Lz4Compressor:
+    """Compressor side (host): byte-identical to block::compress_block."""
+
+    def algorithm(self):
+        return "lz4"
+
+    def max_compressed_size(self, n):
+        return int(_lib.hh_lz4_max_compressed_size(int(n)))
+
+    def compress(self, data):
+        b, pin = _host_buf(data)
+        cap = self.max_compressed_size(len(b))
+        out = C.create_string_buffer(cap)
+        w = _sz(0)
+        _check(_lib.hh_lz4_compress_block(pin, len(b), out, cap, C.byref(w)), "lz4 compress")
+        return out.raw[:w.value]
+
+
+def lz4_max_compressed_size(n):
+    return int(_lib.hh_lz4_max_compressed_size(int(n)))
+
+
+def int4_compressed_size(n):
+    return int(_lib.hh_int4_compressed_size(int(n)))
+
+
+def hctt_tile_bytes(k):
+    return int(_lib.hh_hctt_tile_bytes(int(k)))
+
+
+def hctt_retain_count(rho):
+    return int(_lib.hh_hctt_retain_count(float(rho)))
+
+
+def quantize_int4(w):
+    """testing::quantize_int4 on the host; w is a float32 numpy array."""
+    import numpy as np
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros(max(int4_compressed_size(w.size), 1), dtype=np.uint8)
+    n = _lib.hh_quantize_int4(w.ctypes.data, w.size, out.ctypes.data)
+    return out[:n]
+
+
+def hctt_encode(w, k, threads=0):
+    """HCT-T tiles for a float32 (rows, cols) numpy array (host producer)."""
+    import numpy as np
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    out = np.zeros((rows // 64) * (cols // 64) * hctt_tile_bytes(k), dtype=np.uint8)
+    _check(_lib.hh_hctt_encode(w.ctypes.data, rows, cols, int(k), out.ctypes.data, int(threads)),
+           "hh_hctt_encode")
+    return out

@@ -1,0 +1,282 @@
+// C-ABI entry points: contexts, argument validation, kernel launches.
+// Declarations and the reference interface each one replaces are in
+// include/haagenti_hip.h.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "hh_internal.hpp"
+
+namespace {
+
+hipStream_t pick_stream(hh_context *ctx, void *stream) {
+    return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+int32_t from_hip(hipError_t e) {
+    switch (e) {
+        case hipSuccess: return HH_OK;
+        case hipErrorOutOfMemory: return HH_ERR_OUT_OF_MEMORY;
+        case hipErrorInvalidDevice:
+        case hipErrorNoDevice: return HH_ERR_DEVICE_NOT_FOUND;
+        case hipErrorInvalidValue: return HH_ERR_INVALID_ARGUMENT;
+        case hipErrorLaunchFailure:
+        case hipErrorInvalidDeviceFunction:
+        case hipErrorInvalidConfiguration: return HH_ERR_KERNEL_LAUNCH;
+        default: return HH_ERR_DEVICE;
+    }
+}
+
+int32_t ensure_scratch(hh_context *ctx, size_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return HH_OK;
+    if (ctx->d_scratch) {
+        hipError_t e = hipFree(ctx->d_scratch);
+        ctx->d_scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        if (e != hipSuccess) return from_hip(e);
+    }
+    size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+    hipError_t e = hipMalloc(&ctx->d_scratch, sz);
+    if (e != hipSuccess) {
+        ctx->d_scratch = nullptr;
+        return from_hip(e);
+    }
+    ctx->scratch_bytes = sz;
+    return HH_OK;
+}
+
+}  // namespace
+
+namespace hh {
+
+// MFMA fragments of M' = 256 * M, M[v][j] = a_v cos(pi v (2j+1) / 128),
+// split into f16 hi + lo.  Entry ((hl*2 + jb)*4 + s)*64 + lane holds the 8
+// values M'[pi(16s + 8h + e)][32 jb + lane%32] for e = 0..7, h = lane/32,
+// pi(16s + 8h + e) = 16s + 8(e/4) + 4h + e%4 (the accumulator row order of
+// v_mfma_f32_32x32x16_f16).
+size_t basis_table_bytes() { return 2 * 2 * 4 * 64 * 8 * sizeof(_Float16); }
+
+void build_basis_table(void *buf) {
+    _Float16 *t = reinterpret_cast<_Float16 *>(buf);
+    const double pi = 3.14159265358979323846;
+    for (int hl = 0; hl < 2; hl++)
+        for (int jb = 0; jb < 2; jb++)
+            for (int s = 0; s < 4; s++)
+                for (int lane = 0; lane < 64; lane++)
+                    for (int e = 0; e < 8; e++) {
+                        const int h = lane >> 5;
+                        const int v = 16 * s + 8 * (e >> 2) + 4 * h + (e & 3);
+                        const int j = 32 * jb + (lane & 31);
+                        const double a = v == 0 ? std::sqrt(1.0 / 64) : std::sqrt(2.0 / 64);
+                        const double m = 256.0 * a * std::cos(pi * v * (2 * j + 1) / 128.0);
+                        const _Float16 hi = (_Float16)m;
+                        const _Float16 lo = (_Float16)(m - (double)hi);
+                        t[((((hl * 2 + jb) * 4 + s) * 64 + lane) * 8) + e] = hl == 0 ? hi : lo;
+                    }
+}
+
+}  // namespace hh
+
+extern "C" {
+
+const char *hh_status_category(int32_t code) {
+    switch (code) {
+        case HH_OK: return "ok";
+        case HH_ERR_CORRUPTED_DATA: return "corrupted_data";
+        case HH_ERR_BUFFER_TOO_SMALL: return "buffer_too_small";
+        case HH_ERR_UNEXPECTED_EOF: return "unexpected_eof";
+        case HH_ERR_CHECKSUM_MISMATCH: return "checksum_mismatch";
+        case HH_ERR_UNSUPPORTED: return "unsupported";
+        case HH_ERR_ALGORITHM: return "algorithm_error";
+        case HH_ERR_INVALID_ARGUMENT: return "invalid_argument";
+        case HH_ERR_OUT_OF_MEMORY: return "allocation_failed";
+        case HH_ERR_DEVICE: return "device_error";
+        case HH_ERR_KERNEL_LAUNCH: return "kernel_launch";
+        case HH_ERR_DEVICE_NOT_FOUND: return "device_not_found";
+        default: return "unknown";
+    }
+}
+
+int32_t hh_status_is_recoverable(int32_t code) {
+    return code == HH_ERR_UNEXPECTED_EOF || code == HH_ERR_BUFFER_TOO_SMALL;
+}
+
+const char *hh_version(void) { return "haagenti-hip 0.1.0 (gfx950)"; }
+
+int32_t hh_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int32_t hh_context_create(int32_t device, hh_context **out) {
+    if (!out) return HH_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return HH_ERR_DEVICE_NOT_FOUND;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return from_hip(e);
+    hh_context *ctx = new hh_context();
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        delete ctx;
+        return from_hip(e);
+    }
+    ctx->num_cus = prop.multiProcessorCount;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return from_hip(e);
+    }
+    std::vector<unsigned char> table(hh::basis_table_bytes());
+    hh::build_basis_table(table.data());
+    e = hipMalloc(&ctx->d_basis, table.size());
+    if (e == hipSuccess) e = hipMemcpy(ctx->d_basis, table.data(), table.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hh_context_destroy(ctx);
+        return from_hip(e);
+    }
+    *out = ctx;
+    return HH_OK;
+}
+
+void hh_context_destroy(hh_context *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    if (ctx->d_basis) hipFree(ctx->d_basis);
+    if (ctx->d_scratch) hipFree(ctx->d_scratch);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+void *hh_context_stream(hh_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int32_t hh_context_synchronize(hh_context *ctx) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    return from_hip(hipStreamSynchronize(ctx->stream));
+}
+
+// ---------------------------------------------------------------- LZ4
+
+int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                const uint64_t *d_in_off, const uint32_t *d_in_len, uint8_t *d_out,
+                                const uint64_t *d_out_off, const uint32_t *d_out_cap,
+                                uint32_t nblocks, hh_block_status *d_status, void *stream) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    if (nblocks == 0) return HH_OK;
+    if (!d_in || !d_in_off || !d_in_len || !d_out || !d_out_off || !d_out_cap || !d_status)
+        return HH_ERR_INVALID_ARGUMENT;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(hh::launch_lz4_batch(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
+                                         d_out_cap, nblocks, d_status, pick_stream(ctx, stream)));
+}
+
+int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, uint8_t *out,
+                             size_t out_cap, size_t *written, hh_block_status *status) {
+    if (!ctx || (!in && in_len) || (!out && out_cap)) return HH_ERR_INVALID_ARGUMENT;
+    if (in_len > 0xffffffffu || out_cap > 0xffffffffu) return HH_ERR_UNSUPPORTED;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return from_hip(e);
+    // scratch layout: [status 32][in_off 8][in_len 4 pad 4][out_off 8][out_cap 4 pad 4][in][out]
+    const size_t hdr = 64;
+    const size_t in_at = hdr, out_at = (hdr + in_len + 255) & ~(size_t)255;
+    int32_t rc = ensure_scratch(ctx, out_at + out_cap + 16);
+    if (rc != HH_OK) return rc;
+    uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+    struct {
+        uint64_t in_off;
+        uint32_t in_len, pad0;
+        uint64_t out_off;
+        uint32_t out_cap, pad1;
+    } meta = {0, (uint32_t)in_len, 0, 0, (uint32_t)out_cap, 0};
+    hipStream_t s = ctx->stream;
+    e = hipMemcpyAsync(base + 32, &meta, sizeof(meta), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && in_len)
+        e = hipMemcpyAsync(base + in_at, in, in_len, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return from_hip(e);
+    e = hh::launch_lz4_batch(base + in_at, in_len, reinterpret_cast<uint64_t *>(base + 32),
+                             reinterpret_cast<uint32_t *>(base + 40), base + out_at,
+                             reinterpret_cast<uint64_t *>(base + 48),
+                             reinterpret_cast<uint32_t *>(base + 56), 1,
+                             reinterpret_cast<hh_block_status *>(base), s);
+    if (e != hipSuccess) return from_hip(e);
+    hh_block_status st;
+    e = hipMemcpyAsync(&st, base, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return from_hip(e);
+    if (st.code == HH_OK && st.written) {
+        e = hipMemcpy(out, base + out_at, st.written, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return from_hip(e);
+    }
+    if (written) *written = st.code == HH_OK ? st.written : 0;
+    if (status) *status = st;
+    return st.code;
+}
+
+// ---------------------------------------------------------------- INT4
+
+int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_t n,
+                        int32_t out_dtype, void *d_out, size_t *produced, void *stream) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    if (out_dtype != HH_F32 && out_dtype != HH_F16 && out_dtype != HH_BF16)
+        return HH_ERR_UNSUPPORTED;
+    const size_t groups = (n + 31) / 32;
+    size_t m = 0;
+    if (n > 0 && q_len >= 2 * groups) {
+        const size_t packed = q_len - 2 * groups;
+        m = n < 2 * packed ? n : 2 * packed;
+    }
+    if (produced) *produced = m;
+    if (m == 0) return HH_OK;
+    if (!d_q || !d_out || ((uintptr_t)d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(hh::launch_dequant_int4(d_q, m, groups, out_dtype, d_out, ctx->num_cus,
+                                            pick_stream(ctx, stream)));
+}
+
+// ---------------------------------------------------------------- HCT-T
+
+static int32_t check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
+    if (T.rows % 64 || T.cols % 64 || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
+    const size_t nt = (size_t)(T.rows / 64) * (T.cols / 64);
+    *ntiles = nt;
+    if (nt == 0) return HH_OK;
+    if (T.tiles_len < nt * hh_hctt_tile_bytes(T.k)) return HH_ERR_UNEXPECTED_EOF;
+    if (!T.d_tiles || !T.d_out || ((uintptr_t)T.d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
+    return HH_OK;
+}
+
+int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uint32_t n,
+                             int32_t out_dtype, void *stream) {
+    if (!ctx || (!tensors && n)) return HH_ERR_INVALID_ARGUMENT;
+    if (out_dtype != HH_F32 && out_dtype != HH_F16 && out_dtype != HH_BF16)
+        return HH_ERR_UNSUPPORTED;
+    size_t total = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        size_t nt = 0;
+        int32_t rc = check_hctt_tensor(tensors[i], &nt);
+        if (rc != HH_OK) return rc;
+        total += nt;
+    }
+    if (total == 0) return HH_OK;
+    if (total > 0xffffffffu) return HH_ERR_UNSUPPORTED;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(hh::launch_hctt_decode(tensors, n, out_dtype, ctx->d_basis, ctx->num_cus,
+                                           pick_stream(ctx, stream)));
+}
+
+int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len, uint32_t rows,
+                       uint32_t cols, uint32_t k, int32_t out_dtype, void *d_out,
+                       int32_t *d_tile_status, void *stream) {
+    hh_hctt_tensor T = {d_tiles, tiles_len, rows, cols, k, d_out, d_tile_status};
+    return hh_hctt_decode_batch(ctx, &T, 1, out_dtype, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// Internal declarations shared by the HIP kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/haagenti_hip.h"
+
+struct hh_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int num_cus = 0;
+    // 64x64 inverse-DCT basis, pre-split into f16 hi/lo MFMA fragments in
+    // per-lane order (see hctt_decode.hip), uploaded once per context.
+    void *d_basis = nullptr;
+    // Small device scratch used by the host-pointer entry points.
+    void *d_scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+namespace hh {
+
+// ---- device helpers -------------------------------------------------------
+
+// f16 bit pattern -> f32, exact for every code, NaN payload kept
+// (crates/haagenti/src/testing/quantization.rs:166-197).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t frac = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0x1fu) {
+        bits = sign | 0x7f800000u | (frac << 13);
+    } else if (exp != 0) {
+        bits = sign | ((exp + 112u) << 23) | (frac << 13);
+    } else if (frac == 0) {
+        bits = sign;
+    } else {
+        // subnormal: value = frac * 2^-24, normalise with a leading-zero count
+        uint32_t lz = __clz(frac) - 21;          // shifts to bring bit 10 up
+        uint32_t f = (frac << lz) & 0x3ffu;
+        bits = sign | ((113u - lz) << 23) | (f << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// f32 -> bf16 round-to-nearest-even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// f32 -> f16 round-to-nearest-even (hardware conversion, default round mode).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// ---- launchers (return hipSuccess or the launch error) ---------------------
+
+hipError_t launch_dequant_int4(const uint8_t *d_q, size_t n, size_t nscale_groups,
+                               int dtype, void *d_out, int num_cus, hipStream_t s);
+
+hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
+                            const uint32_t *d_in_len, uint8_t *d_out,
+                            const uint64_t *d_out_off, const uint32_t *d_out_cap,
+                            uint32_t nblocks, hh_block_status *d_status, hipStream_t s);
+
+// Build the MFMA basis fragments on the host (host_basis.cpp).
+size_t basis_table_bytes();
+void build_basis_table(void *host_buf);
+
+// Decodes n tensors (validated by the caller) in ceil(n/8) launches.
+hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dtype,
+                              const void *d_basis, int num_cus, hipStream_t s);
+
+}  // namespace hh

@@ -1,0 +1,191 @@
+/*
+ * haagenti_hip.h -- C ABI of the MI355X (gfx950) HCT decode path.
+ *
+ * This is the boundary a `haagenti-hip` crate binds in place of
+ * `haagenti-cuda`.  Every entry point names the reference interface it
+ * replaces (file:line in the reference repository).  Signatures carry plain
+ * pointers and sizes only: device pointers are prefixed d_, host pointers h_
+ * (or unprefixed in host-only calls), streams are hipStream_t passed as
+ * void* (NULL = the context's own stream).
+ *
+ * Ownership: the caller allocates every input and output buffer.  A context
+ * owns its device id, a stream, the IDCT basis table and a small scratch
+ * pool; it is not thread-safe (one context per host thread), matching
+ * GpuDctContext / GpuContext (crates/haagenti-cuda/src/lib.rs:99-108).
+ * Device entry points are asynchronous on the given stream; results are
+ * valid after that stream is synchronised.  Host-pointer entry points are
+ * synchronous.
+ *
+ * Errors: every entry returns an hh_status.  Kernels additionally write
+ * per-block / per-tile status records (first error wins inside a block).
+ */
+#ifndef HAAGENTI_HIP_H
+#define HAAGENTI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1-6 mirror haagenti_core::Error
+ * (crates/haagenti-core/src/error.rs:10-60); 7-11 mirror CudaError
+ * (crates/haagenti-cuda/src/error.rs:10-62). */
+typedef enum hh_status {
+    HH_OK = 0,
+    HH_ERR_CORRUPTED_DATA = 1,    /* Error::CorruptedData */
+    HH_ERR_BUFFER_TOO_SMALL = 2,  /* Error::BufferTooSmall {required, provided} */
+    HH_ERR_UNEXPECTED_EOF = 3,    /* Error::UnexpectedEof {bytes_read} */
+    HH_ERR_CHECKSUM_MISMATCH = 4, /* Error::ChecksumMismatch */
+    HH_ERR_UNSUPPORTED = 5,       /* Error::Unsupported / CudaError::UnsupportedAlgorithm */
+    HH_ERR_ALGORITHM = 6,         /* Error::Algorithm ("hct" container I/O) */
+    HH_ERR_INVALID_ARGUMENT = 7,  /* CudaError::InvalidData / SizeMismatch */
+    HH_ERR_OUT_OF_MEMORY = 8,     /* CudaError::OutOfMemory, Error::AllocationFailed */
+    HH_ERR_DEVICE = 9,            /* CudaError::Driver / StreamSync */
+    HH_ERR_KERNEL_LAUNCH = 10,    /* CudaError::KernelLaunch / KernelLoad */
+    HH_ERR_DEVICE_NOT_FOUND = 11  /* CudaError::DeviceNotFound */
+} hh_status;
+
+/* Sub-kinds of HH_ERR_CORRUPTED_DATA (the reference's message strings). */
+typedef enum hh_corrupt_kind {
+    HH_CORRUPT_NONE = 0,
+    HH_CORRUPT_ZERO_OFFSET = 1,    /* "invalid zero offset" (haagenti-lz4/src/block.rs:320-322) */
+    HH_CORRUPT_OFFSET_BEYOND = 2,  /* "offset beyond output at offset N" (block.rs:323-325) */
+    HH_CORRUPT_BITMAP_COUNT = 3,   /* "bitmap has N set bits, expected K" (compressive.rs:630-636) */
+    HH_CORRUPT_HEADER = 4,         /* invalid magic/version/algorithm/dtype (tensor.rs:311-331) */
+    HH_CORRUPT_SIZE = 5            /* sizes inconsistent with the header/shape */
+} hh_corrupt_kind;
+
+/* Output element types; values match haagenti_hct::DType (tensor.rs:99-105). */
+typedef enum hh_dtype { HH_F32 = 0, HH_F16 = 1, HH_BF16 = 2 } hh_dtype;
+
+/* Per-block status written by device kernels (32 bytes). */
+typedef struct hh_block_status {
+    int32_t code;      /* hh_status */
+    int32_t detail;    /* hh_corrupt_kind when code == HH_ERR_CORRUPTED_DATA */
+    uint64_t position; /* UnexpectedEof: bytes_read; OffsetBeyond: output position */
+    uint64_t required; /* BufferTooSmall: required output bytes */
+    uint64_t written;  /* bytes produced (valid when code == HH_OK) */
+} hh_block_status;
+
+typedef struct hh_context hh_context;
+
+/* ---------------------------------------------------------------- misc */
+
+/* Error::category() strings (crates/haagenti-core/src/error.rs:120-134). */
+const char *hh_status_category(int32_t code);
+/* Error::is_recoverable() (error.rs:112-117): UnexpectedEof, BufferTooSmall. */
+int32_t hh_status_is_recoverable(int32_t code);
+const char *hh_version(void);
+/* Number of visible devices (haagenti_cuda::is_available, lib.rs:233). */
+int32_t hh_device_count(void);
+
+/* GpuContext::new / GpuDecompressor::new(device_id)
+ * (crates/haagenti-cuda/src/lib.rs:112-142, decompress.rs:117-127). */
+int32_t hh_context_create(int32_t device, hh_context **out);
+void hh_context_destroy(hh_context *ctx);
+/* The context's stream (hipStream_t) as void*. */
+void *hh_context_stream(hh_context *ctx);
+int32_t hh_context_synchronize(hh_context *ctx);
+
+/* ---------------------------------------------------------------- LZ4 */
+
+/* Batched raw-LZ4 block decode, one wavefront per block.  Block i reads
+ * d_in[d_in_off[i] .. +d_in_len[i]) and writes at most d_out_cap[i] bytes
+ * at d_out + d_out_off[i]; d_out_cap[i] is both output.len() and
+ * output_size of decompress_block (haagenti-lz4/src/block.rs:261-366).
+ * in_total bounds every input read (size of the d_in allocation).
+ * d_status[i] receives the block's result; a stream that ends early is
+ * success with written < cap, as in the reference.
+ * Replaces NativeKernels::decompress_lz4_native
+ * (crates/haagenti-cuda/src/native_kernels.rs:623-657) and
+ * GpuContext::decompress_lz4 (lib.rs:173-197). */
+int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                const uint64_t *d_in_off, const uint32_t *d_in_len,
+                                uint8_t *d_out, const uint64_t *d_out_off,
+                                const uint32_t *d_out_cap, uint32_t nblocks,
+                                hh_block_status *d_status, void *stream);
+
+/* Host-pointer, single block: Decompressor::decompress_to
+ * (haagenti-core/src/traits.rs:80; haagenti-lz4/src/decompress.rs:59-61),
+ * decoded on the GPU.  Synchronous.  *status receives the full record. */
+int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len,
+                             uint8_t *out, size_t out_cap, size_t *written,
+                             hh_block_status *status);
+
+/* Compressor::compress_to with the LZ4 block compressor
+ * (haagenti-lz4/src/block.rs:73-147; compress.rs:81-99), on the host.
+ * Byte-identical output.  *written receives the compressed size;
+ * HH_ERR_BUFFER_TOO_SMALL with *written = required when out_cap is short. */
+int32_t hh_lz4_compress_block(const uint8_t *in, size_t in_len, uint8_t *out,
+                              size_t out_cap, size_t *written);
+/* block.rs:370-373 */
+size_t hh_lz4_max_compressed_size(size_t input_len);
+
+/* ---------------------------------------------------------------- INT4 */
+
+/* testing::dequantize_int4 (crates/haagenti/src/testing/quantization.rs:82-131)
+ * on the GPU: d_q = [ceil(n/32) f16 scales][ceil(n/2) nibble bytes],
+ * q_len bytes.  Writes *produced = min(n, 2*(q_len - scale bytes))
+ * elements (0 when q_len is shorter than the scales), as the reference's
+ * early stop does.  HH_F32 output is bit-identical to the reference;
+ * HH_BF16 / HH_F16 are the round-to-nearest-even of that f32.
+ * Replaces NativeKernels::dequantize_int4_fp16 (native_kernels.rs:694-729),
+ * whose signed-nibble fp16 arithmetic disagrees with the CPU format. */
+int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_t n,
+                        int32_t out_dtype, void *d_out, size_t *produced, void *stream);
+
+/* testing::quantize_int4 (quantization.rs:30-70) on the host (producer
+ * side).  out must hold hh_int4_compressed_size(n) bytes. */
+size_t hh_quantize_int4(const float *w, size_t n, uint8_t *out);
+size_t hh_int4_compressed_size(size_t n); /* quantization.rs:202-210 */
+
+/* ---------------------------------------------------------------- HCT-T tiles */
+
+/* Bytes of one 64x64 HCT-T tile with k retained coefficients:
+ * 512-byte bitmap + ceil(k/32) f16 scales + ceil(k/2) nibble bytes. */
+size_t hh_hctt_tile_bytes(uint32_t k);
+/* Retained count for a retention ratio: max(1, (4096 as f32 * clamp(rho,
+ * 0.05, 1)) as usize) (crates/haagenti/src/compressive.rs:97,152). */
+uint32_t hh_hctt_retain_count(float rho);
+
+/* Decode a rows x cols tensor stored as row-major 64x64 HCT-T tiles:
+ * per tile dequantize_int4 -> bitmap scatter (compressive.rs:620-627,
+ * 741-745) -> 2-D inverse DCT (haagenti-core/src/dct.rs:311-337), on MFMA.
+ * d_tile_status (optional, one int32 per tile) receives HH_OK or
+ * HH_ERR_CORRUPTED_DATA (bitmap popcount != k; that tile is written as
+ * zeros).  Output row-major rows x cols of out_dtype.
+ * Replaces GpuDctContext::idct_2d_gpu (crates/haagenti-cuda/src/dct_gpu.rs:1163)
+ * and GpuDecompressor::decompress_to_gpu (decompress.rs:183-203). */
+int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len,
+                       uint32_t rows, uint32_t cols, uint32_t k, int32_t out_dtype,
+                       void *d_out, int32_t *d_tile_status, void *stream);
+
+/* One tensor of a batched decode (device pointers; the array itself is
+ * host memory and is consumed before the call returns). */
+typedef struct hh_hctt_tensor {
+    const uint8_t *d_tiles;
+    size_t tiles_len;
+    uint32_t rows, cols, k;
+    void *d_out;
+    int32_t *d_tile_status; /* optional */
+} hh_hctt_tensor;
+
+/* Several tensors (e.g. all weights of one decoder layer, each with its own
+ * retention k) in as few launches as possible, same output dtype.  Same
+ * per-tensor semantics as hh_hctt_decode; this is the batched form of
+ * GpuDecompressor::decompress_batch_to_gpu (decompress.rs:282-293). */
+int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uint32_t n,
+                             int32_t out_dtype, void *stream);
+
+/* Producer side on the host (threads = 0: all cores): per tile
+ * dct_2d (dct.rs:282-308) -> top-k by |c| (compressive.rs:144-172) ->
+ * quantize_int4 of the kept coefficients in ascending index order. */
+int32_t hh_hctt_encode(const float *w, uint32_t rows, uint32_t cols, uint32_t k,
+                       uint8_t *out, int32_t threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HAAGENTI_HIP_H */

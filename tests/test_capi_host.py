@@ -1,0 +1,123 @@
+"""C-ABI library: loads, exports every declared symbol, and its host-side
+producer (Compressor side) is byte-identical to the oracle.  No GPU."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import haagenti_amd as H
+import oracle_lib as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "haagenti_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(hh_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_every_declared_symbol_is_exported():
+    declared = _declared()
+    assert len(declared) >= 15
+    lib = C.CDLL(H.LIB_PATH)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(H.EXPORTS) == declared
+
+
+def test_status_categories_mirror_core_error():
+    # crates/haagenti-core/src/error.rs:120-134
+    assert H.category(H.CORRUPTED_DATA) == "corrupted_data"
+    assert H.category(H.BUFFER_TOO_SMALL) == "buffer_too_small"
+    assert H.category(H.UNEXPECTED_EOF) == "unexpected_eof"
+    assert H.category(H.CHECKSUM_MISMATCH) == "checksum_mismatch"
+    assert H.category(H.UNSUPPORTED) == "unsupported"
+    assert H.category(H.ALGORITHM) == "algorithm_error"
+    assert H.HaagentiError(H.UNEXPECTED_EOF).is_recoverable()
+    assert H.HaagentiError(H.BUFFER_TOO_SMALL).is_recoverable()
+    assert not H.HaagentiError(H.CORRUPTED_DATA).is_recoverable()
+    # numeric values shared with the oracle's error kinds
+    assert (H.CORRUPTED_DATA, H.BUFFER_TOO_SMALL, H.UNEXPECTED_EOF, H.ALGORITHM) == \
+           (O.CORRUPTED, O.BUFFER_TOO_SMALL, O.UNEXPECTED_EOF, O.ALGORITHM)
+
+
+def _lz4_inputs():
+    rng = np.random.default_rng(21)
+    yield b""
+    yield b"Hello"
+    yield b"A" * 40
+    yield b"0123456789abcdef0123456vwxyz"
+    yield (b"The quick brown fox jumps over the lazy dog. " * 300)[:10000]
+    for n in [13, 100, 4096, 65536]:
+        yield rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        yield rng.integers(0, 3, n, dtype=np.uint8).tobytes()
+        a = rng.integers(0, 256, n, dtype=np.uint8)
+        a[(np.arange(n) // 256) % 2 == 0] = 0
+        yield a.tobytes()
+    # config-2 style payload: packed INT4 nibbles of Gaussian weights
+    w = rng.normal(0, 0.02, 2 * 65536).astype(np.float32)
+    q = O.quantize_int4(w)
+    yield q[:65536]
+    z = np.frombuffer(q[:65536], np.uint8).copy()
+    z[np.repeat(rng.random(256) < 0.5, 256)] = 0
+    yield z.tobytes()
+
+
+def test_lz4_compressor_byte_identical_to_oracle():
+    comp = H.Lz4Compressor()
+    for src in _lz4_inputs():
+        mine = comp.compress(src)
+        ref, e = O.lz4_compress_block(src)
+        assert mine == ref, len(src)
+        assert comp.max_compressed_size(len(src)) == O.lz4_max_compressed_size(len(src))
+
+
+def test_lz4_compressor_buffer_too_small():
+    out = C.create_string_buffer(4)
+    w = C.c_size_t(0)
+    rc = H.lib().hh_lz4_compress_block(b"Hello", 5, out, 4, C.byref(w))
+    assert rc == H.BUFFER_TOO_SMALL and w.value == 7
+
+
+def test_quantize_byte_identical_to_oracle():
+    rng = np.random.default_rng(22)
+    cases = [rng.normal(0, 0.02, n).astype(np.float32) for n in [1, 31, 32, 33, 97, 1000, 65537]]
+    w = np.zeros(64, np.float32)
+    w[0] = 7.005126953125
+    w[33] = np.nan
+    w[40] = np.inf
+    cases.append(w)
+    cases.append(np.array([(i - 50.0) / 10.0 for i in range(100)], np.float32))
+    for w in cases:
+        assert H.quantize_int4(w).tobytes() == O.quantize_int4(w)
+    assert H.int4_compressed_size(33) == 21
+
+
+def test_retain_count_and_tile_bytes():
+    assert H.hctt_retain_count(0.3) == O.retain_count(4096, 0.3) == 1228
+    assert H.hctt_retain_count(0.25) == 1024
+    assert H.hctt_retain_count(0.01) == O.retain_count(4096, 0.01)
+    assert H.hctt_tile_bytes(1228) == O.hctt_tile_bytes(1228) == 1204
+
+
+def test_hctt_encoder_matches_oracle_encoder():
+    # Same format; the producer's f64 DCT may flip near-ties, so compare the
+    # decoded tensors, the bitmaps' popcount and most of the bytes.
+    rng = np.random.default_rng(23)
+    w = rng.normal(0, 0.02, (128, 192)).astype(np.float32)
+    for k in [1024, 1228]:
+        mine = H.hctt_encode(w, k, threads=2)
+        ref = O.hctt_encode_tensor(w, k, nthreads=2)
+        assert mine.size == ref.size
+        tb = H.hctt_tile_bytes(k)
+        for t in range(mine.size // tb):
+            assert int(np.unpackbits(mine[t * tb:t * tb + 512]).sum()) == k
+        assert (mine == ref).mean() > 0.99
+        rc1, a = O.hctt_decode_tensor(mine, 128, 192, k)
+        rc2, b = O.hctt_decode_tensor(ref, 128, 192, k)
+        assert rc1 == rc2 == O.OK
+        rms = np.sqrt((b ** 2).mean())
+        assert np.abs(a - b).max() < 0.2 * rms  # at most a few near-tie flips

@@ -1,0 +1,193 @@
+"""Batched LZ4 block decode on the GPU vs the oracle
+(crates/haagenti-lz4/src/block.rs:261-366): bit-exact bytes and identical
+error records."""
+import numpy as np
+import pytest
+
+import gpu_util as G
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_batch(streams, caps, in_pad=0, out_pad=0, in_align=0, out_align=0):
+    """Decode independent blocks in one launch.  Returns (outputs, statuses)."""
+    import haagenti_amd as H
+    T = G.torch()
+    in_off, pos = [], in_align
+    for s in streams:
+        in_off.append(pos)
+        pos += len(s) + in_pad
+    comp = np.zeros(max(pos, 1), np.uint8)
+    for o, s in zip(in_off, streams):
+        comp[o:o + len(s)] = np.frombuffer(bytes(s), np.uint8)
+    out_off, opos = [], out_align
+    for c in caps:
+        out_off.append(opos)
+        opos += c + out_pad
+    d_in = G.dev(comp)
+    d_out = T.full((max(opos, 1),), 0xA5, dtype=T.uint8, device="cuda")
+    d_in_off = G.dev(np.array(in_off, np.uint64))
+    d_in_len = G.dev(np.array([len(s) for s in streams], np.uint32))
+    d_out_off = G.dev(np.array(out_off, np.uint64))
+    d_out_cap = G.dev(np.array(caps, np.uint32))
+    d_status = T.zeros(len(streams) * 32, dtype=T.uint8, device="cuda")
+    rc = G.ctx().lz4_decompress_batch(d_in, comp.size, d_in_off, d_in_len, d_out, d_out_off,
+                                      d_out_cap, len(streams), d_status, stream=G.stream())
+    assert rc == H.OK
+    G.sync()
+    st = np.frombuffer(G.host_u8(d_status).tobytes(), dtype=np.dtype(
+        [("code", "<i4"), ("detail", "<i4"), ("position", "<u8"), ("required", "<u8"),
+         ("written", "<u8")]))
+    out = G.host_u8(d_out)
+    outs = [out[o:o + int(s["written"])].tobytes() for o, s in zip(out_off, st)]
+    # bytes beyond `written` inside each block's capacity, and the padding
+    # between blocks, must be untouched (0xA5) -- nothing written out of range
+    for o, c, s in zip(out_off, caps, st):
+        if s["code"] == 0:
+            assert (out[o + int(s["written"]):o + c] == 0xA5).all()
+    if out_pad:
+        for o, c in zip(out_off, caps):
+            assert (out[o + c:o + c + out_pad] == 0xA5).all()
+    return outs, st
+
+
+def check_against_oracle(streams, caps, **kw):
+    outs, st = gpu_batch(streams, caps, **kw)
+    for s, c, o, r in zip(streams, caps, outs, st):
+        ref, e = O.lz4_decompress_block(s, c)
+        assert r["code"] == e.kind, (r, e.kind)
+        if e.kind == O.OK:
+            assert o == ref
+        else:
+            assert r["detail"] == e.sub
+            assert r["position"] == e.position
+            assert r["required"] == e.required
+    return outs, st
+
+
+def test_reference_inputs_roundtrip():
+    srcs = [b"Hello", b"A" * 40, b"Hello, World! Hello, World! Hello, World! This is a test.",
+            (b"The quick brown fox jumps over the lazy dog. " * 300)[:10000],
+            (b"ABCDEFGH" * 200)[:1000], b"", b"x"]
+    streams = [O.lz4_compress_block(s)[0] for s in srcs]
+    outs, st = check_against_oracle(streams, [len(s) for s in srcs])
+    assert outs == srcs
+
+
+def test_hand_written_streams_and_errors():
+    cases = [
+        (bytes([0x14, 0x78, 0x01, 0x00, 0x10, 0x79]), 10),
+        (bytes([0x35]) + b"abc" + bytes([0x03, 0x00, 0x00]), 12),
+        (bytes([0xF0, 0xFF, 0x00]) + bytes(range(256)) + bytes(range(14)), 270),
+        (bytes([0x1F, 0x7A, 0x01, 0x00, 0xFF, 0x01]), 276),
+        (bytes([0x14, 0x78, 0x01, 0x00]), 20),                  # short block: success
+        (bytes([0x10, 0x61, 0x00, 0x00]), 10),                  # zero offset
+        (bytes([0x10, 0x61, 0x02, 0x00]), 10),                  # offset beyond output
+        (bytes([0xF0]), 10),                                    # eof in literal length
+        (bytes([0x30, 0x61]), 10),                              # eof in literals
+        (bytes([0x10, 0x61, 0x01]), 10),                        # eof in offset
+        (bytes([0x1F, 0x61, 0x01, 0x00]), 100),                 # eof in match length
+        (bytes([0x30, 0x61, 0x62, 0x63]), 2),                   # literal overflow
+        (bytes([0x14, 0x78, 0x01, 0x00]), 5),                   # match overflow
+        (bytes([0x30, 0x61, 0x62, 0x63]), 10),                  # eof after literals
+        (b"\x00", 0),
+    ]
+    check_against_oracle([c[0] for c in cases], [c[1] for c in cases], out_pad=7)
+
+
+def _config2_sources(rng, nsrc):
+    """Block contents as in the 64 KiB LZ4 benchmark: packed INT4 nibbles of
+    N(0, 0.02) weights, or the same with half of the 256-byte spans zeroed."""
+    import haagenti_amd as H
+    out = []
+    for i in range(nsrc):
+        w = rng.normal(0, 0.02, 131072).astype(np.float32)
+        q = H.quantize_int4(w)
+        nib = q[2 * 4096:].copy()
+        assert nib.size == 65536
+        if i % 2:
+            nib[np.repeat(rng.random(256) < 0.5, 256)] = 0
+        out.append(nib.tobytes())
+    return out
+
+
+def test_config2_blocks_vs_oracle():
+    import haagenti_amd as H
+    rng = np.random.default_rng(2)
+    srcs = _config2_sources(rng, 16)
+    comp = [H.Lz4Compressor().compress(s) for s in srcs]
+    ratios = [len(s) / len(c) for s, c in zip(srcs, comp)]
+    assert min(ratios[1::2]) > 1.5  # zeroed spans compress
+    outs, st = check_against_oracle(comp, [65536] * len(comp))
+    assert outs == srcs
+
+
+def test_config2_full_256MiB_roundtrip():
+    # 4096 x 64 KiB blocks; every block must come back bit-identical.
+    import haagenti_amd as H
+    rng = np.random.default_rng(3)
+    srcs = _config2_sources(rng, 64)
+    comp = [H.Lz4Compressor().compress(s) for s in srcs]
+    pick = rng.integers(0, 2, 4096) + 2 * rng.integers(0, 32, 4096)   # seeded coin per block
+    streams = [comp[i] for i in pick]
+    outs, st = gpu_batch(streams, [65536] * 4096)
+    assert (st["code"] == 0).all() and (st["written"] == 65536).all()
+    for i, o in zip(pick, outs):
+        assert o == srcs[i]
+
+
+def test_unaligned_offsets_and_padding():
+    rng = np.random.default_rng(4)
+    srcs = []
+    for n in [1, 15, 16, 17, 63, 64, 65, 255, 1000, 4097, 20000]:
+        a = rng.integers(0, 4, n, dtype=np.uint8)
+        a[rng.random(n) < 0.3] = 0
+        srcs.append(a.tobytes())
+    streams = [O.lz4_compress_block(s)[0] for s in srcs]
+    for in_align, out_align, in_pad, out_pad in [(1, 3, 5, 9), (2, 1, 0, 1), (3, 7, 13, 0)]:
+        outs, st = check_against_oracle(streams, [len(s) for s in srcs], in_align=in_align,
+                                        out_align=out_align, in_pad=in_pad, out_pad=out_pad)
+        assert outs == srcs
+
+
+def test_overlapping_match_periods():
+    # offset 1..70 with long matches: periodic copies of every period
+    streams, srcs = [], []
+    for off in list(range(1, 20)) + [31, 32, 33, 63, 64, 65, 70]:
+        lit = bytes((i * 29 + off) & 0xFF for i in range(off))
+        ml = 300 + off
+        s = bytes([0xFF if off >= 15 else (off << 4) | 15])
+        if off >= 15:
+            s = bytes([0xFF, off - 15])
+        s += lit + bytes([off & 0xFF, off >> 8, 255, ml - 4 - 15 - 255])
+        out = bytearray(lit)
+        for j in range(ml):
+            out.append(out[len(out) - off])
+        streams.append(s)
+        srcs.append(bytes(out))
+    outs, st = check_against_oracle(streams, [len(x) for x in srcs])
+    assert outs == srcs
+
+
+def test_corrupted_stream_fuzz():
+    rng = np.random.default_rng(5)
+    base = []
+    for n in [100, 1000, 5000]:
+        a = rng.integers(0, 3, n, dtype=np.uint8).tobytes()
+        base.append((O.lz4_compress_block(a)[0], n))
+    streams, caps = [], []
+    for trial in range(300):
+        s, n = base[trial % len(base)]
+        b = bytearray(s)
+        kind = trial % 3
+        if kind == 0:
+            for _ in range(int(rng.integers(1, 4))):
+                b[int(rng.integers(0, len(b)))] = int(rng.integers(0, 256))
+        elif kind == 1:
+            b = b[:int(rng.integers(0, len(b)))]
+        else:
+            b[int(rng.integers(0, len(b)))] ^= 0xFF
+        streams.append(bytes(b))
+        caps.append(n if trial % 5 else int(rng.integers(0, n + 1)))
+    check_against_oracle(streams, caps, out_pad=3)
