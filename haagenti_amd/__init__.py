@@ -50,6 +50,15 @@ if not os.path.exists(LIB_PATH):
         f"{LIB_PATH} is not built; run `python haagenti_amd/build.py` "
         "(the HIP extension is required, there is no CPU fallback)")
 
+try:
+    # torch ships its own HIP runtime under the same soname
+    # (libamdhip64.so.7).  Loading torch first makes this library bind to
+    # that copy, so the process has one HIP runtime and torch's streams and
+    # allocations are valid here.
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 _lib = C.CDLL(LIB_PATH)
 _vp, _sz, _i32, _u32 = C.c_void_p, C.c_size_t, C.c_int32, C.c_uint32
 

@@ -9,8 +9,11 @@
 
 namespace {
 
-hipStream_t pick_stream(hh_context *ctx, void *stream) {
-    return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+// The caller's stream is used as given; NULL is HIP's null stream (torch's
+// default stream is that null stream).  hh_context_stream() returns the
+// context's own stream for callers that want it.
+hipStream_t pick_stream(hh_context *, void *stream) {
+    return reinterpret_cast<hipStream_t>(stream);
 }
 
 int32_t from_hip(hipError_t e) {

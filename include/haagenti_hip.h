@@ -6,7 +6,8 @@
  * replaces (file:line in the reference repository).  Signatures carry plain
  * pointers and sizes only: device pointers are prefixed d_, host pointers h_
  * (or unprefixed in host-only calls), streams are hipStream_t passed as
- * void* (NULL = the context's own stream).
+ * void* (NULL = HIP's null stream; hh_context_stream() gives the context's
+ * own stream).
  *
  * Ownership: the caller allocates every input and output buffer.  A context
  * owns its device id, a stream, the IDCT basis table and a small scratch
