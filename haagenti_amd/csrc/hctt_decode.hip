@@ -10,24 +10,33 @@
 // Math.  With the basis M[v][j] = a_v cos(pi v (2j+1) / 128) (a_0 = 1/8,
 // a_v = 1/sqrt(32)), the tile is X = M^T C M.  It is computed as two 64^3
 // contractions on v_mfma_f32_32x32x16_f16:
-//   GEMM1  S = C M     (A = C rows from LDS, B = M from registers)
-//   GEMM2  X = M^T S   (A = M^T from registers, B = S straight from GEMM1's
-//                       accumulators)
-// The contraction index of both GEMMs runs in the order pi(k) below, which
-// is exactly the row order of the 32x32 accumulator layout, so GEMM1's
-// output registers are GEMM2's B fragments without any shuffle or LDS trip,
-// and the same M fragments serve as GEMM1's B and GEMM2's A.
+//   GEMM1  S = C M     (A = C, gathered into registers; B = M)
+//   GEMM2  X = M^T S   (A = M^T; B = S straight from GEMM1's accumulators)
+// The contraction index of both GEMMs runs in the order
+//   pi(16 s + 8 h + e) = 16 s + 8 (e / 4) + 4 h + e % 4
+// (k step s, lane half h, element e), which is exactly the row order of the
+// 32x32 accumulator layout, so GEMM1's output registers are GEMM2's B
+// fragments without any shuffle or LDS trip, and one table of M fragments
+// serves as GEMM1's B and GEMM2's A.
 //
-// Precision.  Every operand is split into f16 hi + lo (x = hi + lo exactly
-// for the coefficients, to ~2^-22 for M and S) and each GEMM runs three
-// passes hi*hi + hi*lo + lo*hi with f32 accumulation, giving ~f32 accuracy
-// (the bar is max-abs error <= 1e-3 x RMS).  Coefficients are prescaled by
-// 2^E per tile (E from the largest f16 scale exponent) and M by 2^8 so that
-// the lo parts stay in f16's normal range; the output is rescaled exactly.
+// Precision.  Operands are split into f16 hi + lo (exact for the
+// coefficients, ~2^-20 relative for M and S) and each GEMM runs three passes
+// hi*hi + hi*lo + lo*hi with f32 accumulation (max-abs error ~1e-6 x RMS; the
+// bar is 1e-3 x RMS).  Coefficients are prescaled by 2^E per tile (E from
+// the largest f16 scale exponent) and M by 2^8 so that the lo parts stay in
+// f16's normal range; the output is rescaled exactly.
 //
-// LDS per wave: staged tile bytes, scaled f32 scales, C hi and C lo
-// (64 x 64 f16 each, 16-byte chunks XOR-swizzled by row to spread banks);
-// the C area is reused to stage the output tile for coalesced row stores.
+// Data flow per tile (per wave):
+//   1. each lane reads one 64-bit bitmap row; a wave prefix sum gives every
+//      row's first retained index;
+//   2. the k retained coefficients are dequantized once, in index order, into
+//      a per-wave LDS table V[r] = f16 hi | f16 lo << 16;
+//   3. every lane gathers its GEMM1 A fragments (2 rows x 32 columns) from V
+//      by bitmap rank, branch-free (unset positions read a zero word);
+//   4. GEMM1 / GEMM2 per 32-column block; the M fragments live in LDS, shared
+//      by the workgroup;
+//   5. the output block is parked in LDS (reusing V's space) and written as
+//      coalesced 16-byte row segments.
 #include <cstring>
 
 #include "hh_internal.hpp"
@@ -36,13 +45,22 @@ namespace hh {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Global-address-space views.  Pointers read from LDS are generic; memory
+// operations through them would be flat instructions, whose completion also
+// counts against the LDS wait counter.
+#define HH_GLOBAL __attribute__((address_space(1)))
+typedef const uint8_t HH_GLOBAL g_u8;
+typedef const u32x4 HH_GLOBAL g_u32x4;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr uint32_t kCBytes = 2u * 64u * 64u * 2u;  // C hi + C lo
-constexpr uint32_t kScaleBytes = 512;               // up to 128 f32 scales
+constexpr uint32_t kMTabBytes = 2 * 2 * 4 * 64 * 16;  // [hl][block][kstep][lane] x 16 B
+constexpr uint32_t kZeroBytes = 16;
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -50,8 +68,9 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ floatx16 mfma(half8 a, half8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
@@ -61,15 +80,25 @@ __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        uint32_t o = __shfl_xor(v, d);
+        const uint32_t o = __shfl_xor(v, d);
         v = v > o ? v : o;
     }
     return v;
 }
 
+// (a, b) -> f16 hi pair and f16 lo pair with a = hi.x + lo.x, b = hi.y + lo.y
+// to ~2^-20 relative (exactly when a, b have at most 21 significant bits).
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(a, b);
+    const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(a - (float)h.x, b - (float)h.y);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
 constexpr int kMaxTensors = 8;
+constexpr int kMaxPrefetch = 3;  // 16-byte loads per lane: tiles up to 3 KiB (k <= 4096)
 struct TileBatch {
     const uint8_t *tiles[kMaxTensors];
     void *out[kMaxTensors];
@@ -81,57 +110,107 @@ struct TileBatch {
     uint32_t tb[kMaxTensors];
     uint32_t dword_ok[kMaxTensors];
     uint32_t n;
-    uint32_t wave_lds;
+    uint32_t wave_lds;  // per-wave LDS bytes: V/output union + staged tile bytes
+    uint32_t vo_bytes;  // size of the V/output union
 };
 
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void hctt_decode_kernel(TileBatch B,
-                                                                   const half8 *__restrict__ basis) {
+// Workgroup LDS layout: [batch descriptor][M fragment table][zero word][per-wave areas].
+// The descriptor is copied from the kernel arguments once: indexing the
+// by-value argument with a per-tile tensor index would compile to vector
+// loads whose waits also stall on the prefetch and the output stores.
+constexpr uint32_t kBatchBytes = (sizeof(TileBatch) + 15u) & ~15u;
+constexpr uint32_t kMTabOff = kBatchBytes;
+constexpr uint32_t kZeroOff = kMTabOff + kMTabBytes;
+constexpr uint32_t kSharedBytes = kZeroOff + kZeroBytes;
+
+// Loads the bytes of global tile gt into registers, 16 bytes per lane per
+// KiB, always issuing kMaxPrefetch loads (chunks past the tile end re-read
+// its last 16 bytes) so that the wait counts stay static.  Register chunk i
+// holds tile bytes [16*(lane + 64 i), +16) wherever those lie inside the
+// tile.  DW: every tile of
+// the batch starts 4-byte aligned and has a size divisible by 4 (16-byte
+// loads at 4-byte alignment); otherwise bytes are gathered one by one.
+template <bool DW>
+__device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, int lane,
+                                              u32x4 (&pf)[kMaxPrefetch]) {
+    uint32_t ti = 0;
+    while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
+    const uint32_t tb = B.tb[ti];
+    g_u8 *src = (g_u8 *)B.tiles[ti] + (size_t)(gt - B.start[ti]) * tb;
+#pragma unroll
+    for (int i = 0; i < kMaxPrefetch; i++) {
+        const uint32_t off = 16u * (lane + 64u * i);
+        if constexpr (DW) {
+            // A chunk reaching past the tile end is read at tb - 16 (tiles
+            // are >= 515 bytes) and shifted down by s dwords so that byte
+            // off lands first; dwords beyond the tile end are don't-care.
+            const uint32_t o = off + 16 <= tb ? off : tb - 16;
+            const u32x4 v = *(g_u32x4 *)(src + o);
+            const uint32_t s = (off - o) >> 2;
+            const uint32_t d0 = s == 0 ? v[0] : s == 1 ? v[1] : s == 2 ? v[2] : v[3];
+            const uint32_t d1 = s == 0 ? v[1] : s == 1 ? v[2] : v[3];
+            const uint32_t d2 = s == 0 ? v[2] : v[3];
+            pf[i] = u32x4{d0, d1, d2, v[3]};
+        } else {
+            uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int b = 0; b < 16; b++)
+                if (off + b < tb) d[b >> 2] |= (uint32_t)src[off + b] << (8 * (b & 3));
+            pf[i] = u32x4{d[0], d[1], d[2], d[3]};
+        }
+    }
+}
+
+template <int DT, bool DW>
+__global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
+                                                                   const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int h = lane >> 5;
     const int l32 = lane & 31;
-    const uint32_t wave_lds = B.wave_lds;
-    uint8_t *wsm = smem + wave * wave_lds;
-    const uint32_t payb = wave_lds - kScaleBytes - kCBytes;
-    uint8_t *pay = wsm;
-    float *sc32 = reinterpret_cast<float *>(wsm + payb);
-    _Float16 *chi = reinterpret_cast<_Float16 *>(wsm + payb + kScaleBytes);
-    _Float16 *clo = chi + 64 * 64;
-    float *xs = reinterpret_cast<float *>(chi);
+    u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
+    for (int i = threadIdx.x; i < (int)(sizeof(TileBatch) / 4); i += kThreads)
+        reinterpret_cast<uint32_t *>(smem)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
+    for (int i = threadIdx.x; i < (int)(kMTabBytes / 16); i += kThreads) mtab[i] = basis[i];
+    if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem);
+    const uint32_t wbase = kSharedBytes + wave * B.wave_lds;  // byte offset of this wave's area
+    const uint32_t pbase = wbase + B.vo_bytes;                // staged tile bytes
+    uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
+    const uint8_t *pay = smem + pbase;
 
-    half8 mf[2][2][4];  // [hi/lo][column block][k step]
-#pragma unroll
-    for (int hl = 0; hl < 2; hl++)
-#pragma unroll
-        for (int jb = 0; jb < 2; jb++)
-#pragma unroll
-            for (int s = 0; s < 4; s++) mf[hl][jb][s] = basis[((hl * 2 + jb) * 4 + s) * 64 + lane];
-
+    // Tile bytes travel global -> registers (prefetched one tile ahead, 16 B
+    // per lane per 1 KiB) -> LDS, so no global latency sits on the critical
+    // path of a tile.
     const uint32_t ntiles = B.start[B.n];
-    for (uint32_t gt = blockIdx.x * kWaves + wave; gt < ntiles; gt += gridDim.x * kWaves) {
+    const uint32_t stride = gridDim.x * kWaves;
+    u32x4 pf[kMaxPrefetch];
+    uint32_t gt = blockIdx.x * kWaves + wave;
+    if (gt < ntiles) {
+        prefetch_tile<DW>(B, gt, lane, pf);
+#pragma unroll
+        for (int i = 0; i < kMaxPrefetch; i++)
+            *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
+    }
+    for (; gt < ntiles; gt += stride) {
         uint32_t ti = 0;
         while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
         const uint32_t t = gt - B.start[ti];
-        const uint32_t k = B.k[ti], tb = B.tb[ti], cols = B.cols[ti];
-        const uint32_t tiles_per_row = B.tiles_per_row[ti], dword_ok = B.dword_ok[ti];
-        void *__restrict__ out = B.out[ti];
-        int32_t *__restrict__ tstatus = B.status[ti];
+        const uint32_t k = B.k[ti], cols = B.cols[ti];
         const uint32_t nsc = (k + 31) >> 5;
         const uint32_t nib_off = 512 + 2 * nsc;
-        const uint8_t *src = B.tiles[ti] + (size_t)t * tb;
-        // 1. stage the tile's bytes in LDS
-        if (dword_ok) {
-            const uint32_t *s32 = reinterpret_cast<const uint32_t *>(src);
-            uint32_t *d32 = reinterpret_cast<uint32_t *>(pay);
-            for (uint32_t i = lane; i < (tb >> 2); i += 64) d32[i] = s32[i];
-        } else {
-            for (uint32_t i = lane; i < tb; i += 64) pay[i] = src[i];
-        }
+
+        // This tile's bytes are staged in LDS.  Fetch the next tile now; it is
+        // staged at the end of this iteration, long after the loads landed
+        // and before this tile's output stores are issued (the wait counter
+        // is in order, so stores issued earlier would have to drain first).
+        const bool has_next = gt + stride < ntiles;
+        prefetch_tile<DW>(B, has_next ? gt + stride : gt, lane, pf);
         wave_sync();
 
-        // 2. bitmap row `lane`: set-bit count and exclusive prefix over rows
+        // 1. bitmap row `lane`: set-bit count and exclusive prefix over rows
         const uint64_t bits = reinterpret_cast<const uint64_t *>(pay)[lane];
         const uint32_t cnt = (uint32_t)__popcll(bits);
         uint32_t incl = cnt;
@@ -140,79 +219,97 @@ __global__ __launch_bounds__(kThreads, 1) void hctt_decode_kernel(TileBatch B,
             const uint32_t y = __shfl_up(incl, d);
             if (lane >= d) incl += y;
         }
-        const uint32_t total = __shfl(incl, 63);
-        const bool ok = total == k;
-        uint32_t rank = incl - cnt;
+        const bool ok = __shfl(incl, 63) == k;
+        const uint32_t pre = incl - cnt;
 
-        // 3. per-tile power-of-two prescale from the largest scale exponent
+        // 2. per-tile power-of-two prescale from the largest scale exponent
+        const uint16_t *sc16 = reinterpret_cast<const uint16_t *>(pay + 512);
         uint32_t emax = 0;
         for (uint32_t g = lane; g < nsc; g += 64) {
-            const uint32_t sb = (uint32_t)pay[512 + 2 * g] | ((uint32_t)pay[513 + 2 * g] << 8);
-            const uint32_t ex = (sb >> 10) & 31u;
+            const uint32_t ex = ((uint32_t)sc16[g] >> 10) & 31u;
             emax = ex > emax ? ex : emax;
         }
         emax = wave_max_u32(emax);
         const int E = 21 - (int)emax;
         const float pe = pow2f(E);
-        for (uint32_t g = lane; g < nsc; g += 64) {
-            const uint32_t sb = (uint32_t)pay[512 + 2 * g] | ((uint32_t)pay[513 + 2 * g] << 8);
-            sc32[g] = f16_bits_to_f32(sb) * pe;
-        }
-        wave_sync();
 
-        // 4. dequantize + scatter row `lane` into C hi/lo (swizzled chunks)
+        // 3. dense table of the retained coefficients, 4 per lane per pass:
+        //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E exactly
+        if (ok) {
+            const uint16_t *nib16 = reinterpret_cast<const uint16_t *>(pay + nib_off);
+            for (uint32_t g4 = lane; 4 * g4 < k; g4 += 64) {
+                const uint32_t r0 = 4 * g4;
+                const uint32_t w4 = nib16[g4];  // nibbles r0 .. r0+3, low first
+                const float s = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
+                uint32_t v[4];
 #pragma unroll
-        for (int g = 0; g < 8; g++) {
-            half8 hv, lv;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int v = 8 * g + e;
-                float c = 0.0f;
-                if (ok && ((bits >> v) & 1ull)) {
-                    const uint32_t r = rank++;
-                    const uint32_t byte = pay[nib_off + (r >> 1)];
-                    const uint32_t q = (r & 1u) ? (byte >> 4) : (byte & 15u);
-                    c = (float)((int)q - 8) * sc32[r >> 5];
+                for (int e = 0; e < 4; e += 2) {
+                    const float x0 = (float)((int)((w4 >> (4 * e)) & 15u) - 8) * s;
+                    const float x1 = (float)((int)((w4 >> (4 * e + 4)) & 15u) - 8) * s;
+                    uint32_t hi, lo;
+                    split2(x0, x1, hi, lo);
+                    v[e] = __builtin_amdgcn_perm(lo, hi, 0x05040100u);
+                    v[e + 1] = __builtin_amdgcn_perm(lo, hi, 0x07060302u);
                 }
-                const _Float16 hi = (_Float16)c;
-                hv[e] = hi;
-                lv[e] = (_Float16)(c - (float)hi);
+                if (r0 + 4 <= k) {
+                    *reinterpret_cast<u32x4 *>(V + r0) = u32x4{v[0], v[1], v[2], v[3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (r0 + e < k) V[r0 + e] = v[e];
+                }
             }
-            const int sw = ((g ^ (lane & 7)) << 3);
-            *reinterpret_cast<half8 *>(chi + lane * 64 + sw) = hv;
-            *reinterpret_cast<half8 *>(clo + lane * 64 + sw) = lv;
         }
         wave_sync();
 
-        // 5-7. Per 32-column block jb of the output:
-        //   GEMM1: S[:, jb] = C M[:, jb]    (rows u, contraction over v in pi order)
-        //   GEMM2: X[:, jb] = M^T S[:, jb]  (B fragments are GEMM1's accumulator rows)
-        // and the block is parked in LDS.  Keeping one column block live at a
-        // time halves the accumulator registers.
+        // 4. GEMM1 A fragments: rows u = 32 ub + l32, columns pi(16 s + 8 h + e)
+        const uint64_t bits_r[2] = {__shfl(bits, l32), __shfl(bits, l32 + 32)};
+        const uint32_t pre_r[2] = {__shfl(pre, l32), __shfl(pre, l32 + 32)};
+        u32x4 ahi[2][4], alo[2][4];
+#pragma unroll
+        for (int ub = 0; ub < 2; ub++) {
+            const uint64_t b64 = ok ? bits_r[ub] : 0ull;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                uint32_t w[8];
+#pragma unroll
+                for (int run = 0; run < 2; run++) {
+                    const int v0 = 16 * s + 8 * run + 4 * h;
+                    uint32_t rank = pre_r[ub] + (uint32_t)__popcll(b64 & ((1ull << v0) - 1ull));
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; e4++) {
+                        const uint32_t bit = (uint32_t)(b64 >> (v0 + e4)) & 1u;
+                        const uint32_t addr = bit ? wbase + 4 * rank : kZeroOff;
+                        w[4 * run + e4] = *reinterpret_cast<const uint32_t *>(smem + addr);
+                        rank += bit;
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    ahi[ub][s][p] = __builtin_amdgcn_perm(w[2 * p + 1], w[2 * p], 0x05040100u);
+                    alo[ub][s][p] = __builtin_amdgcn_perm(w[2 * p + 1], w[2 * p], 0x07060302u);
+                }
+            }
+        }
+        wave_sync();
+
+        // 5-7. per 32-column output block jb: GEMM1, GEMM2, park in LDS
         const float s_down = 1.0f / 256.0f;
         const float os = pow2f(-(E + 8));
-        float xv[2][16];
-#pragma unroll
+#pragma unroll 1
         for (int jb = 0; jb < 2; jb++) {
             floatx16 acc[2];
             acc[0] = floatx16{};
             acc[1] = floatx16{};
 #pragma unroll
             for (int s = 0; s < 4; s++) {
+                const u32x4 mh = mtab[((0 * 2 + jb) * 4 + s) * 64 + lane];
+                const u32x4 ml = mtab[((1 * 2 + jb) * 4 + s) * 64 + lane];
 #pragma unroll
                 for (int ub = 0; ub < 2; ub++) {
-                    const int u = 32 * ub + l32;
-                    const int o1 = u * 64 + (((2 * s) ^ (u & 7)) << 3) + 4 * h;
-                    const int o2 = u * 64 + (((2 * s + 1) ^ (u & 7)) << 3) + 4 * h;
-                    const half4 h1 = *reinterpret_cast<const half4 *>(chi + o1);
-                    const half4 h2 = *reinterpret_cast<const half4 *>(chi + o2);
-                    const half4 q1 = *reinterpret_cast<const half4 *>(clo + o1);
-                    const half4 q2 = *reinterpret_cast<const half4 *>(clo + o2);
-                    const half8 ahi = __builtin_shufflevector(h1, h2, 0, 1, 2, 3, 4, 5, 6, 7);
-                    const half8 alo = __builtin_shufflevector(q1, q2, 0, 1, 2, 3, 4, 5, 6, 7);
-                    acc[ub] = mfma(ahi, mf[0][jb][s], acc[ub]);
-                    acc[ub] = mfma(ahi, mf[1][jb][s], acc[ub]);
-                    acc[ub] = mfma(alo, mf[0][jb][s], acc[ub]);
+                    acc[ub] = mfma(ahi[ub][s], mh, acc[ub]);
+                    acc[ub] = mfma(ahi[ub][s], ml, acc[ub]);
+                    acc[ub] = mfma(alo[ub][s], mh, acc[ub]);
                 }
             }
             floatx16 xacc[2];
@@ -223,72 +320,85 @@ __global__ __launch_bounds__(kThreads, 1) void hctt_decode_kernel(TileBatch B,
 #pragma unroll
                 for (int t2 = 0; t2 < 2; t2++) {
                     const int sk = 2 * ub + t2;
-                    half8 bhi, blo;
+                    u32x4 bhi, blo;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float x = acc[ub][8 * t2 + e] * s_down;
-                        const _Float16 hi = (_Float16)x;
-                        bhi[e] = hi;
-                        blo[e] = (_Float16)(x - (float)hi);
+                    for (int p = 0; p < 4; p++) {
+                        uint32_t hp, lp;
+                        split2(acc[ub][8 * t2 + 2 * p] * s_down, acc[ub][8 * t2 + 2 * p + 1] * s_down,
+                               hp, lp);
+                        bhi[p] = hp;
+                        blo[p] = lp;
                     }
 #pragma unroll
                     for (int ib = 0; ib < 2; ib++) {
-                        xacc[ib] = mfma(mf[0][ib][sk], bhi, xacc[ib]);
-                        xacc[ib] = mfma(mf[1][ib][sk], bhi, xacc[ib]);
-                        xacc[ib] = mfma(mf[0][ib][sk], blo, xacc[ib]);
+                        const u32x4 mh = mtab[((0 * 2 + ib) * 4 + sk) * 64 + lane];
+                        const u32x4 ml = mtab[((1 * 2 + ib) * 4 + sk) * 64 + lane];
+                        xacc[ib] = mfma(mh, bhi, xacc[ib]);
+                        xacc[ib] = mfma(ml, bhi, xacc[ib]);
+                        xacc[ib] = mfma(mh, blo, xacc[ib]);
                     }
                 }
             }
-            if (jb == 0) {
+            // park rows i = 32 ib + (r&3) + 8 (r>>2) + 4 h, column 32 jb + l32
+            if constexpr (DT == HH_F32) {
+                float *xs = reinterpret_cast<float *>(smem + wbase);
 #pragma unroll
                 for (int ib = 0; ib < 2; ib++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) xv[ib][r] = xacc[ib][r] * os;
+                    for (int r = 0; r < 16; r++)
+                        xs[(32 * ib + (r & 3) + 8 * (r >> 2) + 4 * h) * 64 + 32 * jb + l32] =
+                            xacc[ib][r] * os;
             } else {
-                // C has been fully read (both column blocks): park the output
-                wave_sync();
+                uint16_t *xs = reinterpret_cast<uint16_t *>(smem + wbase);
 #pragma unroll
                 for (int ib = 0; ib < 2; ib++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int i = 32 * ib + (r & 3) + 8 * (r >> 2) + 4 * h;
-                        xs[i * 64 + l32] = xv[ib][r];
-                        xs[i * 64 + 32 + l32] = xacc[ib][r] * os;
+                    for (int r = 0; r < 16; r += 2) {
+                        const float a = xacc[ib][r] * os, b = xacc[ib][r + 1] * os;
+                        uint32_t pk;
+                        if constexpr (DT == HH_BF16) {
+                            pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
+                        } else {
+                            pk = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+                        }
+                        const int i0 = 32 * ib + (r & 3) + 8 * (r >> 2) + 4 * h;
+                        xs[i0 * 64 + 32 * jb + l32] = (uint16_t)pk;
+                        xs[(i0 + 1) * 64 + 32 * jb + l32] = (uint16_t)(pk >> 16);
                     }
             }
         }
         wave_sync();
 
-        // 8. coalesced row stores
-        const uint32_t tr = t / tiles_per_row, tc = t % tiles_per_row;
+        // stage the next tile's bytes (the current ones are no longer needed)
+#pragma unroll
+        for (int i = 0; i < kMaxPrefetch; i++)
+            *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
+
+        // 8. coalesced row stores (16 bytes per lane)
+        const uint32_t tpr = B.tiles_per_row[ti];
+        const uint32_t tr = t / tpr, tc = t % tpr;
         const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
         if constexpr (DT == HH_F32) {
-            float *o = reinterpret_cast<float *>(out) + base;
+            const float *xs = reinterpret_cast<const float *>(smem + wbase);
+            float HH_GLOBAL *o = (float HH_GLOBAL *)B.out[ti] + base;
 #pragma unroll
             for (int it = 0; it < 16; it++) {
                 const int row = 4 * it + (lane >> 4), c4 = (lane & 15) * 4;
-                const float4 v = *reinterpret_cast<const float4 *>(xs + row * 64 + c4);
-                *reinterpret_cast<float4 *>(o + (size_t)row * cols + c4) = v;
+                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c4) =
+                    *reinterpret_cast<const u32x4 *>(xs + row * 64 + c4);
             }
         } else {
-            uint16_t *o = reinterpret_cast<uint16_t *>(out) + base;
+            const uint16_t *xs = reinterpret_cast<const uint16_t *>(smem + wbase);
+            uint16_t HH_GLOBAL *o = (uint16_t HH_GLOBAL *)B.out[ti] + base;
 #pragma unroll
             for (int it = 0; it < 8; it++) {
                 const int row = 8 * it + (lane >> 3), c8 = (lane & 7) * 8;
-                const float4 a = *reinterpret_cast<const float4 *>(xs + row * 64 + c8);
-                const float4 b = *reinterpret_cast<const float4 *>(xs + row * 64 + c8 + 4);
-                const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-                uint32_t p[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t lo = DT == HH_BF16 ? f32_to_bf16_bits(f[2 * q]) : f32_to_f16_bits(f[2 * q]);
-                    const uint32_t hi = DT == HH_BF16 ? f32_to_bf16_bits(f[2 * q + 1]) : f32_to_f16_bits(f[2 * q + 1]);
-                    p[q] = lo | (hi << 16);
-                }
-                *reinterpret_cast<uint4 *>(o + (size_t)row * cols + c8) = make_uint4(p[0], p[1], p[2], p[3]);
+                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c8) =
+                    *reinterpret_cast<const u32x4 *>(xs + row * 64 + c8);
             }
         }
-        if (tstatus != nullptr && lane == 0) tstatus[t] = ok ? HH_OK : HH_ERR_CORRUPTED_DATA;
+        if (B.status[ti] != nullptr && lane == 0)
+            ((int32_t HH_GLOBAL *)B.status[ti])[t] = ok ? HH_OK : HH_ERR_CORRUPTED_DATA;
         wave_sync();
     }
 }
@@ -300,8 +410,8 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
     for (uint32_t first = 0; first < n; first += kMaxTensors) {
         TileBatch B;
         std::memset(&B, 0, sizeof(B));
-        uint32_t max_tb = 0, total = 0;
-        B.n = 0;
+        uint32_t max_k = 0, total = 0;
+        bool all_dw = true;
         for (uint32_t i = first; i < n && B.n < (uint32_t)kMaxTensors; i++) {
             const hh_hctt_tensor &T = tensors[i];
             const uint32_t nt = (T.rows / 64) * (T.cols / 64);
@@ -318,26 +428,39 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
             B.tb[j] = tb;
             B.dword_ok[j] = ((tb & 3u) == 0 && ((uintptr_t)T.d_tiles & 3u) == 0) ? 1u : 0u;
             total += nt;
-            max_tb = tb > max_tb ? tb : max_tb;
+            max_k = T.k > max_k ? T.k : max_k;
+            all_dw = all_dw && B.dword_ok[j];
         }
         if (B.n == 0) continue;
         B.start[B.n] = total;
-        const uint32_t payb = (max_tb + 15u) & ~15u;
-        B.wave_lds = payb + kScaleBytes + kCBytes;
-        const uint32_t lds = B.wave_lds * kWaves;
-        // one 4-wave workgroup per CU (1 wave per SIMD), persistent over tiles
-        uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256);
+        // per wave: the V table (k words) shares space with the parked output
+        // tile; the staged tile bytes follow (2 bytes of slack for the last
+        // 16-bit nibble read)
+        const uint32_t vbytes = 4 * max_k;
+        const uint32_t obytes = 64 * 64 * (dtype == HH_F32 ? 4u : 2u);
+        B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
+        B.wave_lds = B.vo_bytes + 16u * 64u * kMaxPrefetch;
+        const uint32_t lds = kSharedBytes + B.wave_lds * kWaves;
+        const uint32_t per_cu = (160u * 1024u) / lds >= 2 ? 2u : 1u;
+        uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256) * per_cu;
         const uint32_t need = (total + kWaves - 1) / kWaves;
         if (grid > need) grid = need;
-        const half8 *basis = reinterpret_cast<const half8 *>(d_basis);
+        const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
         hipError_t e = hipSuccess;
-#define HH_LAUNCH(DTV)                                                                  \
-    do {                                                                                \
-        e = hipFuncSetAttribute((const void *)hctt_decode_kernel<DTV>,                  \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);  \
-        if (e != hipSuccess) return e;                                                  \
-        hipLaunchKernelGGL(hctt_decode_kernel<DTV>, dim3(grid), dim3(kThreads), lds, s, \
-                           B, basis);                                                   \
+#define HH_LAUNCH2(DTV, DWV)                                                                 \
+    do {                                                                                     \
+        e = hipFuncSetAttribute((const void *)hctt_decode_kernel<DTV, DWV>,                  \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
+        if (e != hipSuccess) return e;                                                       \
+        hipLaunchKernelGGL((hctt_decode_kernel<DTV, DWV>), dim3(grid), dim3(kThreads), lds, \
+                           s, B, basis);                                                     \
+    } while (0)
+#define HH_LAUNCH(DTV)                  \
+    do {                                \
+        if (all_dw)                     \
+            HH_LAUNCH2(DTV, true);      \
+        else                            \
+            HH_LAUNCH2(DTV, false);     \
     } while (0)
         switch (dtype) {
             case HH_F32: HH_LAUNCH(HH_F32); break;
@@ -346,6 +469,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
             default: return hipErrorInvalidValue;
         }
 #undef HH_LAUNCH
+#undef HH_LAUNCH2
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

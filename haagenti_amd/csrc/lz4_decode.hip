@@ -7,13 +7,17 @@
 //
 // Per wave:
 //  * Token parsing is wave-uniform (scalar registers).  The compressed
-//    stream is read through a 256-byte register window (one dword per lane)
-//    and bytes are picked out with v_readlane; the window at the byte after a
-//    literal run is fetched before the run is copied, so its latency hides
-//    behind the copy.
+//    stream is read through a 256-byte register window (one dword per lane);
+//    single bytes are picked out with v_readlane, and a run of 255-valued
+//    length-extension bytes is measured with one ballot per window instead of
+//    byte by byte.  The window at the byte after a literal run is fetched
+//    before the run is copied, so its latency hides behind the copy.
 //  * Literal runs and non-overlapping matches are copied in destination-
-//    aligned 16-byte chunks (one per lane, 1 KiB per wave instruction);
+//    aligned 16-byte chunks, one per lane (1 KiB per wave instruction), as a
+//    software pipeline that keeps two groups of kCopyUnroll chunks in flight;
 //    an unaligned source is realigned with v_alignbyte on 5 loaded dwords.
+//    Only chunks whose reads could leave the caller's buffer take a clamped
+//    byte-wise path.
 //  * Overlapping matches (offset < length) are periodic with period offset:
 //    out[op + j] = out[op - offset + (j mod offset)], all of whose source
 //    bytes precede op, so every lane copies independently.
@@ -30,80 +34,126 @@
 namespace hh {
 namespace {
 
-constexpr int kWaves = 4;               // blocks per workgroup
+constexpr int kWaves = 4;  // blocks per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kCopyUnroll = 4;
 
-__device__ __forceinline__ void wave_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-}
+// Compiler-only ordering point between a match's stores and the next
+// sequence's loads; the hardware already performs a wave's vector memory
+// operations in order, so no wait instruction is emitted.
+__device__ __forceinline__ void wave_fence() { __asm__ __volatile__("" ::: "memory"); }
 
-// Dword at 4-aligned address a; bytes outside [lo, hi) read as zero.
-__device__ __forceinline__ uint32_t ld_dw(uintptr_t a, uintptr_t lo, uintptr_t hi) {
-    if (a >= lo && a + 4 <= hi) return *reinterpret_cast<const uint32_t *>(a);
+// Dword at 4-aligned p; bytes outside [lo, hi) read as zero.
+__device__ __forceinline__ uint32_t ld_dw_clamped(const uint8_t *__restrict__ p,
+                                                  const uint8_t *__restrict__ lo,
+                                                  const uint8_t *__restrict__ hi) {
+    if (p >= lo && p + 4 <= hi) return *reinterpret_cast<const uint32_t *>(p);
     uint32_t v = 0;
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const uintptr_t x = a + b;
-        if (x >= lo && x < hi) v |= (uint32_t)(*reinterpret_cast<const uint8_t *>(x)) << (8 * b);
-    }
+    for (int b = 0; b < 4; b++)
+        if (p + b >= lo && p + b < hi) v |= (uint32_t)p[b] << (8 * b);
     return v;
 }
 
-// dst[0..n) = src[0..n); [src, src+n) lies inside the readable [slo, shi).
-__device__ __forceinline__ void wave_copy(uint8_t *dst, uintptr_t src, uint32_t n, uintptr_t slo,
-                                          uintptr_t shi, int lane) {
+struct Chunk {
+    uint32_t d[5];
+};
+
+__device__ __forceinline__ uint4 realign(const Chunk &c, uint32_t sh) {
+    uint4 o;
+    o.x = __builtin_amdgcn_alignbyte(c.d[1], c.d[0], sh);
+    o.y = __builtin_amdgcn_alignbyte(c.d[2], c.d[1], sh);
+    o.z = __builtin_amdgcn_alignbyte(c.d[3], c.d[2], sh);
+    o.w = __builtin_amdgcn_alignbyte(c.d[4], c.d[3], sh);
+    return o;
+}
+
+// dst[0..n) = src[0..n).  [src, src+n) lies inside the readable [lo, hi).
+// dst and src may point into the same buffer (non-overlapping matches), so
+// neither is declared __restrict__.
+__device__ __forceinline__ void wave_copy(uint8_t *dst, const uint8_t *src, uint32_t n,
+                                          const uint8_t *__restrict__ lo,
+                                          const uint8_t *__restrict__ hi, int lane) {
     uint32_t head = (uint32_t)((16u - ((uintptr_t)dst & 15u)) & 15u);
     if (head > n) head = n;
-    if (lane < (int)head) dst[lane] = *reinterpret_cast<const uint8_t *>(src + lane);
+    if (lane < (int)head) dst[lane] = src[lane];
     dst += head;
     src += head;
     n -= head;
     const uint32_t nch = n >> 4;
-    const uint32_t sh = (uint32_t)(src & 3u);
-    const uintptr_t sal = src - sh;
-    for (uint32_t c0 = 0; c0 < nch; c0 += 64 * kCopyUnroll) {
-        uint4 o[kCopyUnroll];
+    const uint32_t sh = (uint32_t)((uintptr_t)src & 3u);
+    const uint8_t *base = src - sh;  // 4-aligned
+    const uint32_t *s32 = reinterpret_cast<const uint32_t *>(base);
+    uint4 *d16 = reinterpret_cast<uint4 *>(dst);
+    const uint32_t span = 20u;  // bytes a chunk's loads touch
+    // chunks [c_lo, c_hi) are readable without clamping
+    const uint32_t c_lo = base >= lo ? 0u : 1u;
+    const int64_t room = (int64_t)(hi - base);
+    uint32_t c_hi = room >= (int64_t)span ? (uint32_t)((room - span) / 16 + 1) : 0u;
+    if (c_hi > nch) c_hi = nch;
+    if (c_hi < c_lo) c_hi = c_lo;
+
+    auto load = [&](uint32_t c, Chunk &k) {
+        const uint32_t *p = s32 + 4 * (size_t)c;
+        k.d[0] = p[0];
+        k.d[1] = p[1];
+        k.d[2] = p[2];
+        k.d[3] = p[3];
+        k.d[4] = p[4];  // unused when sh == 0 (alignbyte by 0)
+    };
+    auto load_clamped = [&](uint32_t c, Chunk &k) {
+        const uint8_t *p = base + 16 * (size_t)c;
 #pragma unroll
-        for (int u = 0; u < kCopyUnroll; u++) {
-            const uint32_t c = c0 + 64u * u + lane;
-            if (c < nch) {
-                const uintptr_t a = sal + 16u * (uintptr_t)c;
-                uint32_t d0, d1, d2, d3, d4 = 0;
-                if (a >= slo && a + 20 <= shi) {
-                    const uint32_t *p = reinterpret_cast<const uint32_t *>(a);
-                    d0 = p[0];
-                    d1 = p[1];
-                    d2 = p[2];
-                    d3 = p[3];
-                    if (sh) d4 = p[4];
-                } else {
-                    d0 = ld_dw(a, slo, shi);
-                    d1 = ld_dw(a + 4, slo, shi);
-                    d2 = ld_dw(a + 8, slo, shi);
-                    d3 = ld_dw(a + 12, slo, shi);
-                    if (sh) d4 = ld_dw(a + 16, slo, shi);
-                }
-                o[u].x = __builtin_amdgcn_alignbyte(d1, d0, sh);
-                o[u].y = __builtin_amdgcn_alignbyte(d2, d1, sh);
-                o[u].z = __builtin_amdgcn_alignbyte(d3, d2, sh);
-                o[u].w = __builtin_amdgcn_alignbyte(d4, d3, sh);
-            }
+        for (int i = 0; i < 4; i++) k.d[i] = ld_dw_clamped(p + 4 * i, lo, hi);
+        k.d[4] = ld_dw_clamped(p + 16, lo, hi);
+    };
+
+    // edge chunks before c_lo
+    for (uint32_t c = lane; c < c_lo; c += 64) {
+        Chunk k;
+        load_clamped(c, k);
+        d16[c] = realign(k, sh);
+    }
+    // pipelined body: groups of 64*U chunks, two groups in flight
+    constexpr uint32_t G = 64u * kCopyUnroll;
+    uint32_t c0 = c_lo;
+    if (c0 + G <= c_hi) {
+        Chunk a[kCopyUnroll];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; u++) load(c0 + 64u * u + lane, a[u]);
+        for (uint32_t c1 = c0 + G; c1 + G <= c_hi; c1 += G) {
+            Chunk b[kCopyUnroll];
+#pragma unroll
+            for (int u = 0; u < kCopyUnroll; u++) load(c1 + 64u * u + lane, b[u]);
+#pragma unroll
+            for (int u = 0; u < kCopyUnroll; u++) d16[c0 + 64u * u + lane] = realign(a[u], sh);
+#pragma unroll
+            for (int u = 0; u < kCopyUnroll; u++) a[u] = b[u];
+            c0 = c1;
         }
 #pragma unroll
-        for (int u = 0; u < kCopyUnroll; u++) {
-            const uint32_t c = c0 + 64u * u + lane;
-            if (c < nch) reinterpret_cast<uint4 *>(dst)[c] = o[u];
-        }
+        for (int u = 0; u < kCopyUnroll; u++) d16[c0 + 64u * u + lane] = realign(a[u], sh);
+        c0 += G;
+    }
+    // remaining unclamped chunks, then clamped ones at the end of the buffer
+    for (uint32_t c = c0 + lane; c < c_hi; c += 64) {
+        Chunk k;
+        load(c, k);
+        d16[c] = realign(k, sh);
+    }
+    for (uint32_t c = (c_hi > c0 ? c_hi : c0) + lane; c < nch; c += 64) {
+        Chunk k;
+        load_clamped(c, k);
+        d16[c] = realign(k, sh);
     }
     const uint32_t done = nch * 16u, tail = n - done;
-    if (lane < (int)tail) dst[done + lane] = *reinterpret_cast<const uint8_t *>(src + done + lane);
+    if (lane < (int)tail) dst[done + lane] = src[done + lane];
 }
 
-// Periodic copy for offset < length: out[j] = out[j - off + ((j) mod off)]
-// relative to the match start; sources all precede the destination.
-__device__ __forceinline__ void wave_copy_periodic(uint8_t *dst, uint32_t off, uint32_t n,
-                                                   int lane) {
+// Periodic copy for offset < length: dst[j] = dst[j - off + (j mod off)]
+// relative to the match start; all sources precede the destination.
+__device__ __forceinline__ void wave_copy_periodic(uint8_t *dst, uint32_t off,
+                                                   uint32_t n, int lane) {
     const uint8_t *src = dst - off;
     uint32_t m = (uint32_t)lane % off;
     const uint32_t step = 64u % off;
@@ -126,10 +176,71 @@ __device__ __forceinline__ void wave_copy_periodic(uint8_t *dst, uint32_t off, u
     }
 }
 
+// 256-byte register window over the compressed stream.  Positions are
+// byte offsets from the input buffer start (no integer-to-pointer casts, so
+// every access stays a global-address-space access).
+struct Window {
+    const uint8_t *__restrict__ g;  // input buffer
+    uint64_t gsz;                   // its size
+    uint64_t wb;                    // 4-aligned window base (offset into g)
+    uint32_t w;                     // this lane's dword of the window
+    int lane;
+
+    __device__ __forceinline__ void load_at(uint64_t a) {
+        wb = a & ~(uint64_t)3;
+        w = ld_dw_clamped(g + wb + 4 * lane, g, g + gsz);
+    }
+    __device__ __forceinline__ uint32_t byte(uint64_t a) {
+        if (a < wb || a >= wb + 256) load_at(a);
+        const uint32_t d = (uint32_t)(a - wb);
+        return (__builtin_amdgcn_readlane(w, d >> 2) >> ((d & 3u) * 8u)) & 0xffu;
+    }
+    // Length extension starting at offset *pp (block.rs:277-289, 329-341):
+    // adds 255 per 0xFF byte plus the first other byte.  Returns false at end
+    // of input (the reference then reports UnexpectedEof at the input end).
+    __device__ __forceinline__ bool extension(uint64_t &pp, uint64_t end, uint64_t &len) {
+        uint64_t p = pp;
+        for (;;) {
+            if (p >= end) {
+                pp = end;
+                return false;
+            }
+            if (p < wb || p >= wb + 256) load_at(p);
+            // terminator: first byte q >= p with (q >= end || byte != 255)
+            const uint64_t q0 = wb + 4 * lane;
+            uint32_t tmask = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint64_t q = q0 + b;
+                const bool t = q >= p && (q >= end || ((w >> (8 * b)) & 0xffu) != 255u);
+                tmask |= (uint32_t)t << b;
+            }
+            const uint64_t ball = __ballot(tmask != 0);
+            if (ball) {
+                const int tl = __ffsll((unsigned long long)ball) - 1;
+                const uint32_t tm = __builtin_amdgcn_readlane(tmask, tl);
+                const uint32_t tb = (uint32_t)(__ffs(tm) - 1);
+                const uint64_t t = wb + 4 * (uint64_t)tl + tb;
+                len += 255ull * (t - p);
+                if (t >= end) {
+                    pp = end;
+                    return false;
+                }
+                len += (__builtin_amdgcn_readlane(w, tl) >> (8 * tb)) & 0xffu;
+                pp = t + 1;
+                return true;
+            }
+            len += 255ull * (wb + 256 - p);
+            p = wb + 256;
+        }
+    }
+};
+
 __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
     const uint8_t *__restrict__ d_in, uint64_t in_total, const uint64_t *__restrict__ in_off,
-    const uint32_t *__restrict__ in_len, uint8_t *d_out, const uint64_t *__restrict__ out_off,
-    const uint32_t *__restrict__ out_cap, uint32_t nblocks, hh_block_status *__restrict__ status) {
+    const uint32_t *__restrict__ in_len, uint8_t *__restrict__ d_out,
+    const uint64_t *__restrict__ out_off, const uint32_t *__restrict__ out_cap, uint32_t nblocks,
+    hh_block_status *__restrict__ status) {
     const int lane = threadIdx.x & 63;
     const uint32_t b = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (b >= nblocks) return;
@@ -146,43 +257,28 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
     if (ioff > in_total || (uint64_t)ilen > in_total - ioff) {
         code = HH_ERR_INVALID_ARGUMENT;
     } else {
-        const uintptr_t glo = (uintptr_t)d_in, ghi = glo + in_total;
-        const uintptr_t ilo = glo + ioff;
-        const uintptr_t olo = (uintptr_t)out, ohi = olo + cap;
+        const uint8_t *__restrict__ glo = d_in;
+        const uint8_t *__restrict__ ghi = d_in + in_total;
+        const uint64_t end = ioff + ilen;  // offsets into d_in
+        Window win;
+        win.g = d_in;
+        win.gsz = in_total;
+        win.lane = lane;
+        win.load_at(ioff);
 
-        uintptr_t wb = ilo & ~(uintptr_t)3;
-        uint32_t w = ld_dw(wb + 4u * lane, glo, ghi);
-        auto byte_at = [&](uint32_t p) -> uint32_t {
-            const uintptr_t a = ilo + p;
-            if (a < wb || a >= wb + 256) {
-                wb = a & ~(uintptr_t)3;
-                w = ld_dw(wb + 4u * lane, glo, ghi);
-            }
-            const uint32_t d = (uint32_t)(a - wb);
-            return (__builtin_amdgcn_readlane(w, d >> 2) >> ((d & 3u) * 8u)) & 0xffu;
-        };
-
-        uint32_t ip = 0;
-        while (ip < ilen) {
-            const uint32_t token = byte_at(ip++);
+        uint64_t ip = ioff;
+        while (ip < end) {
+            const uint32_t token = win.byte(ip++);
             uint64_t ll = token >> 4;
-            if (ll == 15) {
-                for (;;) {
-                    if (ip >= ilen) {
-                        code = HH_ERR_UNEXPECTED_EOF;
-                        pos = ip;
-                        break;
-                    }
-                    const uint32_t x = byte_at(ip++);
-                    ll += x;
-                    if (x != 255) break;
-                }
-                if (code != HH_OK) break;
+            if (ll == 15 && !win.extension(ip, end, ll)) {
+                code = HH_ERR_UNEXPECTED_EOF;
+                pos = ilen;
+                break;
             }
             if (ll > 0) {
-                if ((uint64_t)ip + ll > ilen) {
+                if (end - ip < ll) {
                     code = HH_ERR_UNEXPECTED_EOF;
-                    pos = ip;
+                    pos = ip - ioff;
                     break;
                 }
                 if ((uint64_t)op + ll > cap) {
@@ -190,21 +286,18 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
                     req = (uint64_t)op + ll;
                     break;
                 }
-                // prefetch the window that holds the next offset/token
-                const uintptr_t na = ilo + ip + ll;
-                wb = na & ~(uintptr_t)3;
-                w = ld_dw(wb + 4u * lane, glo, ghi);
-                wave_copy(out + op, ilo + ip, (uint32_t)ll, glo, ghi, lane);
-                ip += (uint32_t)ll;
+                win.load_at(ip + ll);  // prefetch the next offset/token window
+                wave_copy(out + op, d_in + ip, (uint32_t)ll, glo, ghi, lane);
+                ip += ll;
                 op += (uint32_t)ll;
             }
             if (op >= cap) break;  // block.rs:309-311
-            if ((uint64_t)ip + 2 > ilen) {
+            if (end - ip < 2) {
                 code = HH_ERR_UNEXPECTED_EOF;
-                pos = ip;
+                pos = ip - ioff;
                 break;
             }
-            const uint32_t off = byte_at(ip) | (byte_at(ip + 1) << 8);
+            const uint32_t off = win.byte(ip) | (win.byte(ip + 1) << 8);
             ip += 2;
             if (off == 0) {
                 code = HH_ERR_CORRUPTED_DATA;
@@ -218,18 +311,10 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
                 break;
             }
             uint64_t ml = (token & 15u) + 4u;
-            if ((token & 15u) == 15u) {
-                for (;;) {
-                    if (ip >= ilen) {
-                        code = HH_ERR_UNEXPECTED_EOF;
-                        pos = ip;
-                        break;
-                    }
-                    const uint32_t x = byte_at(ip++);
-                    ml += x;
-                    if (x != 255) break;
-                }
-                if (code != HH_OK) break;
+            if ((token & 15u) == 15u && !win.extension(ip, end, ml)) {
+                code = HH_ERR_UNEXPECTED_EOF;
+                pos = ilen;
+                break;
             }
             if ((uint64_t)op + ml > cap) {
                 code = HH_ERR_BUFFER_TOO_SMALL;
@@ -238,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
             }
             wave_fence();
             if (off >= ml)
-                wave_copy(out + op, olo + op - off, (uint32_t)ml, olo, ohi, lane);
+                wave_copy(out + op, out + op - off, (uint32_t)ml, out, out + cap, lane);
             else
                 wave_copy_periodic(out + op, off, (uint32_t)ml, lane);
             wave_fence();
