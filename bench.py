@@ -5,7 +5,9 @@ Workload: the weight set of a Llama-3-8B decoder layer -- q,o 4096x4096;
 k,v 1024x4096; gate,up 14336x4096; down 4096x14336 (218,103,808 elements),
 values N(0, 0.02), seeded -- stored as HCT-T: 64x64 tiles, top 30% of each
 tile's DCT coefficients (k = 1228) as a bitmap + INT4 with f16 scales,
-LZ4-compressed in blocks of 54 whole tiles (65,016 bytes).  One step decodes
+LZ4-compressed in blocks of 13 whole tiles (15,652 bytes: the reference
+HctWriter's default block size, 16 KiB, rounded down to whole tiles;
+crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes
 32 such layers back to back into bf16 tensors: per layer one batched LZ4
 launch (compressed -> tile bytes) and one batched tile launch (dequant +
 scatter + inverse DCT on MFMA -> bf16).  Inputs are resident in HBM before
@@ -100,6 +102,9 @@ def main():
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--lz4-block", type=int, default=16384,
+                    help="LZ4 block size in bytes before rounding down to whole tiles "
+                         "(the reference HctWriter default is 16 KiB)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build "
@@ -113,7 +118,7 @@ def main():
     torch.cuda.set_device(0)
     k = H.hctt_retain_count(RHO)
     tb = H.hctt_tile_bytes(k)
-    tiles_per_block = 65536 // tb
+    tiles_per_block = max(1, args.lz4_block // tb)
     n_elem = sum(r * c for _, r, c in SHAPES)
     out_bytes_layer = n_elem * 2
 
