@@ -53,28 +53,30 @@ int32_t ensure_scratch(hh_context *ctx, size_t bytes) {
 namespace hh {
 
 // MFMA fragments of M' = 256 * M, M[v][j] = a_v cos(pi v (2j+1) / 128),
-// split into f16 hi + lo.  Entry ((hl*2 + jb)*4 + s)*64 + lane holds the 8
-// values M'[pi(16s + 8h + e)][32 jb + lane%32] for e = 0..7, h = lane/32,
+// split into f16 hi + lo, for the even/odd halves of the frequencies.
+// Entry ((hl*2 + par)*2 + s)*64 + lane holds the 8 values
+// M'[2 pi(16s + 8h + e) + par][lane%32] for e = 0..7, h = lane/32,
 // pi(16s + 8h + e) = 16s + 8(e/4) + 4h + e%4 (the accumulator row order of
-// v_mfma_f32_32x32x16_f16).
-size_t basis_table_bytes() { return 2 * 2 * 4 * 64 * 8 * sizeof(_Float16); }
+// v_mfma_f32_32x32x16_f16).  Only j < 32 is tabulated: the other half
+// follows from M[v][63 - j] = (-1)^v M[v][j].
+size_t basis_table_bytes() { return 2 * 2 * 2 * 64 * 8 * sizeof(_Float16); }
 
 void build_basis_table(void *buf) {
     _Float16 *t = reinterpret_cast<_Float16 *>(buf);
     const double pi = 3.14159265358979323846;
     for (int hl = 0; hl < 2; hl++)
-        for (int jb = 0; jb < 2; jb++)
-            for (int s = 0; s < 4; s++)
+        for (int par = 0; par < 2; par++)
+            for (int s = 0; s < 2; s++)
                 for (int lane = 0; lane < 64; lane++)
                     for (int e = 0; e < 8; e++) {
                         const int h = lane >> 5;
-                        const int v = 16 * s + 8 * (e >> 2) + 4 * h + (e & 3);
-                        const int j = 32 * jb + (lane & 31);
+                        const int v = 2 * (16 * s + 8 * (e >> 2) + 4 * h + (e & 3)) + par;
+                        const int j = lane & 31;
                         const double a = v == 0 ? std::sqrt(1.0 / 64) : std::sqrt(2.0 / 64);
                         const double m = 256.0 * a * std::cos(pi * v * (2 * j + 1) / 128.0);
                         const _Float16 hi = (_Float16)m;
                         const _Float16 lo = (_Float16)(m - (double)hi);
-                        t[((((hl * 2 + jb) * 4 + s) * 64 + lane) * 8) + e] = hl == 0 ? hi : lo;
+                        t[((((hl * 2 + par) * 2 + s) * 64 + lane) * 8) + e] = hl == 0 ? hi : lo;
                     }
 }
 

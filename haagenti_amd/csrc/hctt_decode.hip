@@ -59,7 +59,7 @@ typedef const u32x4 HH_GLOBAL g_u32x4;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr uint32_t kMTabBytes = 2 * 2 * 4 * 64 * 16;  // [hl][block][kstep][lane] x 16 B
+constexpr uint32_t kMTabBytes = 2 * 2 * 2 * 64 * 16;  // [hl][parity][kstep][lane] x 16 B
 constexpr uint32_t kZeroBytes = 16;
 
 __device__ __forceinline__ void wave_sync() {
@@ -262,109 +262,131 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         }
         wave_sync();
 
-        // 4. GEMM1 A fragments: rows u = 32 ub + l32, columns pi(16 s + 8 h + e)
-        const uint64_t bits_r[2] = {__shfl(bits, l32), __shfl(bits, l32 + 32)};
-        const uint32_t pre_r[2] = {__shfl(pre, l32), __shfl(pre, l32 + 32)};
-        u32x4 ahi[2][4], alo[2][4];
+        // 4. GEMM1 A fragments.  A[upar][vpar][s] holds, for row
+        //    u = 2 l32 + upar, the columns v = 2 pi(16 s + 8 h + e) + vpar,
+        //    e = 0..7.  For fixed (upar, s) these are two runs of 8
+        //    consecutive columns, v0 = 32 s + 16 run + 8 h: even offsets feed
+        //    vpar 0, odd offsets vpar 1.
+        const uint64_t bits_r[2] = {__shfl(bits, 2 * l32), __shfl(bits, 2 * l32 + 1)};
+        const uint32_t pre_r[2] = {__shfl(pre, 2 * l32), __shfl(pre, 2 * l32 + 1)};
+        u32x4 ahi[2][2][2], alo[2][2][2];  // [upar][vpar][s]
 #pragma unroll
-        for (int ub = 0; ub < 2; ub++) {
-            const uint64_t b64 = ok ? bits_r[ub] : 0ull;
+        for (int up = 0; up < 2; up++) {
+            const uint64_t b64 = ok ? bits_r[up] : 0ull;
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                uint32_t w[8];
+            for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int run = 0; run < 2; run++) {
-                    const int v0 = 16 * s + 8 * run + 4 * h;
-                    uint32_t rank = pre_r[ub] + (uint32_t)__popcll(b64 & ((1ull << v0) - 1ull));
+                    const int v0 = 32 * s + 16 * run + 8 * h;
+                    uint32_t rank = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << v0) - 1ull));
+                    uint32_t w[8];
 #pragma unroll
-                    for (int e4 = 0; e4 < 4; e4++) {
-                        const uint32_t bit = (uint32_t)(b64 >> (v0 + e4)) & 1u;
+                    for (int o = 0; o < 8; o++) {
+                        const uint32_t bit = (uint32_t)(b64 >> (v0 + o)) & 1u;
                         const uint32_t addr = bit ? wbase + 4 * rank : kZeroOff;
-                        w[4 * run + e4] = *reinterpret_cast<const uint32_t *>(smem + addr);
+                        w[o] = *reinterpret_cast<const uint32_t *>(smem + addr);
                         rank += bit;
                     }
-                }
+                    // dword p of a fragment packs elements e = 2p, 2p + 1;
+                    // this run supplies e = 4 run .. 4 run + 3
 #pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    ahi[ub][s][p] = __builtin_amdgcn_perm(w[2 * p + 1], w[2 * p], 0x05040100u);
-                    alo[ub][s][p] = __builtin_amdgcn_perm(w[2 * p + 1], w[2 * p], 0x07060302u);
+                    for (int vp = 0; vp < 2; vp++) {
+                        ahi[up][vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
+                        alo[up][vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
+                        ahi[up][vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
+                        alo[up][vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
+                    }
                 }
             }
         }
         wave_sync();
 
-        // 5-7. per 32-column output block jb: GEMM1, GEMM2, park in LDS
-        const float s_down = 1.0f / 256.0f;
-        const float os = pow2f(-(E + 8));
-#pragma unroll 1
-        for (int jb = 0; jb < 2; jb++) {
-            floatx16 acc[2];
-            acc[0] = floatx16{};
-            acc[1] = floatx16{};
+        // 5. GEMM1 (even/odd halves of the column frequencies):
+        //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
+        //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
+        floatx16 acc[2][2];
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const u32x4 mh = mtab[((0 * 2 + jb) * 4 + s) * 64 + lane];
-                const u32x4 ml = mtab[((1 * 2 + jb) * 4 + s) * 64 + lane];
+        for (int up = 0; up < 2; up++)
 #pragma unroll
-                for (int ub = 0; ub < 2; ub++) {
-                    acc[ub] = mfma(ahi[ub][s], mh, acc[ub]);
-                    acc[ub] = mfma(ahi[ub][s], ml, acc[ub]);
-                    acc[ub] = mfma(alo[ub][s], mh, acc[ub]);
+            for (int vp = 0; vp < 2; vp++) acc[up][vp] = floatx16{};
+#pragma unroll
+        for (int vp = 0; vp < 2; vp++) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
+                const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
+#pragma unroll
+                for (int up = 0; up < 2; up++) {
+                    acc[up][vp] = mfma(ahi[up][vp][s], mh, acc[up][vp]);
+                    acc[up][vp] = mfma(ahi[up][vp][s], ml, acc[up][vp]);
+                    acc[up][vp] = mfma(alo[up][vp][s], mh, acc[up][vp]);
                 }
             }
-            floatx16 xacc[2];
-            xacc[0] = floatx16{};
-            xacc[1] = floatx16{};
+        }
+
+        // 6-7. per output column block jb (jb = 0: j = n; jb = 1: j = 63 - n):
+        //    B = S rows of parity upar; GEMM2 X[i][j] = sum_u M[u][i] S[u][j]
+        //    split by u parity into E2 (upar 0) and O2 (upar 1); then
+        //    X[i][j] = E2 + O2, X[63 - i][j] = E2 - O2; park in LDS.
+        const float s_down = 1.0f / 256.0f;
+        const float os = pow2f(-(E + 8));
 #pragma unroll
-            for (int ub = 0; ub < 2; ub++) {
+        for (int jb = 0; jb < 2; jb++) {
+            const float sg = jb == 0 ? s_down : -s_down;
+            floatx16 x2[2];
+            x2[0] = floatx16{};
+            x2[1] = floatx16{};
 #pragma unroll
-                for (int t2 = 0; t2 < 2; t2++) {
-                    const int sk = 2 * ub + t2;
+            for (int up = 0; up < 2; up++) {
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
                     u32x4 bhi, blo;
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
+                        const int r0 = 8 * s + 2 * p, r1 = r0 + 1;
                         uint32_t hp, lp;
-                        split2(acc[ub][8 * t2 + 2 * p] * s_down, acc[ub][8 * t2 + 2 * p + 1] * s_down,
-                               hp, lp);
+                        split2(acc[up][0][r0] * s_down + acc[up][1][r0] * sg,
+                               acc[up][0][r1] * s_down + acc[up][1][r1] * sg, hp, lp);
                         bhi[p] = hp;
                         blo[p] = lp;
                     }
-#pragma unroll
-                    for (int ib = 0; ib < 2; ib++) {
-                        const u32x4 mh = mtab[((0 * 2 + ib) * 4 + sk) * 64 + lane];
-                        const u32x4 ml = mtab[((1 * 2 + ib) * 4 + sk) * 64 + lane];
-                        xacc[ib] = mfma(mh, bhi, xacc[ib]);
-                        xacc[ib] = mfma(ml, bhi, xacc[ib]);
-                        xacc[ib] = mfma(mh, blo, xacc[ib]);
-                    }
+                    const u32x4 mh = mtab[((0 * 2 + up) * 2 + s) * 64 + lane];
+                    const u32x4 ml = mtab[((1 * 2 + up) * 2 + s) * 64 + lane];
+                    x2[up] = mfma(mh, bhi, x2[up]);
+                    x2[up] = mfma(ml, bhi, x2[up]);
+                    x2[up] = mfma(mh, blo, x2[up]);
                 }
             }
-            // park rows i = 32 ib + (r&3) + 8 (r>>2) + 4 h, column 32 jb + l32
+            // park rows i = (r&3) + 8 (r>>2) + 4 h and 63 - i, column j
+            const int j = jb == 0 ? l32 : 63 - l32;
             if constexpr (DT == HH_F32) {
                 float *xs = reinterpret_cast<float *>(smem + wbase);
 #pragma unroll
-                for (int ib = 0; ib < 2; ib++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        xs[(32 * ib + (r & 3) + 8 * (r >> 2) + 4 * h) * 64 + 32 * jb + l32] =
-                            xacc[ib][r] * os;
+                for (int r = 0; r < 16; r++) {
+                    const int i = (r & 3) + 8 * (r >> 2) + 4 * h;
+                    xs[i * 64 + j] = (x2[0][r] + x2[1][r]) * os;
+                    xs[(63 - i) * 64 + j] = (x2[0][r] - x2[1][r]) * os;
+                }
             } else {
                 uint16_t *xs = reinterpret_cast<uint16_t *>(smem + wbase);
 #pragma unroll
-                for (int ib = 0; ib < 2; ib++)
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2) {
-                        const float a = xacc[ib][r] * os, b = xacc[ib][r + 1] * os;
-                        uint32_t pk;
-                        if constexpr (DT == HH_BF16) {
-                            pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
-                        } else {
-                            pk = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
-                        }
-                        const int i0 = 32 * ib + (r & 3) + 8 * (r >> 2) + 4 * h;
-                        xs[i0 * 64 + 32 * jb + l32] = (uint16_t)pk;
-                        xs[(i0 + 1) * 64 + 32 * jb + l32] = (uint16_t)(pk >> 16);
+                for (int r = 0; r < 16; r += 2) {
+                    const float a = (x2[0][r] + x2[1][r]) * os, b = (x2[0][r + 1] + x2[1][r + 1]) * os;
+                    const float c = (x2[0][r] - x2[1][r]) * os, d = (x2[0][r + 1] - x2[1][r + 1]) * os;
+                    uint32_t pk, pm;
+                    if constexpr (DT == HH_BF16) {
+                        pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
+                        pm = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{c, d}, bf16x2));
+                    } else {
+                        pk = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+                        pm = f32_to_f16_bits(c) | (f32_to_f16_bits(d) << 16);
                     }
+                    const int i0 = (r & 3) + 8 * (r >> 2) + 4 * h;  // rows i0, i0 + 1
+                    xs[i0 * 64 + j] = (uint16_t)pk;
+                    xs[(i0 + 1) * 64 + j] = (uint16_t)(pk >> 16);
+                    xs[(63 - i0) * 64 + j] = (uint16_t)pm;
+                    xs[(62 - i0) * 64 + j] = (uint16_t)(pm >> 16);
+                }
             }
         }
         wave_sync();
