@@ -88,11 +88,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 
 // (a, b) -> f16 hi pair and f16 lo pair with a = hi.x + lo.x, b = hi.y + lo.y
 // to ~2^-20 relative (exactly when a, b have at most 21 significant bits).
+// The lo halves come from mixed-precision FMAs that read the f16 hi halves
+// in place: lo = round_f16(a * 1 - hi), computed exactly in f32 first.
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(a, b);
-    const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(a - (float)h.x, b - (float)h.y);
-    hi = __builtin_bit_cast(uint32_t, h);
-    lo = __builtin_bit_cast(uint32_t, l);
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+    uint32_t l = 0;
+    __asm__("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]\n\t"
+            "v_fma_mixhi_f16 %0, %3, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+            : "+&v"(l)
+            : "v"(a), "v"(hi), "v"(b));
+    lo = l;
 }
 
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
@@ -273,20 +278,30 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
 #pragma unroll
         for (int up = 0; up < 2; up++) {
             const uint64_t b64 = ok ? bits_r[up] : 0ull;
+            // the row shifted so that column 8 h is bit 0: every column this
+            // lane needs sits at a compile-time bit position
+            const uint64_t bh = b64 >> (8 * h);
+            const uint32_t wd[2] = {(uint32_t)bh, (uint32_t)(bh >> 32)};
+            const uint32_t rank_h = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << (8 * h)) - 1ull));
+            // LDS byte address of V[rank] minus the zero word's address; a
+            // column that is not retained selects the zero word (bit * diff = 0)
+            uint32_t diff = wbase + 4 * rank_h - kZeroOff;
 #pragma unroll
             for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int run = 0; run < 2; run++) {
-                    const int v0 = 32 * s + 16 * run + 8 * h;
-                    uint32_t rank = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << v0) - 1ull));
+                    const uint32_t word = wd[s];
                     uint32_t w[8];
 #pragma unroll
                     for (int o = 0; o < 8; o++) {
-                        const uint32_t bit = (uint32_t)(b64 >> (v0 + o)) & 1u;
-                        const uint32_t addr = bit ? wbase + 4 * rank : kZeroOff;
-                        w[o] = *reinterpret_cast<const uint32_t *>(smem + addr);
-                        rank += bit;
+                        // all-ones when column 16 run + o of the word is retained
+                        const int32_t m = (int32_t)(word << (31 - (16 * run + o))) >> 31;
+                        w[o] = *reinterpret_cast<const uint32_t *>(smem + kZeroOff + ((uint32_t)m & diff));
+                        diff += (uint32_t)(m * -4);
                     }
+                    // columns 16 run + 8 .. 16 run + 15 of this word belong to the
+                    // other lane half
+                    diff += (uint32_t)__popc((word >> (16 * run + 8)) & 0xffu) << 2;
                     // dword p of a fragment packs elements e = 2p, 2p + 1;
                     // this run supplies e = 4 run .. 4 run + 3
 #pragma unroll
@@ -364,22 +379,29 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int i = (r & 3) + 8 * (r >> 2) + 4 * h;
-                    xs[i * 64 + j] = (x2[0][r] + x2[1][r]) * os;
-                    xs[(63 - i) * 64 + j] = (x2[0][r] - x2[1][r]) * os;
+                    const float o2 = x2[1][r] * os;
+                    xs[i * 64 + j] = __builtin_fmaf(x2[0][r], os, o2);
+                    xs[(63 - i) * 64 + j] = __builtin_fmaf(x2[0][r], os, -o2);
                 }
             } else {
                 uint16_t *xs = reinterpret_cast<uint16_t *>(smem + wbase);
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
-                    const float a = (x2[0][r] + x2[1][r]) * os, b = (x2[0][r + 1] + x2[1][r + 1]) * os;
-                    const float c = (x2[0][r] - x2[1][r]) * os, d = (x2[0][r + 1] - x2[1][r + 1]) * os;
+                    const float o0 = x2[1][r] * os, o1 = x2[1][r + 1] * os;
+                    const float a = __builtin_fmaf(x2[0][r], os, o0), b = __builtin_fmaf(x2[0][r + 1], os, o1);
+                    const float c = __builtin_fmaf(x2[0][r], os, -o0), d = __builtin_fmaf(x2[0][r + 1], os, -o1);
                     uint32_t pk, pm;
                     if constexpr (DT == HH_BF16) {
                         pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
                         pm = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{c, d}, bf16x2));
                     } else {
-                        pk = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
-                        pm = f32_to_f16_bits(c) | (f32_to_f16_bits(d) << 16);
+                        // keep the f32 values as such: a fused fma -> f16
+                        // (v_fma_mix) would round once from the exact result,
+                        // not from the f32 output
+                        float fa = a, fb = b, fc = c, fd = d;
+                        __asm__("" : "+v"(fa), "+v"(fb), "+v"(fc), "+v"(fd));
+                        pk = f32_to_f16_bits(fa) | (f32_to_f16_bits(fb) << 16);
+                        pm = f32_to_f16_bits(fc) | (f32_to_f16_bits(fd) << 16);
                     }
                     const int i0 = (r & 3) + 8 * (r >> 2) + 4 * h;  // rows i0, i0 + 1
                     xs[i0 * 64 + j] = (uint16_t)pk;
