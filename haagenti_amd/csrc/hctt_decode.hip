@@ -19,12 +19,14 @@
 // fragments without any shuffle or LDS trip, and one table of M fragments
 // serves as GEMM1's B and GEMM2's A.
 //
-// Precision.  Operands are split into f16 hi + lo (exact for the
-// coefficients, ~2^-20 relative for M and S) and each GEMM runs three passes
-// hi*hi + hi*lo + lo*hi with f32 accumulation (max-abs error ~1e-6 x RMS; the
-// bar is 1e-3 x RMS).  Coefficients are prescaled by 2^E per tile (E from
-// the largest f16 scale exponent) and M by 2^8 so that the lo parts stay in
-// f16's normal range; the output is rescaled exactly.
+// Precision.  Operands are split into f16 hi + lo (~2^-20 relative for the
+// coefficients, M and S) and each GEMM runs three passes hi*hi + hi*lo +
+// lo*hi with f32 accumulation (max-abs error ~1e-6 x RMS; the bar is
+// 1e-3 x RMS).  Coefficients are prescaled by 2^E per tile (E from the
+// largest f16 scale exponent, so that |C 2^E| < 4) and M by 2^8, which puts
+// GEMM1's output directly in the range of GEMM2's f16 operands; only lo
+// parts of coefficients below ~2^-10 of the tile maximum lose bits to f16
+// subnormals (2^-25 absolute).  The output is rescaled exactly.
 //
 // Data flow per tile (per wave):
 //   1. each lane reads one 64-bit bitmap row; a wave prefix sum gives every
@@ -235,11 +237,12 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
             emax = ex > emax ? ex : emax;
         }
         emax = wave_max_u32(emax);
-        const int E = 21 - (int)emax;
+        // coefficients are scaled by 2^E (|C 2^E| < 4); the basis carries 2^8
+        const int E = 13 - (int)emax;
         const float pe = pow2f(E);
 
         // 3. dense table of the retained coefficients, 4 per lane per pass:
-        //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E exactly
+        //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E
         if (ok) {
             const uint16_t *nib16 = reinterpret_cast<const uint16_t *>(pay + nib_off);
             for (uint32_t g4 = lane; 4 * g4 < k; g4 += 64) {
@@ -343,11 +346,9 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         //    B = S rows of parity upar; GEMM2 X[i][j] = sum_u M[u][i] S[u][j]
         //    split by u parity into E2 (upar 0) and O2 (upar 1); then
         //    X[i][j] = E2 + O2, X[63 - i][j] = E2 - O2; park in LDS.
-        const float s_down = 1.0f / 256.0f;
-        const float os = pow2f(-(E + 8));
+        const float os = pow2f(-(E + 16));
 #pragma unroll
         for (int jb = 0; jb < 2; jb++) {
-            const float sg = jb == 0 ? s_down : -s_down;
             floatx16 x2[2];
             x2[0] = floatx16{};
             x2[1] = floatx16{};
@@ -360,8 +361,10 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
                     for (int p = 0; p < 4; p++) {
                         const int r0 = 8 * s + 2 * p, r1 = r0 + 1;
                         uint32_t hp, lp;
-                        split2(acc[up][0][r0] * s_down + acc[up][1][r0] * sg,
-                               acc[up][0][r1] * s_down + acc[up][1][r1] * sg, hp, lp);
+                        if (jb == 0)
+                            split2(acc[up][0][r0] + acc[up][1][r0], acc[up][0][r1] + acc[up][1][r1], hp, lp);
+                        else
+                            split2(acc[up][0][r0] - acc[up][1][r0], acc[up][0][r1] - acc[up][1][r1], hp, lp);
                         bhi[p] = hp;
                         blo[p] = lp;
                     }
