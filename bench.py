@@ -1,20 +1,39 @@
 #!/usr/bin/env python3
 """HCT decode throughput on one MI355X: decoded weight output GB/s.
 
-Workload: the weight set of a Llama-3-8B decoder layer -- q,o 4096x4096;
-k,v 1024x4096; gate,up 14336x4096; down 4096x14336 (218,103,808 elements),
-values N(0, 0.02), seeded -- stored as HCT-T: 64x64 tiles, top 30% of each
-tile's DCT coefficients (k = 1228) as a bitmap + INT4 with f16 scales,
-LZ4-compressed in blocks of 13 whole tiles (15,652 bytes: the reference
-HctWriter's default block size, 16 KiB, rounded down to whole tiles;
-crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes
-32 such layers back to back into bf16 tensors: per layer one batched LZ4
-launch (compressed -> tile bytes) and one batched tile launch (dequant +
-scatter + inverse DCT on MFMA -> bf16).  Inputs are resident in HBM before
-timing starts.  Synthetic data: a few distinct layers are encoded on the host
-and replicated into 32 separate device buffers.
+Default workload (--workload llama3-8b-layer): the weight set of a
+Llama-3-8B decoder layer -- q,o 4096x4096; k,v 1024x4096; gate,up
+14336x4096; down 4096x14336 (218,103,808 elements), values N(0, 0.02),
+seeded -- stored as HCT-T: 64x64 tiles, top 30% of each tile's DCT
+coefficients (k = 1228) as a bitmap + INT4 with f16 scales, LZ4-compressed
+in blocks of 13 whole tiles (15,652 bytes: the reference HctWriter's default
+block size, 16 KiB, rounded down to whole tiles;
+crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes 32 such layers
+back to back into bf16 tensors: per layer one batched LZ4 launch (compressed
+-> tile bytes) and one batched tile launch (dequant + scatter + inverse DCT
+on MFMA -> bf16).  Inputs are resident in HBM before timing starts.
 
-Prints one JSON line (see the roofline / cpu_baseline fields).
+Other workloads (one JSON line each, same contract):
+  int4-4096        4096x4096 f32 N(0, 0.02) through quantize_int4 (block 32,
+                   truncated f16 scales); GPU dequant to f32, bit-exact mode
+  lz4-256mib       4096 independent 64 KiB blocks (256 MiB out), each packed
+                   INT4 nibbles of N(0, 0.02) weights or the same with half of
+                   the 256-byte spans zeroed, seeded coin per block
+  idct-8192        one 8192x8192 tensor as HCT-T at 25% retention (k = 1024),
+                   dequant + scatter + tile inverse DCT to bf16
+  llama70b-stream  80 Llama-70B-shaped layers (q,o 8192^2; k,v 1024x8192;
+                   gate,up,down 28672x8192 / 8192x28672), per-tensor retention
+                   U[0.10, 0.50]; compressed layers in pinned host memory,
+                   H2D copies on a copy stream overlapped with decode into a
+                   double-buffered bf16 layer slot
+  hbm-copy         a plain 1 GiB device copy: the HBM reference rate and the
+                   calibration for the FETCH_SIZE / WRITE_SIZE counters
+
+Synthetic data throughout (no network): a few distinct encodings are made on
+the host and replicated or cycled.  `roofline.traffic` is read from
+profiles/traffic.json (HBM bytes per launch of the dominant kernel, from
+rocprofv3 FETCH_SIZE and WRITE_SIZE runs scaled by the copy calibration) when
+that file holds the workload, else null.
 """
 import argparse
 import json
@@ -29,68 +48,585 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decoded weight output GB/s on 1 MI355X + % of HBM peak; vs host-CPU ref"
 HBM_PEAK_GBS = 8000.0
-SHAPES = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
-          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
-RHO = 0.3
+L8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+       ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+L70B = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
+        ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672)]
+RHO_8B = 0.3
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def encode_layer(H, seed, k, tb, tiles_per_block):
-    """Host producer: HCT-T tiles + LZ4 blocks for the 7 tensors of a layer."""
-    rng = np.random.default_rng(seed)
-    comp_parts, in_off, in_len, out_off, out_cap = [], [], [], [], []
-    tensors = []          # (name, rows, cols, scratch_offset, tiles_len)
-    pos = spos = 0
+def cpu_threads():
+    return os.cpu_count() or 1
+
+
+def oracle():
+    """The CPU oracle (test infrastructure) used only for the cpu_baseline leg
+    and the spot check; None when its library is not built."""
+    try:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as O
+        O.lib()
+        return O
+    except Exception as ex:  # the GPU timing does not depend on it
+        log(f"oracle unavailable: {ex}")
+        return None
+
+
+def traffic_for(workload):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f).get(workload)
+        return None if t is None else t["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def roofline(workload, kernel, algo_bytes, avg_s, extra=None):
+    achieved = algo_bytes / avg_s / 1e9
+    r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(workload),
+         "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
+         "algorithmic_bytes_per_launch": int(algo_bytes)}
+    if extra:
+        r.update(extra)
+    return r
+
+
+def line(workload, value, ms_step, args, dtype, data, config, roof, cpu, extra=None):
+    d = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+         "data": data, "config": dict(workload=workload, **config), "roofline": roof,
+         "cpu_baseline": cpu}
+    if extra:
+        d.update(extra)
+    return d
+
+
+class Timed:
+    """HIP events on one stream around a region (torch.cuda.Event records on
+    the stream it is given, which is the stream the kernels are launched on)."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+        self.pairs = []
+
+    def start(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record(self.stream)
+        return e
+
+    def stop(self, e0):
+        e1 = self.torch.cuda.Event(enable_timing=True)
+        e1.record(self.stream)
+        self.pairs.append((e0, e1))
+
+    def mean_s(self):
+        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) / 1e3
+
+
+def devtab(torch, a):
+    a = np.ascontiguousarray(a)
+    view = np.int64 if a.dtype == np.uint64 else np.int32
+    return torch.from_numpy(a.view(view).copy()).cuda()
+
+
+# ---------------------------------------------------------------- producers
+def encode_tensor_lz4(H, w, k, tiles_per_block):
+    """HCT-T tiles of w, cut into LZ4 blocks of whole tiles (host producer)."""
+    tb = H.hctt_tile_bytes(k)
+    tiles = H.hctt_encode(w, k)
     comp = H.Lz4Compressor()
-    for name, rows, cols in SHAPES:
+    blk = tiles_per_block * tb
+    parts, lens, outs, caps = [], [], [], []
+    for s in range(0, tiles.size, blk):
+        chunk = tiles[s:s + blk]
+        c = comp.compress(chunk.tobytes())
+        parts.append(c)
+        lens.append(len(c))
+        outs.append(s)
+        caps.append(chunk.size)
+    return tiles, parts, lens, outs, caps
+
+
+def encode_layer(H, shapes, ks, seed, block_bytes, keep_first=False):
+    """One layer: for each tensor its HCT-T tiles LZ4-compressed in blocks of
+    whole tiles; block tables index one concatenated blob and one scratch."""
+    rng = np.random.default_rng(seed)
+    parts, in_off, in_len, out_off, out_cap, tensors = [], [], [], [], [], []
+    pos = spos = 0
+    for (name, rows, cols), k in zip(shapes, ks):
         w = rng.normal(0.0, 0.02, (rows, cols)).astype(np.float32)
-        tiles = H.hctt_encode(w, k)
+        tb = H.hctt_tile_bytes(k)
+        tiles, p, lens, outs, caps = encode_tensor_lz4(H, w, k, max(1, block_bytes // tb))
         del w
-        blk = tiles_per_block * tb
-        for s in range(0, tiles.size, blk):
-            chunk = tiles[s:s + blk]
-            c = comp.compress(chunk.tobytes())
-            comp_parts.append(c)
+        for c, ln, o, cp in zip(p, lens, outs, caps):
+            parts.append(c)
             in_off.append(pos)
-            in_len.append(len(c))
-            out_off.append(spos + s)
-            out_cap.append(chunk.size)
-            pos += len(c)
-        tensors.append((name, rows, cols, spos, tiles.size, tiles if seed == 0 and name == "q" else None))
+            in_len.append(ln)
+            out_off.append(spos + o)
+            out_cap.append(cp)
+            pos += ln
+        tensors.append(dict(name=name, rows=rows, cols=cols, k=k, soff=spos, tlen=tiles.size,
+                            tiles=tiles if keep_first and not tensors else None))
         spos += tiles.size
-    blob = np.frombuffer(b"".join(comp_parts), np.uint8)
-    return dict(blob=blob, in_off=np.array(in_off, np.uint64), in_len=np.array(in_len, np.uint32),
-                out_off=np.array(out_off, np.uint64), out_cap=np.array(out_cap, np.uint32),
-                tensors=tensors, scratch_bytes=spos)
+    return dict(blob=np.frombuffer(b"".join(parts), np.uint8), in_off=np.array(in_off, np.uint64),
+                in_len=np.array(in_len, np.uint32), out_off=np.array(out_off, np.uint64),
+                out_cap=np.array(out_cap, np.uint32), tensors=tensors, scratch_bytes=spos)
 
 
-def cpu_baseline(O, layer, k, budget_s):
-    """Oracle (C restatement of the reference CPU decode) on the host cores:
-    LZ4 blocks -> tile bytes -> dequant + scatter + f32 IDCT, all threads."""
-    nthreads = os.cpu_count() or 1
-    n_elem = sum(r * c for _, r, c in SHAPES)
-    reps, t_total = 0, 0.0
+def cpu_layer_decode(O, layer, reps_budget_s, max_reps=20, tensor_subset=None):
+    """Oracle decode (LZ4 blocks -> tile bytes -> dequant + scatter + f32
+    Makhoul IDCT) on all host threads; returns (reps, seconds, elements)."""
+    nthreads = cpu_threads()
+    reps, t_total, n_elem = 0, 0.0, 0
+    tens = layer["tensors"] if tensor_subset is None else [layer["tensors"][i] for i in tensor_subset]
     while True:
         t0 = time.perf_counter()
         scratch, kinds, _ = O.lz4_decompress_batch(layer["blob"], layer["in_off"], layer["in_len"],
                                                    layer["out_off"], layer["out_cap"],
                                                    layer["scratch_bytes"], nthreads=nthreads)
         assert (kinds == 0).all()
-        for name, rows, cols, soff, tlen, _ in layer["tensors"]:
-            rc, _ = O.hctt_decode_tensor(scratch[soff:soff + tlen], rows, cols, k, nthreads=nthreads)
+        n_elem = 0
+        for T in tens:
+            rc, _ = O.hctt_decode_tensor(scratch[T["soff"]:T["soff"] + T["tlen"]], T["rows"],
+                                         T["cols"], T["k"], nthreads=nthreads)
             assert rc == O.OK
+            n_elem += T["rows"] * T["cols"]
         t_total += time.perf_counter() - t0
         reps += 1
-        if t_total >= budget_s or reps >= 20:
-            break
-    gbs = reps * n_elem * 2 / t_total / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": f"{reps} full Llama-3-8B layer decode(s) ({n_elem} elements each: LZ4 + "
-                      f"dequant + scatter + f32 Makhoul IDCT), {nthreads} threads, output counted "
-                      f"as bf16 bytes (2 B/element) like the GPU line; {t_total:.1f} s"}
+        if t_total >= reps_budget_s or reps >= max_reps:
+            return reps, t_total, n_elem
+
+
+# ---------------------------------------------------------------- workloads
+def wl_llama3_8b_layer(args, torch, H, O):
+    k = H.hctt_retain_count(RHO_8B)
+    tb = H.hctt_tile_bytes(k)
+    tiles_per_block = max(1, args.lz4_block // tb)
+    n_elem = sum(r * c for _, r, c in L8B)
+    out_bytes_layer = n_elem * 2
+
+    t0 = time.time()
+    layers_host = [encode_layer(H, L8B, [k] * len(L8B), d, tiles_per_block * tb, keep_first=d == 0)
+                   for d in range(args.distinct)]
+    log(f"encoded {args.distinct} distinct layer(s) in {time.time() - t0:.1f}s: "
+        f"{layers_host[0]['blob'].size / 1e6:.1f} MB compressed, "
+        f"{layers_host[0]['scratch_bytes'] / 1e6:.1f} MB tile bytes per layer")
+
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    tabs = [dict(in_off=devtab(torch, L["in_off"]), in_len=devtab(torch, L["in_len"]),
+                 out_off=devtab(torch, L["out_off"]), out_cap=devtab(torch, L["out_cap"]),
+                 n=L["in_off"].size) for L in layers_host]
+    d_comp, outs = [], []
+    for l in range(args.layers):
+        L = layers_host[l % args.distinct]
+        d_comp.append(torch.from_numpy(L["blob"].copy()).cuda())
+        outs.append([torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L8B])
+    scratch = [torch.empty(layers_host[0]["scratch_bytes"], dtype=torch.uint8, device="cuda")
+               for _ in range(2)]
+    status = torch.zeros(max(t["n"] for t in tabs) * 32, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    t_lz4, t_tile = Timed(torch, stream), Timed(torch, stream)
+
+    def run_layer(l, timed):
+        L = layers_host[l % args.distinct]
+        T = tabs[l % args.distinct]
+        s = scratch[l % 2]
+        e = t_lz4.start() if timed else None
+        rc = ctx.lz4_decompress_batch(d_comp[l], d_comp[l].numel(), T["in_off"], T["in_len"], s,
+                                      T["out_off"], T["out_cap"], T["n"], status, stream=sp)
+        assert rc == H.OK
+        if timed:
+            t_lz4.stop(e)
+            e = t_tile.start()
+        ctx.hctt_decode_batch([(s.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"], k,
+                                outs[l][i]) for i, t in enumerate(L["tensors"])],
+                              dtype=H.BF16, stream=sp)
+        if timed:
+            t_tile.stop(e)
+
+    def step(timed=False):
+        for l in range(args.layers):
+            run_layer(l, timed)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    codes = status.cpu().numpy().view(np.int32)[0::8][:tabs[-1]["n"]]
+    assert (codes == 0).all(), "LZ4 block errors"
+    check = None
+    if O is not None:
+        T0 = layers_host[0]["tensors"][0]
+        sub = 256
+        rc, ref = O.hctt_decode_tensor(T0["tiles"][: (sub // 64) * (T0["cols"] // 64) * tb], sub,
+                                       T0["cols"], k)
+        got = outs[0][0].view(T0["rows"], T0["cols"])[:sub].float().cpu().numpy()
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        check = float(np.abs(got - ref).max() / rms)
+        log(f"spot check layer0/q rows 0..{sub}: max|bf16 - oracle f32| = {check:.2e} x RMS")
+
+    torch.cuda.synchronize()
+    ta, tz = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ta.record(stream)
+    for _ in range(args.steps):
+        step(timed=True)
+    tz.record(stream)
+    torch.cuda.synchronize()
+    ms_step = ta.elapsed_time(tz) / args.steps
+    value = out_bytes_layer * args.layers / (ms_step / 1e3) / 1e9
+    in_tile = layers_host[0]["scratch_bytes"]
+    comp_bytes = layers_host[0]["blob"].size
+    tile_s, lz4_s = t_tile.mean_s(), t_lz4.mean_s()
+    log(f"per layer: lz4 {lz4_s * 1e6:.1f} us ({(comp_bytes + in_tile) / lz4_s / 1e9:.0f} GB/s "
+        f"in+out), tiles {tile_s * 1e6:.1f} us ({(in_tile + out_bytes_layer) / tile_s / 1e9:.0f} "
+        f"GB/s in+out)")
+    cpu = None
+    if not args.no_cpu and O is not None:
+        log("cpu baseline ...")
+        reps, secs, ne = cpu_layer_decode(O, layers_host[0], args.cpu_budget)
+        cpu = {"value": round(reps * ne * 2 / secs / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+               "kind": "port",
+               "sample": f"{reps} full Llama-3-8B layer decode(s) ({ne} elements each: LZ4 + dequant "
+                         f"+ scatter + f32 Makhoul IDCT), {cpu_threads()} threads, output counted as "
+                         f"bf16 bytes like the GPU line; {secs:.1f} s"}
+    return line("llama3-8b-layer", value, ms_step, args, "f16-split-mfma/f32",
+                f"synthetic (N(0,0.02) weights, seeded; {args.distinct} distinct layers replicated)",
+                {"layers": args.layers, "elements_per_layer": n_elem, "rho": RHO_8B, "k": k,
+                 "tile": 64, "tile_bytes": tb, "lz4_block_tiles": tiles_per_block,
+                 "out_dtype": "bf16", "hct_bytes_per_layer": in_tile,
+                 "lz4_bytes_per_layer": comp_bytes},
+                roofline("llama3-8b-layer", "hctt_decode_kernel<bf16>", in_tile + out_bytes_layer,
+                         tile_s),
+                cpu,
+                {"kernels_us": {"lz4_batch_kernel": round(lz4_s * 1e6, 2),
+                                "hctt_decode_kernel": round(tile_s * 1e6, 2)},
+                 "lz4_roofline": {"achieved": round((comp_bytes + in_tile) / lz4_s / 1e9, 1),
+                                  "frac": round((comp_bytes + in_tile) / lz4_s / 1e9 / HBM_PEAK_GBS, 4)},
+                 "spot_check_max_err_over_rms": check})
+
+
+def wl_int4(args, torch, H, O):
+    n = 4096 * 4096
+    rng = np.random.default_rng(1)
+    w = rng.normal(0, 0.02, n).astype(np.float32)
+    q = H.quantize_int4(w)
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    dq = torch.from_numpy(q.copy()).cuda()
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    launches = 200
+
+    def step():
+        for _ in range(launches):
+            ctx.dequant_int4(dq, q.size, n, out, dtype=H.F32, stream=sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    exact = None
+    if O is not None:
+        ref = O.dequantize_int4(q, n, threads=cpu_threads())
+        exact = bool((out.cpu().numpy().view(np.uint32) == ref.view(np.uint32)).all())
+        log(f"bit-exact vs oracle: {exact}")
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps):
+        step()
+    T.stop(e)
+    torch.cuda.synchronize()
+    ms_step = T.mean_s() * 1e3 / args.steps
+    per = ms_step / 1e3 / launches
+    out_b = n * 4
+    algo = q.size + out_b
+    cpu = None
+    if not args.no_cpu and O is not None:
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_budget and reps < 50:
+            O.dequantize_int4(q, n, threads=cpu_threads())
+            reps += 1
+        secs = time.perf_counter() - t0
+        cpu = {"value": round(reps * out_b / secs / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+               "kind": "port", "sample": f"{reps} dequantizations of the full 4096x4096 tensor to "
+                                         f"f32, {cpu_threads()} threads, {secs:.1f} s"}
+    return line("int4-4096", out_b / per / 1e9, ms_step, args, "f32",
+                "synthetic (4096x4096 N(0,0.02), seed 1)",
+                {"elements": n, "group": 32, "in_bytes": int(q.size), "out_dtype": "f32",
+                 "launches_per_step": launches},
+                roofline("int4-4096", "dequant_int4_kernel<f32>", algo, per), cpu,
+                {"bit_exact": exact})
+
+
+def config2_blocks(H, seed=3, nsrc=64, nblocks=4096):
+    rng = np.random.default_rng(seed)
+    srcs = []
+    for i in range(nsrc):
+        w = rng.normal(0, 0.02, 131072).astype(np.float32)
+        nib = H.quantize_int4(w)[2 * 4096:].copy()
+        if i % 2:
+            nib[np.repeat(rng.random(256) < 0.5, 256)] = 0
+        srcs.append(nib.tobytes())
+    comp = [H.Lz4Compressor().compress(s) for s in srcs]
+    pick = rng.integers(0, nsrc, nblocks)
+    in_len = np.array([len(comp[i]) for i in pick], np.uint32)
+    in_off = np.concatenate([[0], np.cumsum(in_len.astype(np.uint64))[:-1]]).astype(np.uint64)
+    blob = np.frombuffer(b"".join(comp[i] for i in pick), np.uint8)
+    return srcs, pick, blob, in_off, in_len
+
+
+def wl_lz4(args, torch, H, O):
+    nb = 4096
+    srcs, pick, blob, in_off, in_len = config2_blocks(H)
+    out_off = np.arange(nb, dtype=np.uint64) * 65536
+    out_cap = np.full(nb, 65536, np.uint32)
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    d_in = torch.from_numpy(blob.copy()).cuda()
+    d_out = torch.empty(nb * 65536, dtype=torch.uint8, device="cuda")
+    st = torch.zeros(nb * 32, dtype=torch.uint8, device="cuda")
+    a = (d_in, d_in.numel(), devtab(torch, in_off), devtab(torch, in_len), d_out,
+         devtab(torch, out_off), devtab(torch, out_cap), nb, st)
+    launches = 10
+
+    def step():
+        for _ in range(launches):
+            assert ctx.lz4_decompress_batch(*a, stream=sp) == H.OK
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    codes = st.cpu().numpy().view(np.int32)[0::8]
+    assert (codes == 0).all()
+    o = d_out.cpu().numpy()
+    exact = all(o[j * 65536:(j + 1) * 65536].tobytes() == srcs[pick[j]] for j in range(nb))
+    log(f"all {nb} blocks bit-exact: {exact}")
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps):
+        step()
+    T.stop(e)
+    torch.cuda.synchronize()
+    ms_step = T.mean_s() * 1e3 / args.steps
+    per = ms_step / 1e3 / launches
+    out_b = nb * 65536
+    cpu = None
+    if not args.no_cpu and O is not None:
+        m = 1024
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_budget and reps < 50:
+            O.lz4_decompress_batch(blob, in_off[:m], in_len[:m], out_off[:m], out_cap[:m],
+                                   m * 65536, nthreads=cpu_threads())
+            reps += 1
+        secs = time.perf_counter() - t0
+        cpu = {"value": round(reps * m * 65536 / secs / 1e9, 3), "unit": "GB/s",
+               "cores": cpu_threads(), "kind": "port",
+               "sample": f"{reps} x the first {m} of the 4096 blocks (64 MiB out each), "
+                         f"{cpu_threads()} threads, {secs:.1f} s"}
+    return line("lz4-256mib", out_b / per / 1e9, ms_step, args, "u8",
+                "synthetic (64 distinct seeded blocks, seeded coin per block)",
+                {"blocks": nb, "block_bytes": 65536, "in_bytes": int(blob.size),
+                 "launches_per_step": launches},
+                roofline("lz4-256mib", "lz4_batch_kernel", blob.size + out_b, per), cpu,
+                {"bit_exact": exact})
+
+
+def wl_idct(args, torch, H, O):
+    rows = cols = 8192
+    k = H.hctt_retain_count(0.25)
+    rng = np.random.default_rng(7)
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    t0 = time.time()
+    tiles = H.hctt_encode(w, k)
+    del w
+    log(f"encoded 8192x8192 in {time.time() - t0:.1f}s ({tiles.size} tile bytes)")
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    dt = torch.from_numpy(tiles).cuda()
+    out = torch.empty(rows * cols, dtype=torch.bfloat16, device="cuda")
+    launches = 10
+
+    def step():
+        for _ in range(launches):
+            ctx.hctt_decode(dt, tiles.size, rows, cols, k, out, dtype=H.BF16, stream=sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    check = None
+    if O is not None:
+        sub = 512
+        rc, ref = O.hctt_decode_tensor(tiles[:(sub // 64) * (cols // 64) * H.hctt_tile_bytes(k)],
+                                       sub, cols, k)
+        got = out.view(rows, cols)[:sub].float().cpu().numpy()
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        check = float(np.abs(got - ref).max() / rms)
+        log(f"spot check rows 0..{sub}: max|bf16 - oracle f32| = {check:.2e} x RMS")
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps):
+        step()
+    T.stop(e)
+    torch.cuda.synchronize()
+    ms_step = T.mean_s() * 1e3 / args.steps
+    per = ms_step / 1e3 / launches
+    out_b = rows * cols * 2
+    flop = 256.0 * rows * cols
+    cpu = None
+    if not args.no_cpu and O is not None:
+        sub = 1024
+        part = tiles[:(sub // 64) * (cols // 64) * H.hctt_tile_bytes(k)]
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_budget and reps < 50:
+            O.hctt_decode_tensor(part, sub, cols, k, nthreads=cpu_threads())
+            reps += 1
+        secs = time.perf_counter() - t0
+        cpu = {"value": round(reps * sub * cols * 2 / secs / 1e9, 3), "unit": "GB/s",
+               "cores": cpu_threads(), "kind": "port",
+               "sample": f"{reps} decodes of rows 0..{sub} (2048 tiles: dequant + scatter + f32 "
+                         f"Makhoul IDCT), bf16-equivalent output bytes, {cpu_threads()} threads, "
+                         f"{secs:.1f} s"}
+    return line("idct-8192", out_b / per / 1e9, ms_step, args, "f16-split-mfma/f32",
+                "synthetic (8192x8192 N(0,0.02), seed 7)",
+                {"rows": rows, "cols": cols, "rho": 0.25, "k": k, "tile_bytes": int(tiles.size),
+                 "out_dtype": "bf16", "launches_per_step": launches},
+                roofline("idct-8192", "hctt_decode_kernel<bf16>", tiles.size + out_b, per,
+                         {"algorithmic_tflops": round(flop / per / 1e12, 1),
+                          "issued_mfma": "v_mfma_f32_32x32x16_f16, 3 split passes, even/odd "
+                                         "halves: 48 per tile"}),
+                cpu, {"spot_check_max_err_over_rms": check})
+
+
+def wl_stream(args, torch, H, O):
+    rng = np.random.default_rng(70)
+    rhos = rng.uniform(0.10, 0.50, len(L70B))
+    ks = [H.hctt_retain_count(float(r)) for r in rhos]
+    n_elem = sum(r * c for _, r, c in L70B)
+    out_layer = n_elem * 2
+    t0 = time.time()
+    L = encode_layer(H, L70B, ks, 70, args.lz4_block)
+    log(f"encoded one 70B layer in {time.time() - t0:.1f}s: {L['blob'].size / 1e6:.1f} MB "
+        f"compressed, {L['scratch_bytes'] / 1e6:.1f} MB tile bytes; k = {ks}")
+    ctx = H.HipContext(0)
+    comp_stream = torch.cuda.current_stream()
+    copy_stream = torch.cuda.Stream()
+    csp, ysp = comp_stream.cuda_stream, copy_stream.cuda_stream
+    host = torch.from_numpy(L["blob"].copy()).pin_memory()
+    nin = host.numel()
+    d_in = [torch.empty(nin, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    scratch = torch.empty(L["scratch_bytes"], dtype=torch.uint8, device="cuda")
+    slot = [[torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L70B]
+            for _ in range(2)]
+    T = dict(in_off=devtab(torch, L["in_off"]), in_len=devtab(torch, L["in_len"]),
+             out_off=devtab(torch, L["out_off"]), out_cap=devtab(torch, L["out_cap"]),
+             n=L["in_off"].size)
+    status = torch.zeros(T["n"] * 32, dtype=torch.uint8, device="cuda")
+    copied = [torch.cuda.Event() for _ in range(2)]
+    consumed = [torch.cuda.Event() for _ in range(2)]
+    t_dec, t_h2d = Timed(torch, comp_stream), Timed(torch, copy_stream)
+    torch.cuda.synchronize()
+
+    def run(nlayers, timed):
+        for l in range(nlayers):
+            b = l % 2
+            copy_stream.wait_event(consumed[b])      # layer l - 2 has finished reading d_in[b]
+            e = t_h2d.start() if timed else None
+            with torch.cuda.stream(copy_stream):
+                d_in[b].copy_(host, non_blocking=True)
+            if timed:
+                t_h2d.stop(e)
+            copied[b].record(copy_stream)
+            comp_stream.wait_event(copied[b])
+            e = t_dec.start() if timed else None
+            rc = ctx.lz4_decompress_batch(d_in[b], nin, T["in_off"], T["in_len"], scratch,
+                                          T["out_off"], T["out_cap"], T["n"], status, stream=csp)
+            assert rc == H.OK
+            consumed[b].record(comp_stream)
+            ctx.hctt_decode_batch([(scratch.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"],
+                                    t["k"], slot[b][i]) for i, t in enumerate(L["tensors"])],
+                                  dtype=H.BF16, stream=csp)
+            if timed:
+                t_dec.stop(e)
+
+    run(2 * args.warmup, False)
+    torch.cuda.synchronize()
+    codes = status.cpu().numpy().view(np.int32)[0::8]
+    assert (codes == 0).all()
+    ta, tz = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ta.record(comp_stream)
+    copy_stream.wait_event(ta)
+    w0 = time.perf_counter()
+    run(args.stream_layers, True)
+    tz.record(comp_stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    e2e_s = ta.elapsed_time(tz) / 1e3
+    dec_s, h2d_s = t_dec.mean_s(), t_h2d.mean_s()
+    value = out_layer / dec_s / 1e9
+    e2e = out_layer * args.stream_layers / e2e_s / 1e9
+    h2d_gbs = nin / h2d_s / 1e9
+    # fraction of the shorter stage hidden under the longer one
+    per_layer = e2e_s / args.stream_layers
+    overlap = max(0.0, min(1.0, (dec_s + h2d_s - per_layer) / min(dec_s, h2d_s)))
+    log(f"per layer: decode {dec_s * 1e3:.2f} ms ({value:.0f} GB/s out), H2D {h2d_s * 1e3:.2f} ms "
+        f"({h2d_gbs:.1f} GB/s), end to end {e2e_s / args.stream_layers * 1e3:.2f} ms/layer "
+        f"({e2e:.0f} GB/s out); wall {wall:.2f}s")
+    cpu = None
+    if not args.no_cpu and O is not None:
+        reps, secs, ne = cpu_layer_decode(O, L, args.cpu_budget, max_reps=3, tensor_subset=[1, 2])
+        cpu = {"value": round(reps * ne * 2 / secs / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+               "kind": "port",
+               "sample": f"{reps} x LZ4 of the whole 70B layer + tile decode of its k and v tensors "
+                         f"({ne} elements), {cpu_threads()} threads, {secs:.1f} s"}
+    return line("llama70b-stream", value, e2e_s / args.stream_layers * 1e3, args,
+                "f16-split-mfma/f32",
+                "synthetic (one seeded 70B layer encoding streamed %d times)" % args.stream_layers,
+                {"layers": args.stream_layers, "elements_per_layer": n_elem,
+                 "rho": [round(float(r), 4) for r in rhos], "k": ks,
+                 "compressed_bytes_per_layer": int(nin), "out_dtype": "bf16",
+                 "source": "pinned host memory", "value_is": "decode-only (inputs in HBM)"},
+                roofline("llama70b-stream", "lz4_batch_kernel + hctt_decode_kernel<bf16>",
+                         L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
+                cpu,
+                {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
+                 "decode_ms_per_layer": round(dec_s * 1e3, 3),
+                 "h2d_ms_per_layer": round(h2d_s * 1e3, 3),
+                 "overlap_fraction": round(overlap, 3)})
+
+
+def wl_copy(args, torch, H, O):
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    stream = torch.cuda.current_stream()
+    launches = 10
+    for _ in range(args.warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps * launches):
+        b.copy_(a)
+    T.stop(e)
+    torch.cuda.synchronize()
+    per = T.mean_s() / (args.steps * launches)
+    return line("hbm-copy", 2 * n / per / 1e9, per * 1e3 * launches, args, "u8",
+                "synthetic (1 GiB device buffer)", {"bytes_read": n, "bytes_written": n},
+                roofline("hbm-copy", "torch copy (calibration)", 2 * n, per), None)
+
+
+WORKLOADS = {"llama3-8b-layer": wl_llama3_8b_layer, "int4-4096": wl_int4, "lz4-256mib": wl_lz4,
+             "idct-8192": wl_idct, "llama70b-stream": wl_stream, "hbm-copy": wl_copy}
 
 
 def main():
@@ -98,7 +634,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--workload", default="llama3-8b-layer", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=32, help="llama3-8b-layer: layers per step")
+    ap.add_argument("--stream-layers", type=int, default=80, help="llama70b-stream: layers")
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
@@ -111,147 +649,12 @@ def main():
               "decodes on a single MI355X; see DESIGN.md for how the path would shard).",
               file=sys.stderr)
         sys.exit(2)
-
     import torch
     import haagenti_amd as H
-
     torch.cuda.set_device(0)
-    k = H.hctt_retain_count(RHO)
-    tb = H.hctt_tile_bytes(k)
-    tiles_per_block = max(1, args.lz4_block // tb)
-    n_elem = sum(r * c for _, r, c in SHAPES)
-    out_bytes_layer = n_elem * 2
-
-    t0 = time.time()
-    layers_host = [encode_layer(H, d, k, tb, tiles_per_block) for d in range(args.distinct)]
-    log(f"encoded {args.distinct} distinct layer(s) in {time.time() - t0:.1f}s: "
-        f"{layers_host[0]['blob'].size / 1e6:.1f} MB compressed, "
-        f"{layers_host[0]['scratch_bytes'] / 1e6:.1f} MB tile bytes per layer")
-
-    ctx = H.HipContext(0)
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-
-    def u64(a):
-        return torch.from_numpy(a.view(np.int64)).cuda()
-
-    def u32(a):
-        return torch.from_numpy(a.view(np.int32)).cuda()
-
-    dev_tables = []
-    for L in layers_host:
-        dev_tables.append(dict(in_off=u64(L["in_off"]), in_len=u32(L["in_len"]),
-                               out_off=u64(L["out_off"]), out_cap=u32(L["out_cap"]),
-                               n=L["in_off"].size))
-    d_comp, outs = [], []
-    for l in range(args.layers):
-        L = layers_host[l % args.distinct]
-        d_comp.append(torch.from_numpy(L["blob"]).cuda())
-        outs.append([torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in SHAPES])
-    scratch = [torch.empty(layers_host[0]["scratch_bytes"], dtype=torch.uint8, device="cuda")
-               for _ in range(2)]
-    status = torch.zeros(max(t["n"] for t in dev_tables) * 32, dtype=torch.uint8, device="cuda")
-    torch.cuda.synchronize()
-
-    nlaunch = [0]
-    ev = []
-
-    def run_layer(l, timed):
-        L = layers_host[l % args.distinct]
-        T = dev_tables[l % args.distinct]
-        s = scratch[l % 2]
-        if timed:
-            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-            e0.record(stream)
-        rc = ctx.lz4_decompress_batch(d_comp[l], d_comp[l].numel(), T["in_off"], T["in_len"], s,
-                                      T["out_off"], T["out_cap"], T["n"], status, stream=sp)
-        assert rc == H.OK
-        if timed:
-            e1.record(stream)
-        ctx.hctt_decode_batch([(s.data_ptr() + soff, tlen, rows, cols, k, outs[l][i])
-                               for i, (name, rows, cols, soff, tlen, _) in enumerate(L["tensors"])],
-                              dtype=H.BF16, stream=sp)
-        if timed:
-            e2.record(stream)
-            ev.append((e0, e1, e2))
-
-    def step(timed=False):
-        for l in range(args.layers):
-            run_layer(l, timed)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # correctness spot check of layer 0 / q against the oracle
-    codes = status.cpu().numpy().view(np.int32)[0::8][:dev_tables[-1]["n"]]
-    assert (codes == 0).all(), "LZ4 block errors"
-    check = None
-    try:
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        import oracle_lib as O
-        name, rows, cols, soff, tlen, qtiles = layers_host[0]["tensors"][0]
-        sub_rows = 256
-        rc, ref = O.hctt_decode_tensor(qtiles[: (sub_rows // 64) * (cols // 64) * tb], sub_rows, cols, k)
-        got = outs[0][0].view(rows, cols)[:sub_rows].float().cpu().numpy()
-        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
-        check = float(np.abs(got - ref).max() / rms)
-        log(f"spot check layer0/q rows 0..{sub_rows}: max|bf16 - oracle f32| = {check:.2e} x RMS")
-    except Exception as ex:  # oracle library missing is not fatal for timing
-        O = None
-        log(f"spot check skipped: {ex}")
-
-    torch.cuda.synchronize()
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    ev.clear()
-    t_start.record(stream)
-    w0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(timed=True)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    total_ms = t_start.elapsed_time(t_end)
-    ms_step = total_ms / args.steps
-    value = out_bytes_layer * args.layers / (ms_step / 1e3) / 1e9
-
-    lz4_ms = [a.elapsed_time(b) for a, b, _ in ev]
-    tile_ms = [b.elapsed_time(c) for _, b, c in ev]
-    in_tile_bytes = layers_host[0]["scratch_bytes"]
-    comp_bytes = layers_host[0]["blob"].size
-    tile_avg = float(np.mean(tile_ms))
-    lz4_avg = float(np.mean(lz4_ms))
-    tile_gbs = (in_tile_bytes + out_bytes_layer) / (tile_avg / 1e3) / 1e9
-    lz4_gbs = (comp_bytes + in_tile_bytes) / (lz4_avg / 1e3) / 1e9
-    log(f"per layer: lz4 {lz4_avg * 1e3:.1f} us ({lz4_gbs:.0f} GB/s in+out), "
-        f"tiles {tile_avg * 1e3:.1f} us ({tile_gbs:.0f} GB/s in+out, "
-        f"{256 * n_elem / (tile_avg / 1e3) / 1e12:.0f} TFLOP/s algorithmic); wall {wall:.3f}s")
-
-    line = {
-        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16-split-mfma/f32",
-        "data": "synthetic (N(0,0.02) weights, seeded; %d distinct layers replicated)" % args.distinct,
-        "config": {"workload": "llama3-8b-layer-hct-decode", "layers": args.layers,
-                   "elements_per_layer": n_elem, "rho": RHO, "k": k, "tile": 64,
-                   "tile_bytes": tb, "lz4_block_tiles": tiles_per_block, "out_dtype": "bf16",
-                   "hct_bytes_per_layer": in_tile_bytes, "lz4_bytes_per_layer": comp_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(tile_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(tile_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "hctt_decode_kernel<bf16>",
-                     "avg_launch_us": round(tile_avg * 1e3, 2)},
-        "kernels_us": {"lz4_batch_kernel": round(lz4_avg * 1e3, 2),
-                       "hctt_decode_kernel": round(tile_avg * 1e3, 2)},
-        "spot_check_max_err_over_rms": check,
-    }
-    if not args.no_cpu and O is not None:
-        log("cpu baseline ...")
-        line["cpu_baseline"] = cpu_baseline(O, layers_host[0], k, args.cpu_budget)
-    else:
-        line["cpu_baseline"] = None
-    print(json.dumps(line), flush=True)
+    O = oracle()
+    res = WORKLOADS[args.workload](args, torch, H, O)
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":
