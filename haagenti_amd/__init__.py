@@ -99,6 +99,20 @@ class HcttTensor(C.Structure):
 
 _sig("hh_hctt_decode_batch", _i32, [_vp, C.POINTER(HcttTensor), _u32, _i32, _vp])
 
+
+class HctInfo(C.Structure):
+    """hh_hct_info: HCT v1 header fields (crates/haagenti-hct/src/tensor.rs:275-375)."""
+    _fields_ = [("version", C.c_uint32), ("algorithm", C.c_uint8), ("dtype", C.c_uint8),
+                ("flags", C.c_uint16), ("original_size", C.c_uint64),
+                ("compressed_size", C.c_uint64), ("block_size", C.c_uint32),
+                ("num_blocks", C.c_uint32), ("rank", C.c_uint32), ("pad", C.c_uint32),
+                ("shape", C.c_uint64 * 4), ("data_offset", C.c_uint64)]
+
+
+_sig("hh_hct_read_header", _i32, [_vp, _sz, C.POINTER(HctInfo), C.POINTER(BlockStatus)])
+_sig("hh_hct_decompress_all", _i32, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_sz),
+                                      C.POINTER(BlockStatus), C.POINTER(C.c_int64), _vp])
+
 # Every symbol include/haagenti_hip.h declares (checked by the tests).
 EXPORTS = [
     "hh_status_category", "hh_status_is_recoverable", "hh_version", "hh_device_count",
@@ -107,6 +121,7 @@ EXPORTS = [
     "hh_lz4_max_compressed_size", "hh_dequant_int4", "hh_quantize_int4",
     "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
     "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_encode",
+    "hh_hct_read_header", "hh_hct_decompress_all",
 ]
 
 
@@ -233,6 +248,83 @@ class HipContext:
         if rc != OK:
             raise HaagentiError(rc, "lz4 decompress", st)
         return out.raw[:written.value], st
+
+
+class HctReader:
+    """HctReader (crates/haagenti-hct/src/tensor.rs:408-516) over an in-memory
+    HCT v1 file: header(), num_blocks(), read_block(), decompress_block(),
+    decompress_all() with any decompressor object (per block, as the
+    reference does), plus decompress_all_gpu(): every block in one batched
+    GPU launch (hh_hct_decompress_all)."""
+
+    def __init__(self, data):
+        self._data = bytes(data)
+        self._info = HctInfo()
+        st = BlockStatus()
+        rc = _lib.hh_hct_read_header(self._data, len(self._data), C.byref(self._info), C.byref(st))
+        if rc != OK:
+            raise HaagentiError(rc, "hct header", st)
+
+    def header(self):
+        i = self._info
+        return dict(version=i.version, algorithm=i.algorithm, dtype=i.dtype, flags=i.flags,
+                    original_size=i.original_size, compressed_size=i.compressed_size,
+                    block_size=i.block_size, num_blocks=i.num_blocks,
+                    shape=list(i.shape[:i.rank]))
+
+    def num_blocks(self):
+        return int(self._info.num_blocks)
+
+    def _entry(self, idx):
+        import struct
+        off, csz = struct.unpack_from("<II", self._data, 64 + 8 * idx)
+        return self._info.data_offset + off, csz
+
+    def read_block(self, idx):
+        if idx >= self.num_blocks():
+            raise HaagentiError(CORRUPTED_DATA, f"block index out of range: {idx} >= {self.num_blocks()}")
+        start, csz = self._entry(idx)
+        if start + csz > len(self._data):
+            raise HaagentiError(ALGORITHM, f"failed to read block {idx}")
+        return self._data[start:start + csz]
+
+    def expected_size(self, idx):
+        n, bs = self.num_blocks(), self._info.block_size
+        if idx == n - 1:
+            full = (n - 1) * bs
+            if full > self._info.original_size:
+                raise HaagentiError(CORRUPTED_DATA, "last block size")
+            return self._info.original_size - full
+        return bs
+
+    def decompress_block(self, idx, decompressor):
+        compressed = self.read_block(idx)
+        return decompressor.decompress_with_size(compressed, self.expected_size(idx))
+
+    def decompress_all(self, decompressor):
+        return b"".join(self.decompress_block(i, decompressor) for i in range(self.num_blocks()))
+
+    def decompress_all_gpu(self, ctx, d_file=None, d_out=None, out_cap=None, stream=None):
+        """Batched GPU decode.  Returns (written, d_out); d_file / d_out are
+        allocated with torch when not given.  Raises HaagentiError (with
+        .status and .failed_block) on failure."""
+        import numpy as np
+        import torch
+        if d_file is None:
+            d_file = torch.from_numpy(np.frombuffer(self._data, np.uint8).copy()).cuda()
+        if out_cap is None:
+            out_cap = int(self._info.original_size)
+        if d_out is None:
+            d_out = torch.empty(max(out_cap, 1), dtype=torch.uint8, device="cuda")
+        written, st, fb = _sz(0), BlockStatus(), C.c_int64(-1)
+        rc = _lib.hh_hct_decompress_all(ctx.handle, self._data, _addr(d_file), len(self._data),
+                                        _addr(d_out), int(out_cap), C.byref(written), C.byref(st),
+                                        C.byref(fb), stream)
+        if rc != OK:
+            e = HaagentiError(rc, f"hct block {fb.value}", st)
+            e.failed_block = fb.value
+            raise e
+        return written.value, d_out
 
 
 class Lz4Decompressor:

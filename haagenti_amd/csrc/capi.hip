@@ -284,4 +284,188 @@ int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len
     return hh_hctt_decode_batch(ctx, &T, 1, out_dtype, stream);
 }
 
+// ---------------------------------------------------------------- HCT container
+
+namespace {
+
+uint32_t rd_u32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+uint64_t rd_u64(const uint8_t *p) { return (uint64_t)rd_u32(p) | ((uint64_t)rd_u32(p + 4) << 32); }
+
+int32_t fail(hh_block_status *st, int32_t code, int32_t detail, uint64_t pos = 0,
+             uint64_t req = 0) {
+    if (st) {
+        st->code = code;
+        st->detail = detail;
+        st->position = pos;
+        st->required = req;
+        st->written = 0;
+    }
+    return code;
+}
+
+}  // namespace
+
+int32_t hh_hct_read_header(const uint8_t *file, size_t file_len, hh_hct_info *info,
+                           hh_block_status *status) {
+    if (!info || (!file && file_len)) return HH_ERR_INVALID_ARGUMENT;
+    std::memset(info, 0, sizeof(*info));
+    if (status) std::memset(status, 0, sizeof(*status));
+    const size_t kHeader = 64;
+    if (file_len < kHeader) return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
+    if (std::memcmp(file, "HCTN", 4) != 0) return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER);
+    info->version = rd_u32(file + 4);
+    if (info->version > 2) return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER);
+    info->algorithm = file[8];
+    info->dtype = file[9];
+    if (info->algorithm > 1 || info->dtype > 4)
+        return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER);
+    info->flags = (uint16_t)(file[10] | (file[11] << 8));
+    info->original_size = rd_u64(file + 12);
+    info->compressed_size = rd_u64(file + 20);
+    info->block_size = rd_u32(file + 28);
+    info->num_blocks = rd_u32(file + 32);
+    info->rank = file[36];
+    // four dimensions would overrun the 64-byte header (37 + 4 * 8 > 64)
+    if (info->rank > 3) return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER);
+    for (uint32_t i = 0; i < info->rank; i++) info->shape[i] = rd_u64(file + 37 + 8 * i);
+    info->data_offset = kHeader + (uint64_t)info->num_blocks * 8;
+    if (info->data_offset > file_len) return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
+    return HH_OK;
+}
+
+int32_t hh_hct_decompress_all(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                              size_t file_len, uint8_t *d_out, size_t out_cap, size_t *written,
+                              hh_block_status *status, int64_t *failed_block, void *stream) {
+    if (written) *written = 0;
+    if (failed_block) *failed_block = -1;
+    if (!ctx || !h_file || !d_file || (!d_out && out_cap)) return HH_ERR_INVALID_ARGUMENT;
+    hh_hct_info info;
+    int32_t rc = hh_hct_read_header(h_file, file_len, &info, status);
+    if (rc != HH_OK) return rc;
+    const uint32_t n = info.num_blocks;
+    const uint8_t *index = h_file + 64;
+    // Host-side checks in the reference's per-block order; blocks before the
+    // first failing one are decoded (one of them may fail first).
+    uint32_t m = n;  // blocks [0, m) pass the host checks
+    int32_t host_code = HH_OK, host_detail = HH_CORRUPT_NONE;
+    std::vector<uint64_t> in_off(n), out_off(n);
+    std::vector<uint32_t> in_len(n), expect(n);
+    uint64_t nominal = 0;
+    for (uint32_t b = 0; b < n; b++) {
+        const uint32_t off = rd_u32(index + 8 * (size_t)b), csz = rd_u32(index + 8 * (size_t)b + 4);
+        if (info.data_offset + off + csz > file_len) {  // read_block fails (:477-480)
+            m = b;
+            host_code = HH_ERR_ALGORITHM;
+            break;
+        }
+        uint64_t e = info.block_size;
+        if (b == n - 1) {  // last block: original_size - full blocks (:494-500)
+            const uint64_t full = (uint64_t)(n - 1) * info.block_size;
+            if (full > info.original_size) {
+                m = b;
+                host_code = HH_ERR_CORRUPTED_DATA;
+                host_detail = HH_CORRUPT_SIZE;
+                break;
+            }
+            e = info.original_size - full;
+        }
+        if (e > 0xffffffffull) return fail(status, HH_ERR_UNSUPPORTED, HH_CORRUPT_NONE);
+        in_off[b] = info.data_offset + off;
+        in_len[b] = csz;
+        expect[b] = (uint32_t)e;
+        out_off[b] = nominal;
+        nominal += e;
+    }
+    hipError_t he = hipSetDevice(ctx->device);
+    if (he != hipSuccess) return from_hip(he);
+    hipStream_t s = pick_stream(ctx, stream);
+    // Decode into d_out at the nominal block positions when they fit, else
+    // into a staging area of the context scratch; compact afterwards.
+    const bool direct = nominal <= out_cap;
+    const size_t tab = (size_t)m * (32 + 8 + 4 + 8 + 4);
+    const size_t stage_at = (tab + 255) & ~(size_t)255;
+    std::vector<hh_block_status> st(m);
+    if (m > 0) {
+        rc = ensure_scratch(ctx, stage_at + (direct ? 0 : nominal) + 16);
+        if (rc != HH_OK) return rc;
+        uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+        hh_block_status *d_st = reinterpret_cast<hh_block_status *>(base);
+        uint64_t *d_in_off = reinterpret_cast<uint64_t *>(base + (size_t)m * 32);
+        uint64_t *d_out_off = d_in_off + m;
+        uint32_t *d_in_len = reinterpret_cast<uint32_t *>(d_out_off + m);
+        uint32_t *d_cap = d_in_len + m;
+        uint8_t *dst = direct ? d_out : base + stage_at;
+        he = hipMemcpyAsync(d_in_off, in_off.data(), 8 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess)
+            he = hipMemcpyAsync(d_out_off, out_off.data(), 8 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess)
+            he = hipMemcpyAsync(d_in_len, in_len.data(), 4 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess)
+            he = hipMemcpyAsync(d_cap, expect.data(), 4 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess)
+            he = hh::launch_lz4_batch(d_file, file_len, d_in_off, d_in_len, dst, d_out_off, d_cap, m,
+                                      d_st, s);
+        if (he == hipSuccess)
+            he = hipMemcpyAsync(st.data(), d_st, 32 * (size_t)m, hipMemcpyDeviceToHost, s);
+        if (he == hipSuccess) he = hipStreamSynchronize(s);
+        if (he != hipSuccess) return from_hip(he);
+        // the reference's loop: output cap, then the block's own result
+        uint64_t op = 0;
+        bool shifted = false;
+        for (uint32_t b = 0; b < m; b++) {
+            if (op + expect[b] > out_cap) {
+                if (failed_block) *failed_block = b;
+                return fail(status, HH_ERR_BUFFER_TOO_SMALL, HH_CORRUPT_NONE, 0, op + expect[b]);
+            }
+            if (st[b].code != HH_OK) {
+                if (failed_block) *failed_block = b;
+                if (status) *status = st[b];
+                return st[b].code;
+            }
+            if (op != out_off[b]) shifted = true;
+            op += st[b].written;
+        }
+        if (host_code == HH_OK && (shifted || !direct)) {
+            // a short block shifts the blocks after it (truncate, then extend)
+            if (direct) {  // bounce buffer for the overlapping moves to the left
+                uint64_t maxw = 0;
+                for (uint32_t b = 0; b < m; b++) maxw = st[b].written > maxw ? st[b].written : maxw;
+                rc = ensure_scratch(ctx, stage_at + maxw + 16);
+                if (rc != HH_OK) return rc;
+            }
+            uint64_t o = 0;
+            for (uint32_t b = 0; b < m && he == hipSuccess; b++) {
+                const uint64_t w = st[b].written;
+                if (w && (!direct || o != out_off[b])) {
+                    if (direct) {  // overlapping move to the left: bounce through scratch
+                        uint8_t *bounce = reinterpret_cast<uint8_t *>(ctx->d_scratch) + stage_at;
+                        he = hipMemcpyAsync(bounce, d_out + out_off[b], w, hipMemcpyDeviceToDevice, s);
+                        if (he == hipSuccess)
+                            he = hipMemcpyAsync(d_out + o, bounce, w, hipMemcpyDeviceToDevice, s);
+                    } else {
+                        he = hipMemcpyAsync(d_out + o,
+                                            reinterpret_cast<uint8_t *>(ctx->d_scratch) + stage_at + out_off[b],
+                                            w, hipMemcpyDeviceToDevice, s);
+                    }
+                }
+                o += w;
+            }
+            if (he == hipSuccess) he = hipStreamSynchronize(s);
+            if (he != hipSuccess) return from_hip(he);
+        }
+        if (written) *written = op;
+    }
+    if (host_code != HH_OK) {
+        if (failed_block) *failed_block = m;
+        return fail(status, host_code, host_detail, host_code == HH_ERR_ALGORITHM ? file_len : 0);
+    }
+    if (status) {
+        std::memset(status, 0, sizeof(*status));
+        status->written = written ? *written : 0;
+    }
+    return HH_OK;
+}
+
 }  // extern "C"

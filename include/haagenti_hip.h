@@ -186,6 +186,50 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
 int32_t hh_hctt_encode(const float *w, uint32_t rows, uint32_t cols, uint32_t k,
                        uint8_t *out, int32_t threads);
 
+/* ---------------------------------------------------------------- HCT container */
+
+/* Header and block-index geometry of an HCT v1 file (64-byte header,
+ * tensor.rs:275-375; 8-byte block index entries, :379-405). */
+typedef struct hh_hct_info {
+    uint32_t version;
+    uint8_t algorithm;      /* 0 LZ4, 1 Zstd (tensor.rs CompressionAlgorithm) */
+    uint8_t dtype;          /* haagenti_hct::DType, 0..4 */
+    uint16_t flags;
+    uint64_t original_size;
+    uint64_t compressed_size;
+    uint32_t block_size;
+    uint32_t num_blocks;
+    uint32_t rank;
+    uint32_t pad;
+    uint64_t shape[4];
+    uint64_t data_offset;   /* 64 + 8 * num_blocks */
+} hh_hct_info;
+
+/* HctHeader::from_bytes (crates/haagenti-hct/src/tensor.rs:302-375) and the
+ * index read of HctReader::new (:417-445) on host bytes.  Errors as the
+ * reference reports them: a file shorter than the header or its index is
+ * HH_ERR_ALGORITHM (read_exact failures, :420-431); bad magic, version > 2,
+ * unknown algorithm or dtype, or a rank above 3 are HH_ERR_CORRUPTED_DATA
+ * with detail HH_CORRUPT_HEADER (status, when given, receives the record). */
+int32_t hh_hct_read_header(const uint8_t *file, size_t file_len, hh_hct_info *info,
+                           hh_block_status *status);
+
+/* HctReader::new + decompress_all with the LZ4 decompressor
+ * (tensor.rs:417-515): every block of the file decoded in one batched GPU
+ * launch.  h_file is the file on the host (at least its header and index;
+ * file_len is the full length), d_file the same file in device memory.  The
+ * output is the concatenation of the blocks as the reference builds it (a
+ * block that decodes short shifts the ones after it) in d_out (out_cap
+ * bytes); *written receives its length.  On failure the error is the one
+ * the reference's block-by-block loop meets first: an index entry past the
+ * end of the file (HH_ERR_ALGORITHM, :477-480), an inconsistent last-block
+ * size (HH_ERR_CORRUPTED_DATA / HH_CORRUPT_SIZE, :494-500), output beyond
+ * out_cap (HH_ERR_BUFFER_TOO_SMALL), or the block's LZ4 error; *failed_block
+ * (optional) receives its index, or -1.  Synchronous on the given stream. */
+int32_t hh_hct_decompress_all(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                              size_t file_len, uint8_t *d_out, size_t out_cap, size_t *written,
+                              hh_block_status *status, int64_t *failed_block, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

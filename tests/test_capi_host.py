@@ -121,3 +121,26 @@ def test_hctt_encoder_matches_oracle_encoder():
         assert rc1 == rc2 == O.OK
         rms = np.sqrt((b ** 2).mean())
         assert np.abs(a - b).max() < 0.2 * rms  # at most a few near-tie flips
+
+
+# ---------------------------------------------------------------- HCT header (host)
+def test_hct_header_parse_matches_writer():
+    import haagenti_amd as H
+    f = O.hct_write_lz4(b"\x12" * 1000, 256, 4, [10, 100])
+    h = H.HctReader(f).header()
+    assert h == dict(version=1, algorithm=0, dtype=4, flags=0, original_size=1000,
+                     compressed_size=h["compressed_size"], block_size=256, num_blocks=4,
+                     shape=[10, 100])
+    assert h["compressed_size"] == len(f) - 64 - 4 * 8
+
+
+def test_hct_header_errors_match_oracle():
+    import haagenti_amd as H
+    f = O.hct_write_lz4(b"\x12" * 512, 256, 0, [512])
+    cases = [f[:40], f[:68], b"XXXX" + f[4:], f[:4] + b"\x03" + f[5:], f[:8] + b"\x02" + f[9:],
+             f[:9] + b"\x05" + f[10:], f[:36] + b"\x04" + f[37:]]
+    for c in cases:
+        _, e = O.hct_read_all_lz4(c, 1024)
+        with pytest.raises(H.HaagentiError) as ei:
+            H.HctReader(c)
+        assert ei.value.code == e.kind, (c[:12], ei.value.code, e.kind)
