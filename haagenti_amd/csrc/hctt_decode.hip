@@ -94,12 +94,20 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // in place: lo = round_f16(a * 1 - hi), computed exactly in f32 first.
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
     hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-    uint32_t l = 0;
-    __asm__("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]\n\t"
-            "v_fma_mixhi_f16 %0, %3, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-            : "+&v"(l)
-            : "v"(a), "v"(hi), "v"(b));
+    uint32_t l;
+    __asm__("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l) : "v"(a), "v"(hi));
+    __asm__("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+            : "+v"(l)
+            : "v"(b), "v"(hi));
     lo = l;
+}
+
+// x -> f16 hi in bits 0..15 and f16 lo = round_f16(x - hi) in bits 16..31 of
+// one register (the table entry format of the retained coefficients).
+__device__ __forceinline__ uint32_t split1(float x) {
+    uint32_t v = __builtin_bit_cast(uint16_t, (_Float16)x);
+    __asm__("v_fma_mixhi_f16 %0, %1, 1.0, -%0 op_sel_hi:[0,0,1]" : "+v"(v) : "v"(x));
+    return v;
 }
 
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
@@ -121,14 +129,17 @@ struct TileBatch {
     uint32_t vo_bytes;  // size of the V/output union
 };
 
-// Workgroup LDS layout: [batch descriptor][M fragment table][zero word][per-wave areas].
-// The descriptor is copied from the kernel arguments once: indexing the
-// by-value argument with a per-tile tensor index would compile to vector
-// loads whose waits also stall on the prefetch and the output stores.
+// Workgroup LDS layout: [zero word][batch descriptor][M fragment table][per-wave areas].
+// The zero word sits at LDS address 0, so a gathered address masked to 0
+// reads zeros.  The descriptor is copied from the kernel arguments once:
+// indexing the by-value argument with a per-tile tensor index would compile
+// to vector loads whose waits also stall on the prefetch and the output
+// stores.
+constexpr uint32_t kZeroOff = 0;
+constexpr uint32_t kBatchOff = kZeroBytes;
 constexpr uint32_t kBatchBytes = (sizeof(TileBatch) + 15u) & ~15u;
-constexpr uint32_t kMTabOff = kBatchBytes;
-constexpr uint32_t kZeroOff = kMTabOff + kMTabBytes;
-constexpr uint32_t kSharedBytes = kZeroOff + kZeroBytes;
+constexpr uint32_t kMTabOff = kBatchOff + kBatchBytes;
+constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 
 // Loads the bytes of global tile gt into registers, 16 bytes per lane per
 // KiB, always issuing kMaxPrefetch loads (chunks past the tile end re-read
@@ -178,11 +189,11 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
     const int l32 = lane & 31;
     u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
     for (int i = threadIdx.x; i < (int)(sizeof(TileBatch) / 4); i += kThreads)
-        reinterpret_cast<uint32_t *>(smem)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
+        reinterpret_cast<uint32_t *>(smem + kBatchOff)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
     for (int i = threadIdx.x; i < (int)(kMTabBytes / 16); i += kThreads) mtab[i] = basis[i];
     if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
-    const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem);
+    const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem + kBatchOff);
     const uint32_t wbase = kSharedBytes + wave * B.wave_lds;  // byte offset of this wave's area
     const uint32_t pbase = wbase + B.vo_bytes;                // staged tile bytes
     uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
@@ -249,16 +260,12 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
                 const uint32_t r0 = 4 * g4;
                 const uint32_t w4 = nib16[g4];  // nibbles r0 .. r0+3, low first
                 const float s = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
+                const float s8 = -8.0f * s;
                 uint32_t v[4];
+                // (q - 8) * s = fma(q, s, -8 s): exact in f32, one rounding
 #pragma unroll
-                for (int e = 0; e < 4; e += 2) {
-                    const float x0 = (float)((int)((w4 >> (4 * e)) & 15u) - 8) * s;
-                    const float x1 = (float)((int)((w4 >> (4 * e + 4)) & 15u) - 8) * s;
-                    uint32_t hi, lo;
-                    split2(x0, x1, hi, lo);
-                    v[e] = __builtin_amdgcn_perm(lo, hi, 0x05040100u);
-                    v[e + 1] = __builtin_amdgcn_perm(lo, hi, 0x07060302u);
-                }
+                for (int e = 0; e < 4; e++)
+                    v[e] = split1(__builtin_fmaf((float)((w4 >> (4 * e)) & 15u), s, s8));
                 if (r0 + 4 <= k) {
                     *reinterpret_cast<u32x4 *>(V + r0) = u32x4{v[0], v[1], v[2], v[3]};
                 } else {
@@ -277,70 +284,68 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         //    vpar 0, odd offsets vpar 1.
         const uint64_t bits_r[2] = {__shfl(bits, 2 * l32), __shfl(bits, 2 * l32 + 1)};
         const uint32_t pre_r[2] = {__shfl(pre, 2 * l32), __shfl(pre, 2 * l32 + 1)};
-        u32x4 ahi[2][2][2], alo[2][2][2];  // [upar][vpar][s]
+        // 5. GEMM1 (even/odd halves of the column frequencies), one row
+        //    parity at a time so that only its A fragments are live:
+        //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
+        //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
+        floatx16 acc[2][2];
 #pragma unroll
         for (int up = 0; up < 2; up++) {
+            u32x4 ahi[2][2], alo[2][2];  // [vpar][s]
             const uint64_t b64 = ok ? bits_r[up] : 0ull;
             // the row shifted so that column 8 h is bit 0: every column this
             // lane needs sits at a compile-time bit position
             const uint64_t bh = b64 >> (8 * h);
             const uint32_t wd[2] = {(uint32_t)bh, (uint32_t)(bh >> 32)};
             const uint32_t rank_h = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << (8 * h)) - 1ull));
-            // LDS byte address of V[rank] minus the zero word's address; a
-            // column that is not retained selects the zero word (bit * diff = 0)
-            uint32_t diff = wbase + 4 * rank_h - kZeroOff;
+            // LDS byte address of V[rank]; a column that is not retained
+            // masks it to 0, the zero word
+            uint32_t diff = wbase + 4 * rank_h;
 #pragma unroll
             for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int run = 0; run < 2; run++) {
                     const uint32_t word = wd[s];
-                    uint32_t w[8];
+                    uint32_t a[8];  // LDS address of each column's table entry, or 0
 #pragma unroll
                     for (int o = 0; o < 8; o++) {
                         // all-ones when column 16 run + o of the word is retained
                         const int32_t m = (int32_t)(word << (31 - (16 * run + o))) >> 31;
-                        w[o] = *reinterpret_cast<const uint32_t *>(smem + kZeroOff + ((uint32_t)m & diff));
-                        diff += (uint32_t)(m * -4);
+                        a[o] = (uint32_t)m & diff;
+                        __asm__("v_mad_i32_i24 %0, %1, -4, %0" : "+v"(diff) : "v"(m));
                     }
                     // columns 16 run + 8 .. 16 run + 15 of this word belong to the
                     // other lane half
                     diff += (uint32_t)__popc((word >> (16 * run + 8)) & 0xffu) << 2;
-                    // dword p of a fragment packs elements e = 2p, 2p + 1;
-                    // this run supplies e = 4 run .. 4 run + 3
+                    // dword p of a fragment packs elements e = 2p, 2p + 1 (this run
+                    // supplies e = 4 run .. 4 run + 3, at offsets 2 (e - 4 run) + vpar);
+                    // a table entry is f16 hi | f16 lo << 16
+                    uint32_t w[8];
+#pragma unroll
+                    for (int o = 0; o < 8; o++) w[o] = *reinterpret_cast<const uint32_t *>(smem + a[o]);
 #pragma unroll
                     for (int vp = 0; vp < 2; vp++) {
-                        ahi[up][vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
-                        alo[up][vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
-                        ahi[up][vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
-                        alo[up][vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
+                        ahi[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
+                        alo[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
+                        ahi[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
+                        alo[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
                     }
+                }
+            }
+#pragma unroll
+            for (int vp = 0; vp < 2; vp++) {
+                acc[up][vp] = floatx16{};
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
+                    const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
+                    acc[up][vp] = mfma(ahi[vp][s], mh, acc[up][vp]);
+                    acc[up][vp] = mfma(ahi[vp][s], ml, acc[up][vp]);
+                    acc[up][vp] = mfma(alo[vp][s], mh, acc[up][vp]);
                 }
             }
         }
         wave_sync();
-
-        // 5. GEMM1 (even/odd halves of the column frequencies):
-        //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
-        //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
-        floatx16 acc[2][2];
-#pragma unroll
-        for (int up = 0; up < 2; up++)
-#pragma unroll
-            for (int vp = 0; vp < 2; vp++) acc[up][vp] = floatx16{};
-#pragma unroll
-        for (int vp = 0; vp < 2; vp++) {
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
-                const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
-#pragma unroll
-                for (int up = 0; up < 2; up++) {
-                    acc[up][vp] = mfma(ahi[up][vp][s], mh, acc[up][vp]);
-                    acc[up][vp] = mfma(ahi[up][vp][s], ml, acc[up][vp]);
-                    acc[up][vp] = mfma(alo[up][vp][s], mh, acc[up][vp]);
-                }
-            }
-        }
 
         // 6-7. per output column block jb (jb = 0: j = n; jb = 1: j = 63 - n):
         //    B = S rows of parity upar; GEMM2 X[i][j] = sum_u M[u][i] S[u][j]
