@@ -19,14 +19,18 @@
 // fragments without any shuffle or LDS trip, and one table of M fragments
 // serves as GEMM1's B and GEMM2's A.
 //
-// Precision.  Operands are split into f16 hi + lo (~2^-20 relative for the
-// coefficients, M and S) and each GEMM runs three passes hi*hi + hi*lo +
-// lo*hi with f32 accumulation (max-abs error ~1e-6 x RMS; the bar is
-// 1e-3 x RMS).  Coefficients are prescaled by 2^E per tile (E from the
-// largest f16 scale exponent, so that |C 2^E| < 4) and M by 2^8, which puts
-// GEMM1's output directly in the range of GEMM2's f16 operands; only lo
-// parts of coefficients below ~2^-10 of the tile maximum lose bits to f16
-// subnormals (2^-25 absolute).  The output is rescaled exactly.
+// Precision.  Each retained coefficient (q - 8) * scale is held exactly as
+// an f16 pair hi + lo (the scale split into its top 8 and low 3 significant
+// bits, each product with q - 8 exact), and GEMM1 runs all four passes
+// hi*hi + hi*lo + lo*hi + lo*lo against M = M_hi + M_lo (~2^-22 relative).
+// GEMM1's output S is split the same way by rounding (S_hi = f16(S),
+// S_lo = f16(S - S_hi)) and GEMM2 runs three passes (the dropped
+// S_lo * M_lo is ~2^-24 relative).  Accumulation is f32; the max-abs error
+// is ~1e-6 x RMS against a bar of 1e-3 x RMS.  Coefficients are prescaled
+// by 2^E per tile (E from the largest f16 scale exponent, so that
+// |C 2^E| < 4) and M by 2^8, which puts GEMM1's output directly in the
+// range of GEMM2's f16 operands; only scales below ~2^-12 of the tile's
+// largest lose low bits to f16 subnormals.  The output is rescaled exactly.
 //
 // Data flow per tile (per wave):
 //   1. each lane reads one 64-bit bitmap row; a wave prefix sum gives every
@@ -51,6 +55,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Global-address-space views.  Pointers read from LDS are generic; memory
 // operations through them would be flat instructions, whose completion also
@@ -79,13 +84,29 @@ __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
     return __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_xor(v, d);
-        v = v > o ? v : o;
-    }
+// Inclusive prefix sum over the 64 lanes with DPP row shifts (1, 2, 4, 8
+// within each row of 16 lanes) and the row broadcasts of lanes 15 and 31;
+// lanes whose source lies outside the row keep the 0 passed as `old`.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
     return v;
+}
+
+// Largest value of a 5-bit field over the wave (wave-uniform): a binary
+// search on ballots, one bit at a time from the top.
+__device__ __forceinline__ uint32_t wave_max_u5(uint32_t v) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 4; b >= 0; b--) {
+        const uint32_t c = m | (1u << b);
+        if (__builtin_amdgcn_ballot_w64(v >= c) != 0) m = c;
+    }
+    return m;
 }
 
 // (a, b) -> f16 hi pair and f16 lo pair with a = hi.x + lo.x, b = hi.y + lo.y
@@ -109,6 +130,11 @@ __device__ __forceinline__ uint32_t split1(float x) {
     __asm__("v_fma_mixhi_f16 %0, %1, 1.0, -%0 op_sel_hi:[0,0,1]" : "+v"(v) : "v"(x));
     return v;
 }
+
+// LDS read at an absolute LDS byte address, used as an LDS pointer as is
+// (no base is added to it).
+typedef const uint32_t __attribute__((address_space(3))) lds_u32;
+__device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(size_t)a; }
 
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
@@ -231,13 +257,8 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         // 1. bitmap row `lane`: set-bit count and exclusive prefix over rows
         const uint64_t bits = reinterpret_cast<const uint64_t *>(pay)[lane];
         const uint32_t cnt = (uint32_t)__popcll(bits);
-        uint32_t incl = cnt;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t y = __shfl_up(incl, d);
-            if (lane >= d) incl += y;
-        }
-        const bool ok = __shfl(incl, 63) == k;
+        const uint32_t incl = wave_incl_sum(cnt);
+        const bool ok = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) == k;
         const uint32_t pre = incl - cnt;
 
         // 2. per-tile power-of-two prescale from the largest scale exponent
@@ -247,32 +268,40 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
             const uint32_t ex = ((uint32_t)sc16[g] >> 10) & 31u;
             emax = ex > emax ? ex : emax;
         }
-        emax = wave_max_u32(emax);
+        emax = wave_max_u5(emax);
         // coefficients are scaled by 2^E (|C 2^E| < 4); the basis carries 2^8
         const int E = 13 - (int)emax;
         const float pe = pow2f(E);
 
-        // 3. dense table of the retained coefficients, 4 per lane per pass:
+        // 3. dense table of the retained coefficients, 8 per lane per pass:
         //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E
+        //    exactly.  The scaled scale s = scale * 2^E (11 significant bits)
+        //    is split into s_hi (its top 8 bits) + s_lo (the other 3); with
+        //    |q - 8| <= 8 (at most 3 significant bits) both (q - 8) s_hi and
+        //    (q - 8) s_lo are exact f16 products, formed two at a time by
+        //    packed f16 multiplies.
         if (ok) {
             const uint16_t *nib16 = reinterpret_cast<const uint16_t *>(pay + nib_off);
-            for (uint32_t g4 = lane; 4 * g4 < k; g4 += 64) {
-                const uint32_t r0 = 4 * g4;
-                const uint32_t w4 = nib16[g4];  // nibbles r0 .. r0+3, low first
-                const float s = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
-                const float s8 = -8.0f * s;
-                uint32_t v[4];
-                // (q - 8) * s = fma(q, s, -8 s): exact in f32, one rounding
+            for (uint32_t c8 = lane; 8 * c8 < k; c8 += 64) {
+                const uint32_t r0 = 8 * c8;
+                // nibbles r0 .. r0+7, low first (bytes past the tile's end
+                // are staged slack; their entries lie past V[k - 1])
+                const uint32_t n32 = (uint32_t)nib16[2 * c8] | ((uint32_t)nib16[2 * c8 + 1] << 16);
+                const float sf = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
+                const float shi = __uint_as_float(__float_as_uint(sf) & 0xffff0000u);
+                const half2v sc = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(shi, sf - shi));
+                uint32_t v[8];
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    v[e] = split1(__builtin_fmaf((float)((w4 >> (4 * e)) & 15u), s, s8));
-                if (r0 + 4 <= k) {
-                    *reinterpret_cast<u32x4 *>(V + r0) = u32x4{v[0], v[1], v[2], v[3]};
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        if (r0 + e < k) V[r0 + e] = v[e];
+                for (int e = 0; e < 4; e++) {
+                    // f16 (1024 + q) for nibbles e and e + 4, minus 1032
+                    const uint32_t y = ((n32 >> (4 * e)) & 0x000f000fu) | 0x64006400u;
+                    const half2v q = __builtin_bit_cast(half2v, y) - half2v{(_Float16)1032.0f, (_Float16)1032.0f};
+                    v[e] = __builtin_bit_cast(uint32_t, half2v{q.x, q.x} * sc);
+                    v[e + 4] = __builtin_bit_cast(uint32_t, half2v{q.y, q.y} * sc);
                 }
+                u32x4 *dst = reinterpret_cast<u32x4 *>(V + r0);
+                dst[0] = u32x4{v[0], v[1], v[2], v[3]};
+                dst[1] = u32x4{v[4], v[5], v[6], v[7]};
             }
         }
         wave_sync();
@@ -322,7 +351,7 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
                     // a table entry is f16 hi | f16 lo << 16
                     uint32_t w[8];
 #pragma unroll
-                    for (int o = 0; o < 8; o++) w[o] = *reinterpret_cast<const uint32_t *>(smem + a[o]);
+                    for (int o = 0; o < 8; o++) w[o] = lds_load(a[o]);
 #pragma unroll
                     for (int vp = 0; vp < 2; vp++) {
                         ahi[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
@@ -342,6 +371,7 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
                     acc[up][vp] = mfma(ahi[vp][s], mh, acc[up][vp]);
                     acc[up][vp] = mfma(ahi[vp][s], ml, acc[up][vp]);
                     acc[up][vp] = mfma(alo[vp][s], mh, acc[up][vp]);
+                    acc[up][vp] = mfma(alo[vp][s], ml, acc[up][vp]);
                 }
             }
         }
@@ -488,7 +518,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         // per wave: the V table (k words) shares space with the parked output
         // tile; the staged tile bytes follow (2 bytes of slack for the last
         // 16-bit nibble read)
-        const uint32_t vbytes = 4 * max_k;
+        const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);  // whole 8-entry groups
         const uint32_t obytes = 64 * 64 * (dtype == HH_F32 ? 4u : 2u);
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
         B.wave_lds = B.vo_bytes + 16u * 64u * kMaxPrefetch;
