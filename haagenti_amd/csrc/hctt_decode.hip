@@ -110,25 +110,40 @@ __device__ __forceinline__ uint32_t wave_max_u5(uint32_t v) {
 }
 
 // (a, b) -> f16 hi pair and f16 lo pair with a = hi.x + lo.x, b = hi.y + lo.y
-// to ~2^-20 relative (exactly when a, b have at most 21 significant bits).
-// The lo halves come from mixed-precision FMAs that read the f16 hi halves
-// in place: lo = round_f16(a * 1 - hi), computed exactly in f32 first.
-__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-    uint32_t l;
-    __asm__("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l) : "v"(a), "v"(hi));
-    __asm__("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-            : "+v"(l)
-            : "v"(b), "v"(hi));
-    lo = l;
+// to ~2^-20 relative (exactly when a, b have at most 21 significant bits):
+// lo = round_f16(a * one - hi), where a - hi is exact in f32.  `one` is 1.0
+// passed in at run time, so the compiler keeps the FMA and selects the
+// mixed-precision FMAs (v_fma_mixlo/hi_f16, one instruction per lo half)
+// itself; it then also inserts the wait states an MFMA needs before reading
+// their results (inline assembly would hide those writes from it).
+__device__ __forceinline__ void split2(float a, float b, float one, uint32_t &hi, uint32_t &lo) {
+    const half2v h = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+    const half2v l = {(_Float16)__builtin_fmaf(a, one, -(float)h.x), (_Float16)__builtin_fmaf(b, one, -(float)h.y)};
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
 }
 
-// x -> f16 hi in bits 0..15 and f16 lo = round_f16(x - hi) in bits 16..31 of
-// one register (the table entry format of the retained coefficients).
-__device__ __forceinline__ uint32_t split1(float x) {
-    uint32_t v = __builtin_bit_cast(uint16_t, (_Float16)x);
-    __asm__("v_fma_mixhi_f16 %0, %1, 1.0, -%0 op_sel_hi:[0,0,1]" : "+v"(v) : "v"(x));
-    return v;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef u32x4 __attribute__((address_space(3))) lds_u32x4;
+typedef u32x2 __attribute__((address_space(3))) lds_u32x2;
+
+// Row pitch of the parked output tile in LDS: 64 values plus 8 (16-bit) or
+// 4 (f32) values of padding, so that the 32 rows written by one instruction
+// fall into distinct banks.
+template <int DT>
+constexpr uint32_t kParkPitch = DT == HH_F32 ? 64u * 4u + 16u : 64u * 2u + 8u;
+
+// Two outputs rounded to the 16-bit output type, packed low | high.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (DT == HH_BF16) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
+    } else {
+        // keep the f32 values as such: a fused fma -> f16 (v_fma_mix) would
+        // round once from the exact result, not from the f32 output
+        __asm__("" : "+v"(a), "+v"(b));
+        return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+    }
 }
 
 // LDS read at an absolute LDS byte address, used as an LDS pointer as is
@@ -153,6 +168,8 @@ struct TileBatch {
     uint32_t n;
     uint32_t wave_lds;  // per-wave LDS bytes: V/output union + staged tile bytes
     uint32_t vo_bytes;  // size of the V/output union
+    float one;          // 1.0 and -4, as run-time values (see split2 and the gather)
+    int32_t neg4;
 };
 
 // Workgroup LDS layout: [zero word][batch descriptor][M fragment table][per-wave areas].
@@ -220,6 +237,8 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
     if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
     const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem + kBatchOff);
+    const float one = Bk.one;                 // 1.0
+    const int32_t n4 = (int32_t)(int8_t)Bk.neg4;  // -4, known to fit 24 bits
     const uint32_t wbase = kSharedBytes + wave * B.wave_lds;  // byte offset of this wave's area
     const uint32_t pbase = wbase + B.vo_bytes;                // staged tile bytes
     uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
@@ -341,7 +360,7 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
                         // all-ones when column 16 run + o of the word is retained
                         const int32_t m = (int32_t)(word << (31 - (16 * run + o))) >> 31;
                         a[o] = (uint32_t)m & diff;
-                        __asm__("v_mad_i32_i24 %0, %1, -4, %0" : "+v"(diff) : "v"(m));
+                        diff = (uint32_t)((int32_t)diff + m * n4);  // v_mad_i32_i24
                     }
                     // columns 16 run + 8 .. 16 run + 15 of this word belong to the
                     // other lane half
@@ -377,11 +396,30 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         }
         wave_sync();
 
-        // 6-7. per output column block jb (jb = 0: j = n; jb = 1: j = 63 - n):
-        //    B = S rows of parity upar; GEMM2 X[i][j] = sum_u M[u][i] S[u][j]
-        //    split by u parity into E2 (upar 0) and O2 (upar 1); then
-        //    X[i][j] = E2 + O2, X[63 - i][j] = E2 - O2; park in LDS.
+        // 6. butterfly in place: acc[upar][0] = E + O = S[u][n],
+        //    acc[upar][1] = E - O = S[u][63 - n]
+#pragma unroll
+        for (int up = 0; up < 2; up++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float e = acc[up][0][r], o = acc[up][1][r];
+                acc[up][0][r] = e + o;
+                acc[up][1][r] = e - o;
+            }
+        }
+
+        // 7. GEMM2 transposed, per S column block jb (jb = 0: j = n;
+        //    jb = 1: j = 63 - n): X^T[j][i] = sum_u S[u][j] M[u][i], with S
+        //    (GEMM1's accumulators) as the A operand and the M fragments as B,
+        //    split by u parity into E2 (upar 0) and O2 (upar 1).  Lane l32 then
+        //    holds output rows i = l32 and 63 - i (X[63 - i][j] = E2 - O2) and
+        //    register r the column j = (r & 3) + 8 (r >> 2) + 4 h (or 63 minus
+        //    it): four consecutive columns per register quad, parked in LDS as
+        //    one 8-byte (16-bit outputs) or 16-byte (f32) write per row.
         const float os = pow2f(-(E + 16));
+        const uint32_t i_lo = wbase + (uint32_t)l32 * kParkPitch<DT>;
+        const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * kParkPitch<DT>;
+        constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
 #pragma unroll
         for (int jb = 0; jb < 2; jb++) {
             floatx16 x2[2];
@@ -391,61 +429,44 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
             for (int up = 0; up < 2; up++) {
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
-                    u32x4 bhi, blo;
+                    u32x4 shi, slo;
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
-                        const int r0 = 8 * s + 2 * p, r1 = r0 + 1;
+                        const int r0 = 8 * s + 2 * p;
                         uint32_t hp, lp;
-                        if (jb == 0)
-                            split2(acc[up][0][r0] + acc[up][1][r0], acc[up][0][r1] + acc[up][1][r1], hp, lp);
-                        else
-                            split2(acc[up][0][r0] - acc[up][1][r0], acc[up][0][r1] - acc[up][1][r1], hp, lp);
-                        bhi[p] = hp;
-                        blo[p] = lp;
+                        split2(acc[up][jb][r0], acc[up][jb][r0 + 1], one, hp, lp);
+                        shi[p] = hp;
+                        slo[p] = lp;
                     }
                     const u32x4 mh = mtab[((0 * 2 + up) * 2 + s) * 64 + lane];
                     const u32x4 ml = mtab[((1 * 2 + up) * 2 + s) * 64 + lane];
-                    x2[up] = mfma(mh, bhi, x2[up]);
-                    x2[up] = mfma(ml, bhi, x2[up]);
-                    x2[up] = mfma(mh, blo, x2[up]);
+                    x2[up] = mfma(shi, mh, x2[up]);
+                    x2[up] = mfma(shi, ml, x2[up]);
+                    x2[up] = mfma(slo, mh, x2[up]);
                 }
             }
-            // park rows i = (r&3) + 8 (r>>2) + 4 h and 63 - i, column j
-            const int j = jb == 0 ? l32 : 63 - l32;
-            if constexpr (DT == HH_F32) {
-                float *xs = reinterpret_cast<float *>(smem + wbase);
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int i = (r & 3) + 8 * (r >> 2) + 4 * h;
+            for (int q = 0; q < 4; q++) {
+                float va[4], vc[4];  // rows i and 63 - i, columns ascending
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int r = 4 * q + (jb == 0 ? t : 3 - t);
                     const float o2 = x2[1][r] * os;
-                    xs[i * 64 + j] = __builtin_fmaf(x2[0][r], os, o2);
-                    xs[(63 - i) * 64 + j] = __builtin_fmaf(x2[0][r], os, -o2);
+                    va[t] = __builtin_fmaf(x2[0][r], os, o2);
+                    vc[t] = __builtin_fmaf(x2[0][r], os, -o2);
                 }
-            } else {
-                uint16_t *xs = reinterpret_cast<uint16_t *>(smem + wbase);
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float o0 = x2[1][r] * os, o1 = x2[1][r + 1] * os;
-                    const float a = __builtin_fmaf(x2[0][r], os, o0), b = __builtin_fmaf(x2[0][r + 1], os, o1);
-                    const float c = __builtin_fmaf(x2[0][r], os, -o0), d = __builtin_fmaf(x2[0][r + 1], os, -o1);
-                    uint32_t pk, pm;
-                    if constexpr (DT == HH_BF16) {
-                        pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
-                        pm = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{c, d}, bf16x2));
-                    } else {
-                        // keep the f32 values as such: a fused fma -> f16
-                        // (v_fma_mix) would round once from the exact result,
-                        // not from the f32 output
-                        float fa = a, fb = b, fc = c, fd = d;
-                        __asm__("" : "+v"(fa), "+v"(fb), "+v"(fc), "+v"(fd));
-                        pk = f32_to_f16_bits(fa) | (f32_to_f16_bits(fb) << 16);
-                        pm = f32_to_f16_bits(fc) | (f32_to_f16_bits(fd) << 16);
-                    }
-                    const int i0 = (r & 3) + 8 * (r >> 2) + 4 * h;  // rows i0, i0 + 1
-                    xs[i0 * 64 + j] = (uint16_t)pk;
-                    xs[(i0 + 1) * 64 + j] = (uint16_t)(pk >> 16);
-                    xs[(63 - i0) * 64 + j] = (uint16_t)pm;
-                    xs[(62 - i0) * 64 + j] = (uint16_t)(pm >> 16);
+                // first of the four columns
+                const uint32_t j0 = jb == 0 ? 8 * q + 4 * h : 60 - 8 * q - 4 * h;
+                if constexpr (DT == HH_F32) {
+                    *(lds_u32x4 *)(size_t)(i_lo + esz * j0) =
+                        u32x4{__float_as_uint(va[0]), __float_as_uint(va[1]), __float_as_uint(va[2]),
+                              __float_as_uint(va[3])};
+                    *(lds_u32x4 *)(size_t)(i_hi + esz * j0) =
+                        u32x4{__float_as_uint(vc[0]), __float_as_uint(vc[1]), __float_as_uint(vc[2]),
+                              __float_as_uint(vc[3])};
+                } else {
+                    *(lds_u32x2 *)(size_t)(i_lo + esz * j0) = u32x2{pack2<DT>(va[0], va[1]), pack2<DT>(va[2], va[3])};
+                    *(lds_u32x2 *)(size_t)(i_hi + esz * j0) = u32x2{pack2<DT>(vc[0], vc[1]), pack2<DT>(vc[2], vc[3])};
                 }
             }
         }
@@ -461,22 +482,22 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         const uint32_t tr = t / tpr, tc = t % tpr;
         const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
         if constexpr (DT == HH_F32) {
-            const float *xs = reinterpret_cast<const float *>(smem + wbase);
             float HH_GLOBAL *o = (float HH_GLOBAL *)B.out[ti] + base;
 #pragma unroll
             for (int it = 0; it < 16; it++) {
                 const int row = 4 * it + (lane >> 4), c4 = (lane & 15) * 4;
                 *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c4) =
-                    *reinterpret_cast<const u32x4 *>(xs + row * 64 + c4);
+                    *(lds_u32x4 *)(size_t)(wbase + row * kParkPitch<DT> + 4 * c4);
             }
         } else {
-            const uint16_t *xs = reinterpret_cast<const uint16_t *>(smem + wbase);
             uint16_t HH_GLOBAL *o = (uint16_t HH_GLOBAL *)B.out[ti] + base;
 #pragma unroll
             for (int it = 0; it < 8; it++) {
                 const int row = 8 * it + (lane >> 3), c8 = (lane & 7) * 8;
-                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c8) =
-                    *reinterpret_cast<const u32x4 *>(xs + row * 64 + c8);
+                // rows are 8-byte aligned in the park: two 8-byte reads
+                const uint32_t a0 = wbase + row * kParkPitch<DT> + 2 * c8;
+                const u32x2 lo = *(lds_u32x2 *)(size_t)a0, hi = *(lds_u32x2 *)(size_t)(a0 + 8);
+                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c8) = u32x4{lo[0], lo[1], hi[0], hi[1]};
             }
         }
         if (B.status[ti] != nullptr && lane == 0)
@@ -515,11 +536,13 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         }
         if (B.n == 0) continue;
         B.start[B.n] = total;
+        B.one = 1.0f;
+        B.neg4 = -4;
         // per wave: the V table (k words) shares space with the parked output
         // tile; the staged tile bytes follow (2 bytes of slack for the last
         // 16-bit nibble read)
         const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);  // whole 8-entry groups
-        const uint32_t obytes = 64 * 64 * (dtype == HH_F32 ? 4u : 2u);
+        const uint32_t obytes = 64 * (dtype == HH_F32 ? kParkPitch<HH_F32> : kParkPitch<HH_BF16>);
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
         B.wave_lds = B.vo_bytes + 16u * 64u * kMaxPrefetch;
         const uint32_t lds = kSharedBytes + B.wave_lds * kWaves;
