@@ -155,6 +155,10 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
 constexpr int kMaxTensors = 8;
 constexpr int kMaxPrefetch = 3;  // 16-byte loads per lane: tiles up to 3 KiB (k <= 4096)
+// Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs on the
+// 4-byte-aligned path with at most 2 KiB of tile bytes prefetched (168
+// registers, no spills; the LDS also fits 3 workgroups per CU), else 2.
+constexpr int kWavesPerSimd(int dt, bool dw, int np) { return dt != HH_F32 && dw && np == 2 ? 3 : 2; }
 struct TileBatch {
     const uint8_t *tiles[kMaxTensors];
     void *out[kMaxTensors];
@@ -185,21 +189,21 @@ constexpr uint32_t kMTabOff = kBatchOff + kBatchBytes;
 constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 
 // Loads the bytes of global tile gt into registers, 16 bytes per lane per
-// KiB, always issuing kMaxPrefetch loads (chunks past the tile end re-read
+// KiB, always issuing NP loads (NP KiB cover the tile) (chunks past the tile end re-read
 // its last 16 bytes) so that the wait counts stay static.  Register chunk i
 // holds tile bytes [16*(lane + 64 i), +16) wherever those lie inside the
 // tile.  DW: every tile of
 // the batch starts 4-byte aligned and has a size divisible by 4 (16-byte
 // loads at 4-byte alignment); otherwise bytes are gathered one by one.
-template <bool DW>
+template <bool DW, int NP>
 __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, int lane,
-                                              u32x4 (&pf)[kMaxPrefetch]) {
+                                              u32x4 (&pf)[NP]) {
     uint32_t ti = 0;
     while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
     const uint32_t tb = B.tb[ti];
     g_u8 *src = (g_u8 *)B.tiles[ti] + (size_t)(gt - B.start[ti]) * tb;
 #pragma unroll
-    for (int i = 0; i < kMaxPrefetch; i++) {
+    for (int i = 0; i < NP; i++) {
         const uint32_t off = 16u * (lane + 64u * i);
         if constexpr (DW) {
             // A chunk reaching past the tile end is read at tb - 16 (tiles
@@ -222,8 +226,8 @@ __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, i
     }
 }
 
-template <int DT, bool DW>
-__global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
+template <int DT, bool DW, int NP>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_decode_kernel(TileBatch Bk,
                                                                    const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -249,12 +253,12 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
     // path of a tile.
     const uint32_t ntiles = B.start[B.n];
     const uint32_t stride = gridDim.x * kWaves;
-    u32x4 pf[kMaxPrefetch];
+    u32x4 pf[NP];
     uint32_t gt = blockIdx.x * kWaves + wave;
     if (gt < ntiles) {
-        prefetch_tile<DW>(B, gt, lane, pf);
+        prefetch_tile<DW, NP>(B, gt, lane, pf);
 #pragma unroll
-        for (int i = 0; i < kMaxPrefetch; i++)
+        for (int i = 0; i < NP; i++)
             *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
     }
     for (; gt < ntiles; gt += stride) {
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
         // and before this tile's output stores are issued (the wait counter
         // is in order, so stores issued earlier would have to drain first).
         const bool has_next = gt + stride < ntiles;
-        prefetch_tile<DW>(B, has_next ? gt + stride : gt, lane, pf);
+        prefetch_tile<DW, NP>(B, has_next ? gt + stride : gt, lane, pf);
         wave_sync();
 
         // 1. bitmap row `lane`: set-bit count and exclusive prefix over rows
@@ -474,7 +478,7 @@ __global__ __launch_bounds__(kThreads, 2) void hctt_decode_kernel(TileBatch Bk,
 
         // stage the next tile's bytes (the current ones are no longer needed)
 #pragma unroll
-        for (int i = 0; i < kMaxPrefetch; i++)
+        for (int i = 0; i < NP; i++)
             *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
 
         // 8. coalesced row stores (16 bytes per lane)
@@ -544,21 +548,34 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);  // whole 8-entry groups
         const uint32_t obytes = 64 * (dtype == HH_F32 ? kParkPitch<HH_F32> : kParkPitch<HH_BF16>);
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
-        B.wave_lds = B.vo_bytes + 16u * 64u * kMaxPrefetch;
+        uint32_t max_tb = 0;
+        for (uint32_t j = 0; j < B.n; j++) max_tb = B.tb[j] > max_tb ? B.tb[j] : max_tb;
+        const int np = max_tb <= 2048u ? 2 : 3;  // KiB of tile bytes prefetched per wave
+        B.wave_lds = B.vo_bytes + 16u * 64u * (uint32_t)np;
         const uint32_t lds = kSharedBytes + B.wave_lds * kWaves;
-        const uint32_t per_cu = (160u * 1024u) / lds >= 2 ? 2u : 1u;
+        // workgroups per CU: what the registers allow, then the LDS
+        uint32_t per_cu = (uint32_t)kWavesPerSimd(dtype, all_dw, np);
+        if (per_cu > (160u * 1024u) / lds) per_cu = (160u * 1024u) / lds;
+        if (per_cu == 0) per_cu = 1;
         uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256) * per_cu;
         const uint32_t need = (total + kWaves - 1) / kWaves;
         if (grid > need) grid = need;
         const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
         hipError_t e = hipSuccess;
-#define HH_LAUNCH2(DTV, DWV)                                                                 \
-    do {                                                                                     \
-        e = hipFuncSetAttribute((const void *)hctt_decode_kernel<DTV, DWV>,                  \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
-        if (e != hipSuccess) return e;                                                       \
-        hipLaunchKernelGGL((hctt_decode_kernel<DTV, DWV>), dim3(grid), dim3(kThreads), lds, \
-                           s, B, basis);                                                     \
+#define HH_LAUNCH3(DTV, DWV, NPV)                                                                 \
+    do {                                                                                          \
+        e = hipFuncSetAttribute((const void *)hctt_decode_kernel<DTV, DWV, NPV>,                  \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);            \
+        if (e != hipSuccess) return e;                                                            \
+        hipLaunchKernelGGL((hctt_decode_kernel<DTV, DWV, NPV>), dim3(grid), dim3(kThreads), lds, \
+                           s, B, basis);                                                          \
+    } while (0)
+#define HH_LAUNCH2(DTV, DWV)             \
+    do {                                 \
+        if (np == 2)                     \
+            HH_LAUNCH3(DTV, DWV, 2);     \
+        else                             \
+            HH_LAUNCH3(DTV, DWV, 3);     \
     } while (0)
 #define HH_LAUNCH(DTV)                  \
     do {                                \
@@ -575,6 +592,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         }
 #undef HH_LAUNCH
 #undef HH_LAUNCH2
+#undef HH_LAUNCH3
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
