@@ -25,6 +25,12 @@
  *                            coefficients, f64 truth within tolerance.
  *   HCT container            byte layout asserted by the reference's tests
  *                            (tensor.rs:1056-1091,1637-1722,2088-2207).
+ *   XXH3-64                  the xxhash library's xxh3_64 on every length
+ *                            0..2048 and longer random inputs (python
+ *                            xxhash, tests/test_oracle_xxh3.py).
+ *   HCT v2 container         the reference's v2 tests (tensor.rs:1250-1440,
+ *                            1943-2060): round trips, corruption detection,
+ *                            quantization metadata, v1 compatibility.
  */
 #define _GNU_SOURCE
 #include "hh_oracle.h"
@@ -1138,4 +1144,306 @@ int hho_hct_read_all_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
 bad_header:
     set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_HEADER, 0, 0, 0);
     return HHO_CORRUPTED_DATA;
+}
+
+/* ======================= XXH3-64, seed 0 ================================= */
+
+/* Default secret of the published XXH3 algorithm (192 bytes). */
+static const uint8_t XXH3_SECRET[192] = {
+    0xb8, 0xfe, 0x6c, 0x39, 0x23, 0xa4, 0x4b, 0xbe, 0x7c, 0x01, 0x81, 0x2c, 0xf7, 0x21, 0xad, 0x1c,
+    0xde, 0xd4, 0x6d, 0xe9, 0x83, 0x90, 0x97, 0xdb, 0x72, 0x40, 0xa4, 0xa4, 0xb7, 0xb3, 0x67, 0x1f,
+    0xcb, 0x79, 0xe6, 0x4e, 0xcc, 0xc0, 0xe5, 0x78, 0x82, 0x5a, 0xd0, 0x7d, 0xcc, 0xff, 0x72, 0x21,
+    0xb8, 0x08, 0x46, 0x74, 0xf7, 0x43, 0x24, 0x8e, 0xe0, 0x35, 0x90, 0xe6, 0x81, 0x3a, 0x26, 0x4c,
+    0x3c, 0x28, 0x52, 0xbb, 0x91, 0xc3, 0x00, 0xcb, 0x88, 0xd0, 0x65, 0x8b, 0x1b, 0x53, 0x2e, 0xa3,
+    0x71, 0x64, 0x48, 0x97, 0xa2, 0x0d, 0xf9, 0x4e, 0x38, 0x19, 0xef, 0x46, 0xa9, 0xde, 0xac, 0xd8,
+    0xa8, 0xfa, 0x76, 0x3f, 0xe3, 0x9c, 0x34, 0x3f, 0xf9, 0xdc, 0xbb, 0xc7, 0xc7, 0x0b, 0x4f, 0x1d,
+    0x8a, 0x51, 0xe0, 0x4b, 0xcd, 0xb4, 0x59, 0x31, 0xc8, 0x9f, 0x7e, 0xc9, 0xd9, 0x78, 0x73, 0x64,
+    0xea, 0xc5, 0xac, 0x83, 0x34, 0xd3, 0xeb, 0xc3, 0xc5, 0x81, 0xa0, 0xff, 0xfa, 0x13, 0x63, 0xeb,
+    0x17, 0x0d, 0xdd, 0x51, 0xb7, 0xf0, 0xda, 0x49, 0xd3, 0x16, 0x55, 0x26, 0x29, 0xd4, 0x68, 0x9e,
+    0x2b, 0x16, 0xbe, 0x58, 0x7d, 0x47, 0xa1, 0xfc, 0x8f, 0xf8, 0xb8, 0xd1, 0x7a, 0xd0, 0x31, 0xce,
+    0x45, 0xcb, 0x3a, 0x8f, 0x95, 0x16, 0x04, 0x28, 0xaf, 0xd7, 0xfb, 0xca, 0xbb, 0x4b, 0x40, 0x7e,
+};
+#define P32_1 0x9E3779B1u
+#define P32_2 0x85EBCA77u
+#define P32_3 0xC2B2AE3Du
+#define P64_1 0x9E3779B185EBCA87ull
+#define P64_2 0xC2B2AE3D27D4EB4Full
+#define P64_3 0x165667B19E3779F9ull
+#define P64_4 0x85EBCA77C2B2AE63ull
+#define P64_5 0x27D4EB2F165667C5ull
+#define PMX1 0x165667919E3779F9ull
+#define PMX2 0x9FB21C651E98DF25ull
+
+static uint64_t x_rd64(const uint8_t *p) { return rd_u64le(p); }
+static uint32_t x_rd32(const uint8_t *p) { return rd_u32le(p); }
+static uint64_t x_rotl(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
+static uint64_t x_fold(uint64_t a, uint64_t b) { /* low ^ high of the 128-bit product */
+    unsigned __int128 m = (unsigned __int128)a * b;
+    return (uint64_t)m ^ (uint64_t)(m >> 64);
+}
+static uint64_t x_avalanche(uint64_t h) { /* XXH3 avalanche */
+    h ^= h >> 37;
+    h *= PMX1;
+    return h ^ (h >> 32);
+}
+static uint64_t x64_avalanche(uint64_t h) { /* XXH64 avalanche */
+    h ^= h >> 33;
+    h *= P64_2;
+    h ^= h >> 29;
+    h *= P64_3;
+    return h ^ (h >> 32);
+}
+static uint64_t x_rrmxmx(uint64_t h, uint64_t len) {
+    h ^= x_rotl(h, 49) ^ x_rotl(h, 24);
+    h *= PMX2;
+    h ^= (h >> 35) + len;
+    h *= PMX2;
+    return h ^ (h >> 28);
+}
+static uint64_t x_mix16(const uint8_t *in, const uint8_t *sec) {
+    return x_fold(x_rd64(in) ^ x_rd64(sec), x_rd64(in + 8) ^ x_rd64(sec + 8));
+}
+/* one 64-byte stripe into the eight accumulators */
+static void x_stripe(uint64_t acc[8], const uint8_t *in, const uint8_t *sec) {
+    for (int i = 0; i < 8; i++) {
+        uint64_t v = x_rd64(in + 8 * i), k = v ^ x_rd64(sec + 8 * i);
+        acc[i ^ 1] += v;
+        acc[i] += (k & 0xffffffffull) * (k >> 32);
+    }
+}
+
+uint64_t hho_xxh3_64(const uint8_t *in, size_t len) {
+    const uint8_t *S = XXH3_SECRET;
+    if (len == 0) return x64_avalanche(x_rd64(S + 56) ^ x_rd64(S + 64));
+    if (len <= 3) {
+        uint32_t c = ((uint32_t)in[0] << 16) | ((uint32_t)in[len >> 1] << 24) |
+                     (uint32_t)in[len - 1] | ((uint32_t)len << 8);
+        return x64_avalanche((uint64_t)c ^ (uint64_t)(x_rd32(S) ^ x_rd32(S + 4)));
+    }
+    if (len <= 8) {
+        uint64_t v = (uint64_t)x_rd32(in + len - 4) + ((uint64_t)x_rd32(in) << 32);
+        return x_rrmxmx(v ^ (x_rd64(S + 8) ^ x_rd64(S + 16)), len);
+    }
+    if (len <= 16) {
+        uint64_t lo = x_rd64(in) ^ (x_rd64(S + 24) ^ x_rd64(S + 32));
+        uint64_t hi = x_rd64(in + len - 8) ^ (x_rd64(S + 40) ^ x_rd64(S + 48));
+        return x_avalanche(len + __builtin_bswap64(lo) + hi + x_fold(lo, hi));
+    }
+    if (len <= 128) {
+        uint64_t acc = len * P64_1;
+        size_t r = (len - 1) / 32; /* pairs of 16-byte mixes from both ends */
+        for (size_t i = 0; i <= r; i++) {
+            acc += x_mix16(in + 16 * i, S + 32 * i);
+            acc += x_mix16(in + len - 16 * (i + 1), S + 32 * i + 16);
+        }
+        return x_avalanche(acc);
+    }
+    if (len <= 240) {
+        uint64_t acc = len * P64_1;
+        for (int i = 0; i < 8; i++) acc += x_mix16(in + 16 * i, S + 16 * i);
+        uint64_t tail = x_mix16(in + len - 16, S + 136 - 17);
+        acc = x_avalanche(acc);
+        for (size_t i = 8; i < len / 16; i++) tail += x_mix16(in + 16 * i, S + 16 * (i - 8) + 3);
+        return x_avalanche(acc + tail);
+    }
+    /* long input: 1 KiB blocks of 16 stripes, scramble after each block */
+    uint64_t acc[8] = {P32_3, P64_1, P64_2, P64_3, P64_4, P32_2, P64_5, P32_1};
+    const size_t block = 64 * 16;
+    size_t nb = (len - 1) / block;
+    for (size_t b = 0; b < nb; b++) {
+        for (int s = 0; s < 16; s++) x_stripe(acc, in + b * block + 64 * s, S + 8 * s);
+        for (int i = 0; i < 8; i++) {
+            uint64_t a = acc[i];
+            a ^= a >> 47;
+            a ^= x_rd64(S + 192 - 64 + 8 * i);
+            acc[i] = a * P32_1;
+        }
+    }
+    size_t ns = ((len - 1) - block * nb) / 64;
+    for (size_t s = 0; s < ns; s++) x_stripe(acc, in + nb * block + 64 * s, S + 8 * s);
+    x_stripe(acc, in + len - 64, S + 192 - 64 - 7);
+    uint64_t r = len * P64_1;
+    for (int i = 0; i < 4; i++)
+        r += x_fold(acc[2 * i] ^ x_rd64(S + 11 + 16 * i), acc[2 * i + 1] ^ x_rd64(S + 11 + 16 * i + 8));
+    return x_avalanche(r);
+}
+
+/* ======================= HCT v2 container ================================ */
+
+#define HCT_INDEX_V2 16u
+
+size_t hho_hct_write_v2_lz4(const uint8_t *data, size_t len, uint32_t block_size,
+                            uint8_t dtype, const uint64_t *shape, int rank, uint16_t flags,
+                            const uint8_t *quant8, uint8_t *out, size_t out_cap) {
+    if (block_size == 0 || rank < 0 || rank > 3) return 0;
+    size_t nblocks = (len + block_size - 1) / block_size;
+    size_t qsz = (flags & HHO_FLAG_QUANTIZATION) ? 8 : 0;
+    /* :809-814: the index is always written with 16-byte v2 entries; the
+     * checksum field is 0 when block checksums are off (:726-733) */
+    size_t data_start = HCT_HEADER + qsz + nblocks * HCT_INDEX_V2;
+    if (data_start > out_cap) return 0;
+    size_t pos = data_start;
+    uint32_t offset = 0;
+    for (size_t b = 0; b < nblocks; b++) {
+        size_t s = b * block_size, e = s + block_size < len ? s + block_size : len;
+        size_t cap = hho_lz4_max_compressed_size(e - s);
+        if (pos + cap > out_cap) return 0;
+        size_t w = 0;
+        hho_err er;
+        if (hho_lz4_compress_block(data + s, e - s, out + pos, cap, &w, &er) != HHO_OK) return 0;
+        uint8_t *ie = out + HCT_HEADER + qsz + b * HCT_INDEX_V2;
+        wr_u32(ie, offset);
+        wr_u32(ie + 4, (uint32_t)w);
+        wr_u64(ie + 8, (flags & HHO_FLAG_BLOCK_CHECKSUMS) ? hho_xxh3_64(out + pos, w) : 0);
+        offset += (uint32_t)w;
+        pos += w;
+    }
+    uint8_t *h = out;
+    memset(h, 0, HCT_HEADER);
+    memcpy(h, "HCTN", 4);
+    wr_u32(h + 4, 2); /* HCT_VERSION_V2 */
+    h[8] = 0;         /* LZ4 */
+    h[9] = dtype;
+    wr_u16(h + 10, flags);
+    wr_u64(h + 12, len);
+    wr_u64(h + 20, offset);
+    wr_u32(h + 28, block_size);
+    wr_u32(h + 32, (uint32_t)nblocks);
+    h[36] = (uint8_t)rank;
+    for (int i = 0; i < rank; i++) wr_u64(h + 37 + 8 * i, shape[i]);
+    /* :792-795: XXH3 of bytes 0..56 stored at 56..64 (over dims[2]'s tail) */
+    wr_u64(h + 56, hho_xxh3_64(h, 56));
+    if (qsz) memcpy(h + HCT_HEADER, quant8, 8);
+    return pos;
+}
+
+/* HctReaderV2::new (:841-920): header, header checksum, quantization
+ * metadata, index entry size and data offset. */
+static int v2_open(const uint8_t *file, size_t file_len, hho_err *err, uint64_t *original,
+                   uint32_t *block_size, uint32_t *nblocks, size_t *index_at, size_t *entry,
+                   size_t *data_at) {
+    if (file_len < HCT_HEADER) {
+        set_err(err, HHO_ALGORITHM, 0, file_len, 0, 0);
+        return HHO_ALGORITHM;
+    }
+    if (memcmp(file, "HCTN", 4) != 0) goto bad_header;
+    uint32_t ver = rd_u32le(file + 4);
+    if (ver > 2 || file[8] > 1 || file[9] > 4 || file[36] > 3) goto bad_header;
+    uint16_t flags = (uint16_t)(file[10] | (file[11] << 8));
+    if (ver >= 2 && (flags & HHO_FLAG_HEADER_CHECKSUM) &&
+        hho_xxh3_64(file, 56) != rd_u64le(file + 56)) {
+        set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_HEADER_CHECKSUM, 0, 0, 0);
+        return HHO_CORRUPTED_DATA;
+    }
+    size_t at = HCT_HEADER;
+    if (flags & HHO_FLAG_QUANTIZATION) {
+        if (file_len < at + 8) {
+            set_err(err, HHO_ALGORITHM, 0, file_len, 0, 0);
+            return HHO_ALGORITHM;
+        }
+        if (file[at] > 4) {
+            set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_QUANT_SCHEME, 0, 0, 0);
+            return HHO_CORRUPTED_DATA;
+        }
+        at += 8;
+    }
+    *entry = (ver >= 2 && (flags & HHO_FLAG_BLOCK_CHECKSUMS)) ? HCT_INDEX_V2 : HCT_INDEX_ENTRY;
+    *original = rd_u64le(file + 12);
+    *block_size = rd_u32le(file + 28);
+    *nblocks = rd_u32le(file + 32);
+    *index_at = at;
+    *data_at = at + (size_t)*nblocks * *entry;
+    if (*data_at > file_len) {
+        set_err(err, HHO_ALGORITHM, 0, file_len, 0, 0);
+        return HHO_ALGORITHM;
+    }
+    return HHO_OK;
+bad_header:
+    set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_HEADER, 0, 0, 0);
+    return HHO_CORRUPTED_DATA;
+}
+
+/* read_block_validated (:937-977): range, then checksum when non-zero */
+static int v2_block(const uint8_t *file, size_t file_len, size_t index_at, size_t entry,
+                    size_t data_at, uint32_t b, hho_err *err, const uint8_t **blk, uint32_t *csz) {
+    const uint8_t *ie = file + index_at + (size_t)b * entry;
+    uint32_t off = rd_u32le(ie);
+    *csz = rd_u32le(ie + 4);
+    uint64_t sum = entry == HCT_INDEX_V2 ? rd_u64le(ie + 8) : 0;
+    if (data_at + (size_t)off + *csz > file_len) {
+        set_err(err, HHO_ALGORITHM, 0, file_len, 0, 0);
+        return HHO_ALGORITHM;
+    }
+    *blk = file + data_at + off;
+    if (sum != 0 && hho_xxh3_64(*blk, *csz) != sum) {
+        set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_BLOCK_CHECKSUM, 0, 0, 0);
+        return HHO_CORRUPTED_DATA;
+    }
+    return HHO_OK;
+}
+
+int hho_hct_read_all_v2_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
+                            size_t out_cap, size_t *written, hho_err *err,
+                            int64_t *failed_block) {
+    set_err(err, HHO_OK, 0, 0, 0, 0);
+    if (failed_block) *failed_block = -1;
+    uint64_t original;
+    uint32_t block_size, nblocks;
+    size_t index_at, entry, data_at;
+    int rc = v2_open(file, file_len, err, &original, &block_size, &nblocks, &index_at, &entry,
+                     &data_at);
+    if (rc != HHO_OK) return rc;
+    size_t op = 0;
+    for (uint32_t b = 0; b < nblocks; b++) {
+        if (failed_block) *failed_block = b;
+        const uint8_t *blk;
+        uint32_t csz;
+        rc = v2_block(file, file_len, index_at, entry, data_at, b, err, &blk, &csz);
+        if (rc != HHO_OK) return rc;
+        uint64_t expected;
+        if (b == nblocks - 1) { /* :988-994 */
+            uint64_t full = (uint64_t)(nblocks - 1) * block_size;
+            if (full > original) {
+                set_err(err, HHO_CORRUPTED_DATA, HHO_CORRUPT_SIZE, 0, 0, 0);
+                return HHO_CORRUPTED_DATA;
+            }
+            expected = original - full;
+        } else {
+            expected = block_size;
+        }
+        if (op + expected > out_cap) {
+            set_err(err, HHO_BUFFER_TOO_SMALL, 0, 0, op + expected, out_cap);
+            return HHO_BUFFER_TOO_SMALL;
+        }
+        memset(out + op, 0, expected);
+        size_t w = 0;
+        rc = hho_lz4_decompress_block(blk, csz, out + op, expected, expected, &w, err);
+        if (rc != HHO_OK) return rc;
+        op += w;
+    }
+    if (failed_block) *failed_block = -1;
+    if (written) *written = op;
+    return HHO_OK;
+}
+
+int hho_hct_validate_v2(const uint8_t *file, size_t file_len, hho_err *err,
+                        int64_t *failed_block) {
+    set_err(err, HHO_OK, 0, 0, 0, 0);
+    if (failed_block) *failed_block = -1;
+    uint64_t original;
+    uint32_t block_size, nblocks;
+    size_t index_at, entry, data_at;
+    int rc = v2_open(file, file_len, err, &original, &block_size, &nblocks, &index_at, &entry,
+                     &data_at);
+    if (rc != HHO_OK) return rc;
+    for (uint32_t b = 0; b < nblocks; b++) {
+        const uint8_t *blk;
+        uint32_t csz;
+        rc = v2_block(file, file_len, index_at, entry, data_at, b, err, &blk, &csz);
+        if (rc != HHO_OK) {
+            if (failed_block) *failed_block = b;
+            return rc;
+        }
+    }
+    return HHO_OK;
 }

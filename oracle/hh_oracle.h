@@ -40,6 +40,9 @@ enum {
     HHO_CORRUPT_BITMAP_COUNT = 3,     /* compressive.rs:630-636 popcount != k */
     HHO_CORRUPT_HEADER = 4,           /* tensor.rs:311-331 magic/version/algo/dtype */
     HHO_CORRUPT_SIZE = 5,             /* size/shape inconsistencies in containers */
+    HHO_CORRUPT_HEADER_CHECKSUM = 6,  /* tensor.rs:857-865 "header checksum mismatch" */
+    HHO_CORRUPT_BLOCK_CHECKSUM = 7,   /* tensor.rs:965-974 "block N checksum mismatch" */
+    HHO_CORRUPT_QUANT_SCHEME = 8,     /* tensor.rs:158-173 "unknown quantization scheme" */
 };
 
 typedef struct hho_err {
@@ -152,6 +155,34 @@ size_t hho_hct_write_lz4(const uint8_t *data, size_t len, uint32_t block_size,
  * output into out (capacity out_cap) and *written. */
 int hho_hct_read_all_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
                          size_t out_cap, size_t *written, hho_err *err);
+
+/* ---------------- XXH3-64 (xxhash-rust 0.8.15 xxh3_64, seed 0) ----------
+ * Call sites: tensor.rs:729,794,858,967.  Restated from the published XXH3
+ * algorithm (xxHash 0.8: default 192-byte secret, 0-16 / 17-128 / 129-240 /
+ * long-input paths); pinned against the xxhash library's outputs. */
+uint64_t hho_xxh3_64(const uint8_t *data, size_t len);
+
+/* ---------------- HCT v2 container (tensor.rs:45-271, 676-1021) ---------- */
+
+#define HHO_FLAG_HEADER_CHECKSUM 0x0001u
+#define HHO_FLAG_BLOCK_CHECKSUMS 0x0002u
+#define HHO_FLAG_QUANTIZATION 0x0004u
+
+/* HctWriterV2 (:679-829) with the LZ4 compressor: flags as given (the
+ * writer's default is HEADER_CHECKSUM | BLOCK_CHECKSUMS); quant8 is the
+ * 8-byte QuantizationMetadata (:195-226) written when flags has
+ * QUANTIZATION.  Returns bytes written or 0 on error. */
+size_t hho_hct_write_v2_lz4(const uint8_t *data, size_t len, uint32_t block_size,
+                            uint8_t dtype, const uint64_t *shape, int rank, uint16_t flags,
+                            const uint8_t *quant8, uint8_t *out, size_t out_cap);
+/* HctReaderV2::new + decompress_all_validated (:840-1012).  *failed_block
+ * receives the index of the failing block, or -1 when the header stage fails. */
+int hho_hct_read_all_v2_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
+                            size_t out_cap, size_t *written, hho_err *err,
+                            int64_t *failed_block);
+/* HctReaderV2::new + validate_checksums (:1014-1020). */
+int hho_hct_validate_v2(const uint8_t *file, size_t file_len, hho_err *err,
+                        int64_t *failed_block);
 
 #ifdef __cplusplus
 }

@@ -92,6 +92,16 @@ def lib():
         L.hho_hct_write_lz4.argtypes = [u8p, sz, C.c_uint32, C.c_uint8, u8p, C.c_int, u8p, sz]
         L.hho_hct_read_all_lz4.restype = C.c_int
         L.hho_hct_read_all_lz4.argtypes = [u8p, sz, u8p, sz, C.POINTER(sz), C.POINTER(Err)]
+        L.hho_xxh3_64.restype = C.c_uint64
+        L.hho_xxh3_64.argtypes = [u8p, sz]
+        L.hho_hct_write_v2_lz4.restype = sz
+        L.hho_hct_write_v2_lz4.argtypes = [u8p, sz, C.c_uint32, C.c_uint8, u8p, C.c_int, C.c_uint16,
+                                           u8p, u8p, sz]
+        L.hho_hct_read_all_v2_lz4.restype = C.c_int
+        L.hho_hct_read_all_v2_lz4.argtypes = [u8p, sz, u8p, sz, C.POINTER(sz), C.POINTER(Err),
+                                              C.POINTER(C.c_int64)]
+        L.hho_hct_validate_v2.restype = C.c_int
+        L.hho_hct_validate_v2.argtypes = [u8p, sz, C.POINTER(Err), C.POINTER(C.c_int64)]
         _lib = L
     return _lib
 
@@ -325,6 +335,49 @@ def hct_read_all_lz4(file_bytes, out_cap):
     e = Err()
     rc = lib().hho_hct_read_all_lz4(_p(f), f.size, _p(out), out_cap, C.byref(w), C.byref(e))
     return (out[:w.value].tobytes() if rc == OK else None), e
+
+
+FLAG_HEADER_CHECKSUM, FLAG_BLOCK_CHECKSUMS, FLAG_QUANTIZATION = 1, 2, 4
+CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8
+
+
+def xxh3_64(data):
+    d = _u8(data)
+    return int(lib().hho_xxh3_64(_p(d), d.size))
+
+
+def hct_write_v2_lz4(data, block_size, dtype, shape,
+                     flags=FLAG_HEADER_CHECKSUM | FLAG_BLOCK_CHECKSUMS, quant8=None):
+    d = _u8(data)
+    nblocks = (d.size + block_size - 1) // block_size
+    cap = 64 + 8 + 16 * nblocks + sum(lz4_max_compressed_size(min(block_size, d.size - i * block_size))
+                                      for i in range(nblocks))
+    out = np.zeros(cap, dtype=np.uint8)
+    shp = np.ascontiguousarray(shape, dtype=np.uint64)
+    q = _u8(quant8 if quant8 is not None else bytes(8))
+    n = lib().hho_hct_write_v2_lz4(_p(d), d.size, block_size, dtype, _p(shp), len(shape), flags,
+                                   _p(q), _p(out), cap)
+    return out[:n].tobytes() if n else None
+
+
+def hct_read_all_v2_lz4(file_bytes, out_cap):
+    """Returns (data or None, err, failed_block)."""
+    f = _u8(file_bytes)
+    out = np.zeros(max(out_cap, 1), dtype=np.uint8)
+    w = C.c_size_t(0)
+    e = Err()
+    fb = C.c_int64(-1)
+    rc = lib().hho_hct_read_all_v2_lz4(_p(f), f.size, _p(out), out_cap, C.byref(w), C.byref(e),
+                                       C.byref(fb))
+    return (out[:w.value].tobytes() if rc == OK else None), e, fb.value
+
+
+def hct_validate_v2(file_bytes):
+    f = _u8(file_bytes)
+    e = Err()
+    fb = C.c_int64(-1)
+    lib().hho_hct_validate_v2(_p(f), f.size, C.byref(e), C.byref(fb))
+    return e, fb.value
 
 
 # ---------------------------------------------------------------- reference C decoder
