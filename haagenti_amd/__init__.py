@@ -105,11 +105,26 @@ class HctInfo(C.Structure):
     _fields_ = [("version", C.c_uint32), ("algorithm", C.c_uint8), ("dtype", C.c_uint8),
                 ("flags", C.c_uint16), ("original_size", C.c_uint64),
                 ("compressed_size", C.c_uint64), ("block_size", C.c_uint32),
-                ("num_blocks", C.c_uint32), ("rank", C.c_uint32), ("pad", C.c_uint32),
+                ("num_blocks", C.c_uint32), ("rank", C.c_uint32), ("index_entry_size", C.c_uint32),
                 ("shape", C.c_uint64 * 4), ("data_offset", C.c_uint64)]
 
 
+class HctQuant(C.Structure):
+    """hh_hct_quant: QuantizationMetadata of HCT v2 (tensor.rs:180-226)."""
+    _fields_ = [("present", C.c_uint8), ("scheme", C.c_uint8), ("has_per_group_scales", C.c_uint8),
+                ("zero_point", C.c_int8), ("scale_bits", C.c_uint16), ("pad", C.c_uint16),
+                ("group_size", C.c_uint32)]
+
+
 _sig("hh_hct_read_header", _i32, [_vp, _sz, C.POINTER(HctInfo), C.POINTER(BlockStatus)])
+_sig("hh_hct_read_header_v2", _i32, [_vp, _sz, C.POINTER(HctInfo), C.POINTER(HctQuant),
+                                      C.POINTER(BlockStatus)])
+_sig("hh_hct_decompress_all_validated", _i32, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_sz),
+                                                C.POINTER(BlockStatus), C.POINTER(C.c_int64), _vp])
+_sig("hh_hct_validate_checksums", _i32, [_vp, _vp, _vp, _sz, C.POINTER(BlockStatus),
+                                          C.POINTER(C.c_int64), _vp])
+_sig("hh_xxh3_64", C.c_uint64, [_vp, _sz])
+_sig("hh_xxh3_64_batch", _i32, [_vp, _vp, _sz, _vp, _vp, _u32, _vp, _vp])
 _sig("hh_hct_decompress_all", _i32, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_sz),
                                       C.POINTER(BlockStatus), C.POINTER(C.c_int64), _vp])
 
@@ -122,7 +137,18 @@ EXPORTS = [
     "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
     "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_encode",
     "hh_hct_read_header", "hh_hct_decompress_all",
+    "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
+    "hh_hct_validate_checksums",
 ]
+
+CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8
+FLAG_HEADER_CHECKSUM, FLAG_BLOCK_CHECKSUMS, FLAG_QUANTIZATION = 0x0001, 0x0002, 0x0004
+
+
+def xxh3_64(data):
+    """xxhash_rust::xxh3::xxh3_64 (seed 0) on host bytes (hh_xxh3_64)."""
+    b = bytes(data)
+    return int(_lib.hh_xxh3_64(b, len(b)))
 
 
 def lib():
@@ -212,6 +238,11 @@ class HipContext:
         return _lib.hh_lz4_decompress_batch(
             self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), _addr(d_out),
             _addr(d_out_off), _addr(d_out_cap), int(nblocks), _addr(d_status), stream)
+
+    def xxh3_64_batch(self, d_data, data_len, d_off, d_len, n, d_out, stream=None):
+        """XXH3-64 of n device buffers in one launch (hh_xxh3_64_batch)."""
+        _check(_lib.hh_xxh3_64_batch(self._p, _addr(d_data), int(data_len), _addr(d_off), _addr(d_len),
+                                     int(n), _addr(d_out), stream), "hh_xxh3_64_batch")
 
     def dequant_int4(self, d_q, q_len, n, d_out, dtype=F32, stream=None):
         produced = _sz(0)
@@ -325,6 +356,153 @@ class HctReader:
             e.failed_block = fb.value
             raise e
         return written.value, d_out
+
+
+class HctReaderV2(HctReader):
+    """HctReaderV2 (crates/haagenti-hct/src/tensor.rs:832-1021) over an
+    in-memory HCT file: the constructor verifies the header checksum and
+    reads the quantization metadata; read_block_validated() checks a block's
+    XXH3 when its index entry holds one; decompress_all_validated() works
+    block by block through any decompressor, as the reference does;
+    decompress_all_validated_gpu() / validate_checksums_gpu() hash every block
+    in one GPU launch and decode them in one more."""
+
+    def __init__(self, data):
+        self._data = bytes(data)
+        self._info = HctInfo()
+        self._quant = HctQuant()
+        st = BlockStatus()
+        rc = _lib.hh_hct_read_header_v2(self._data, len(self._data), C.byref(self._info),
+                                        C.byref(self._quant), C.byref(st))
+        if rc != OK:
+            raise HaagentiError(rc, "hct v2 header", st)
+
+    def quantization(self):
+        q = self._quant
+        if not q.present:
+            return None
+        return dict(scheme=q.scheme, group_size=q.group_size, scale_bits=q.scale_bits,
+                    zero_point=q.zero_point, has_per_group_scales=bool(q.has_per_group_scales))
+
+    def _entry(self, idx):
+        import struct
+        e = self._info.index_entry_size
+        at = self._info.data_offset - e * self.num_blocks() + e * idx
+        off, csz = struct.unpack_from("<II", self._data, at)
+        sum_ = struct.unpack_from("<Q", self._data, at + 8)[0] if e == 16 else 0
+        return self._info.data_offset + off, csz, sum_
+
+    def read_block(self, idx):
+        return self.read_block_validated(idx)
+
+    def read_block_validated(self, idx):
+        if idx >= self.num_blocks():
+            raise HaagentiError(CORRUPTED_DATA, f"block index out of range: {idx} >= {self.num_blocks()}")
+        start, csz, sum_ = self._entry(idx)
+        if start + csz > len(self._data):
+            raise HaagentiError(ALGORITHM, f"failed to read block {idx}")
+        buf = self._data[start:start + csz]
+        if sum_ != 0:
+            got = xxh3_64(buf)
+            if got != sum_:
+                raise HaagentiError(CORRUPTED_DATA, f"block {idx} checksum mismatch: expected "
+                                                    f"{sum_:016x}, got {got:016x}")
+        return buf
+
+    def decompress_block_validated(self, idx, decompressor):
+        return self.decompress_block(idx, decompressor)
+
+    def decompress_all_validated(self, decompressor):
+        return self.decompress_all(decompressor)
+
+    def validate_checksums(self):
+        for i in range(self.num_blocks()):
+            self.read_block_validated(i)
+
+    def _gpu(self, ctx, decode, d_file, d_out, out_cap, stream):
+        import numpy as np
+        import torch
+        if d_file is None:
+            d_file = torch.from_numpy(np.frombuffer(self._data, np.uint8).copy()).cuda()
+        written, st, fb = _sz(0), BlockStatus(), C.c_int64(-1)
+        if decode:
+            if out_cap is None:
+                out_cap = int(self._info.original_size)
+            if d_out is None:
+                d_out = torch.empty(max(out_cap, 1), dtype=torch.uint8, device="cuda")
+            rc = _lib.hh_hct_decompress_all_validated(ctx.handle, self._data, _addr(d_file),
+                                                      len(self._data), _addr(d_out), int(out_cap),
+                                                      C.byref(written), C.byref(st), C.byref(fb), stream)
+        else:
+            rc = _lib.hh_hct_validate_checksums(ctx.handle, self._data, _addr(d_file), len(self._data),
+                                                C.byref(st), C.byref(fb), stream)
+        if rc != OK:
+            e = HaagentiError(rc, f"hct block {fb.value}", st)
+            e.failed_block = fb.value
+            raise e
+        return written.value, d_out
+
+    def decompress_all_validated_gpu(self, ctx, d_file=None, d_out=None, out_cap=None, stream=None):
+        """Every block hashed and decoded on the GPU.  Returns (written, d_out)."""
+        return self._gpu(ctx, True, d_file, d_out, out_cap, stream)
+
+    def validate_checksums_gpu(self, ctx, d_file=None, stream=None):
+        self._gpu(ctx, False, d_file, None, 0, stream)
+
+
+class HctWriterV2:
+    """HctWriterV2 (tensor.rs:679-829), host producer: header (version 2,
+    flags), optional quantization metadata, 16-byte index entries with the
+    XXH3 of each compressed block (0 without block checksums), data."""
+
+    def __init__(self, dtype, shape, block_size=16 * 1024, algorithm=0):
+        self.dtype, self.shape, self.block_size, self.algorithm = dtype, list(shape), block_size, algorithm
+        self.flags = FLAG_HEADER_CHECKSUM | FLAG_BLOCK_CHECKSUMS
+        self.quant = None
+        self.blocks = []
+        self.original_size = 0
+
+    def with_block_size(self, block_size):
+        self.block_size = block_size
+        return self
+
+    def with_quantization(self, scheme, group_size, scale_bits, zero_point=0, has_per_group_scales=False):
+        import struct
+        self.quant = (bytes([scheme, 1 if has_per_group_scales else 0]) + struct.pack("<H", scale_bits)
+                      + struct.pack("<b", zero_point) + int(group_size).to_bytes(4, "little")[:3])
+        self.flags |= FLAG_QUANTIZATION
+        return self
+
+    def without_block_checksums(self):
+        self.flags &= ~FLAG_BLOCK_CHECKSUMS
+        return self
+
+    def add_block(self, compressed, original_len):
+        c = bytes(compressed)
+        self.blocks.append((c, xxh3_64(c) if self.flags & FLAG_BLOCK_CHECKSUMS else 0))
+        self.original_size += original_len
+
+    def compress_data(self, data, compressor):
+        data = bytes(data)
+        for s in range(0, len(data), self.block_size):
+            chunk = data[s:s + self.block_size]
+            self.add_block(compressor.compress(chunk), len(chunk))
+
+    def finish(self):
+        import struct
+        index, off = b"", 0
+        for c, sum_ in self.blocks:
+            index += struct.pack("<IIQ", off, len(c), sum_)
+            off += len(c)
+        h = bytearray(64)
+        h[0:4] = b"HCTN"
+        struct.pack_into("<IBBHQQII", h, 4, 2, self.algorithm, self.dtype, self.flags,
+                         self.original_size, off, self.block_size, len(self.blocks))
+        h[36] = len(self.shape)
+        for i, d in enumerate(self.shape[:4]):
+            h[37 + 8 * i:45 + 8 * i] = struct.pack("<Q", d)[:max(0, min(8, 64 - (37 + 8 * i)))]
+        struct.pack_into("<Q", h, 56, xxh3_64(bytes(h[:56])))
+        return bytes(h) + (self.quant or b"") + index + b"".join(c for c, _ in self.blocks)
 
 
 class Lz4Decompressor:

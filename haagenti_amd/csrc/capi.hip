@@ -330,10 +330,172 @@ int32_t hh_hct_read_header(const uint8_t *file, size_t file_len, hh_hct_info *in
     // four dimensions would overrun the 64-byte header (37 + 4 * 8 > 64)
     if (info->rank > 3) return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER);
     for (uint32_t i = 0; i < info->rank; i++) info->shape[i] = rd_u64(file + 37 + 8 * i);
+    info->index_entry_size = 8;
     info->data_offset = kHeader + (uint64_t)info->num_blocks * 8;
     if (info->data_offset > file_len) return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
     return HH_OK;
 }
+
+}  // extern "C"
+
+namespace {
+
+// The block loop shared by HctReader::decompress_all (v1, tensor.rs:486-515)
+// and HctReaderV2::decompress_all_validated / validate_checksums (:937-1020):
+// host checks of every index entry, one batched XXH3 launch (validate) and
+// one batched LZ4 launch (decode) over the blocks that can be read, then
+// the reference's per-block order of errors: index range, checksum, last
+// block size, output capacity, LZ4 result.
+int32_t hct_blocks(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file, size_t file_len,
+                   const hh_hct_info &info, bool validate, bool decode, uint8_t *d_out,
+                   size_t out_cap, size_t *written, hh_block_status *status, int64_t *failed_block,
+                   void *stream) {
+    const uint32_t n = info.num_blocks;
+    const uint32_t entry = info.index_entry_size;
+    const uint8_t *index = h_file + (info.data_offset - (uint64_t)n * entry);
+    // blocks [0, m) can be read (:470-480); size_fail: the last one's
+    // expected size is inconsistent (:494-500 / :988-994)
+    uint32_t m = n;
+    bool size_fail = false;
+    std::vector<uint64_t> in_off(n), out_off(n), sum(n, 0);
+    std::vector<uint32_t> in_len(n), expect(n);
+    uint64_t nominal = 0;
+    for (uint32_t b = 0; b < n; b++) {
+        const uint8_t *ie = index + (size_t)entry * b;
+        const uint32_t off = rd_u32(ie), csz = rd_u32(ie + 4);
+        if (entry == 16) sum[b] = rd_u64(ie + 8);
+        if (info.data_offset + off + csz > file_len) {
+            m = b;
+            break;
+        }
+        uint64_t e = info.block_size;
+        if (b == n - 1) {
+            const uint64_t full = (uint64_t)(n - 1) * info.block_size;
+            if (full > info.original_size) {
+                size_fail = true;
+                e = 0;
+            } else {
+                e = info.original_size - full;
+            }
+        }
+        if (e > 0xffffffffull) return fail(status, HH_ERR_UNSUPPORTED, HH_CORRUPT_NONE);
+        in_off[b] = info.data_offset + off;
+        in_len[b] = csz;
+        expect[b] = (uint32_t)e;
+        out_off[b] = nominal;
+        nominal += e;
+    }
+    // blocks that are decoded: the readable ones, less a last block of
+    // inconsistent size
+    const uint32_t md = decode ? (size_fail && m == n ? n - 1 : m) : 0;
+    hipError_t he = hipSetDevice(ctx->device);
+    if (he != hipSuccess) return from_hip(he);
+    hipStream_t s = pick_stream(ctx, stream);
+    const bool direct = nominal <= out_cap;
+    const size_t tab = (size_t)m * (32 + 8 + 8 + 4 + 4 + 8);
+    const size_t stage_at = (tab + 255) & ~(size_t)255;
+    std::vector<hh_block_status> st(md);
+    std::vector<uint64_t> hash(validate ? m : 0);
+    int32_t rc = HH_OK;
+    uint8_t *base = nullptr;
+    if (m > 0) {
+        rc = ensure_scratch(ctx, stage_at + (decode && !direct ? nominal : 0) + 16);
+        if (rc != HH_OK) return rc;
+        base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+        hh_block_status *d_st = reinterpret_cast<hh_block_status *>(base);
+        uint64_t *d_in_off = reinterpret_cast<uint64_t *>(base + (size_t)m * 32);
+        uint64_t *d_out_off = d_in_off + m;
+        uint64_t *d_hash = d_out_off + m;
+        uint32_t *d_in_len = reinterpret_cast<uint32_t *>(d_hash + m);
+        uint32_t *d_cap = d_in_len + m;
+        uint8_t *dst = direct ? d_out : base + stage_at;
+        he = hipMemcpyAsync(d_in_off, in_off.data(), 8 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess)
+            he = hipMemcpyAsync(d_in_len, in_len.data(), 4 * (size_t)m, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess && validate)
+            he = hh::launch_xxh3_batch(d_file, file_len, d_in_off, d_in_len, m, d_hash, s);
+        if (he == hipSuccess && validate)
+            he = hipMemcpyAsync(hash.data(), d_hash, 8 * (size_t)m, hipMemcpyDeviceToHost, s);
+        if (md > 0) {
+            if (he == hipSuccess)
+                he = hipMemcpyAsync(d_out_off, out_off.data(), 8 * (size_t)md, hipMemcpyHostToDevice, s);
+            if (he == hipSuccess)
+                he = hipMemcpyAsync(d_cap, expect.data(), 4 * (size_t)md, hipMemcpyHostToDevice, s);
+            if (he == hipSuccess)
+                he = hh::launch_lz4_batch(d_file, file_len, d_in_off, d_in_len, dst, d_out_off, d_cap, md,
+                                          d_st, s);
+            if (he == hipSuccess)
+                he = hipMemcpyAsync(st.data(), d_st, 32 * (size_t)md, hipMemcpyDeviceToHost, s);
+        }
+        if (he == hipSuccess) he = hipStreamSynchronize(s);
+        if (he != hipSuccess) return from_hip(he);
+    }
+    // the reference's loop, block by block
+    uint64_t op = 0;
+    bool shifted = false;
+    for (uint32_t b = 0; b < n; b++) {
+        if (b == m) {  // read_block / read_block_validated: read_exact fails
+            if (failed_block) *failed_block = b;
+            return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
+        }
+        if (validate && sum[b] != 0 && hash[b] != sum[b]) {
+            if (failed_block) *failed_block = b;
+            return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_BLOCK_CHECKSUM);
+        }
+        if (!decode) continue;
+        if (b == n - 1 && size_fail) {
+            if (failed_block) *failed_block = b;
+            return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_SIZE);
+        }
+        if (op + expect[b] > out_cap) {
+            if (failed_block) *failed_block = b;
+            return fail(status, HH_ERR_BUFFER_TOO_SMALL, HH_CORRUPT_NONE, 0, op + expect[b]);
+        }
+        if (st[b].code != HH_OK) {
+            if (failed_block) *failed_block = b;
+            if (status) *status = st[b];
+            return st[b].code;
+        }
+        if (op != out_off[b]) shifted = true;
+        op += st[b].written;
+    }
+    if (decode && md > 0 && (shifted || !direct)) {
+        // a short block shifts the blocks after it (truncate, then extend)
+        if (direct) {  // bounce buffer for the overlapping moves to the left
+            uint64_t maxw = 0;
+            for (uint32_t b = 0; b < md; b++) maxw = st[b].written > maxw ? st[b].written : maxw;
+            rc = ensure_scratch(ctx, stage_at + maxw + 16);
+            if (rc != HH_OK) return rc;
+        }
+        uint8_t *scr = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+        uint64_t o = 0;
+        for (uint32_t b = 0; b < md && he == hipSuccess; b++) {
+            const uint64_t w = st[b].written;
+            if (w && (!direct || o != out_off[b])) {
+                if (direct) {
+                    he = hipMemcpyAsync(scr + stage_at, d_out + out_off[b], w, hipMemcpyDeviceToDevice, s);
+                    if (he == hipSuccess)
+                        he = hipMemcpyAsync(d_out + o, scr + stage_at, w, hipMemcpyDeviceToDevice, s);
+                } else {
+                    he = hipMemcpyAsync(d_out + o, scr + stage_at + out_off[b], w, hipMemcpyDeviceToDevice, s);
+                }
+            }
+            o += w;
+        }
+        if (he == hipSuccess) he = hipStreamSynchronize(s);
+        if (he != hipSuccess) return from_hip(he);
+    }
+    if (written) *written = op;
+    if (status) {
+        std::memset(status, 0, sizeof(*status));
+        status->written = op;
+    }
+    return HH_OK;
+}
+
+}  // namespace
+
+extern "C" {
 
 int32_t hh_hct_decompress_all(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
                               size_t file_len, uint8_t *d_out, size_t out_cap, size_t *written,
@@ -344,128 +506,85 @@ int32_t hh_hct_decompress_all(hh_context *ctx, const uint8_t *h_file, const uint
     hh_hct_info info;
     int32_t rc = hh_hct_read_header(h_file, file_len, &info, status);
     if (rc != HH_OK) return rc;
-    const uint32_t n = info.num_blocks;
-    const uint8_t *index = h_file + 64;
-    // Host-side checks in the reference's per-block order; blocks before the
-    // first failing one are decoded (one of them may fail first).
-    uint32_t m = n;  // blocks [0, m) pass the host checks
-    int32_t host_code = HH_OK, host_detail = HH_CORRUPT_NONE;
-    std::vector<uint64_t> in_off(n), out_off(n);
-    std::vector<uint32_t> in_len(n), expect(n);
-    uint64_t nominal = 0;
-    for (uint32_t b = 0; b < n; b++) {
-        const uint32_t off = rd_u32(index + 8 * (size_t)b), csz = rd_u32(index + 8 * (size_t)b + 4);
-        if (info.data_offset + off + csz > file_len) {  // read_block fails (:477-480)
-            m = b;
-            host_code = HH_ERR_ALGORITHM;
-            break;
-        }
-        uint64_t e = info.block_size;
-        if (b == n - 1) {  // last block: original_size - full blocks (:494-500)
-            const uint64_t full = (uint64_t)(n - 1) * info.block_size;
-            if (full > info.original_size) {
-                m = b;
-                host_code = HH_ERR_CORRUPTED_DATA;
-                host_detail = HH_CORRUPT_SIZE;
-                break;
-            }
-            e = info.original_size - full;
-        }
-        if (e > 0xffffffffull) return fail(status, HH_ERR_UNSUPPORTED, HH_CORRUPT_NONE);
-        in_off[b] = info.data_offset + off;
-        in_len[b] = csz;
-        expect[b] = (uint32_t)e;
-        out_off[b] = nominal;
-        nominal += e;
+    return hct_blocks(ctx, h_file, d_file, file_len, info, false, true, d_out, out_cap, written, status,
+                      failed_block, stream);
+}
+
+uint64_t hh_xxh3_64(const uint8_t *data, size_t len) {
+    if (!data && len) return 0;
+    return hh::xxh3_64_host(data, len);
+}
+
+int32_t hh_xxh3_64_batch(hh_context *ctx, const uint8_t *d_data, size_t data_len, const uint64_t *d_off,
+                         const uint32_t *d_len, uint32_t n, uint64_t *d_out, void *stream) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    if (n == 0) return HH_OK;
+    if (!d_data || !d_off || !d_len || !d_out) return HH_ERR_INVALID_ARGUMENT;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hh::launch_xxh3_batch(d_data, data_len, d_off, d_len, n, d_out, pick_stream(ctx, stream));
+    return from_hip(e);
+}
+
+int32_t hh_hct_read_header_v2(const uint8_t *file, size_t file_len, hh_hct_info *info,
+                              hh_hct_quant *quant, hh_block_status *status) {
+    if (!info || (!file && file_len)) return HH_ERR_INVALID_ARGUMENT;
+    if (quant) std::memset(quant, 0, sizeof(*quant));
+    // header fields (from_bytes); the v1 index geometry is replaced below
+    int32_t rc = hh_hct_read_header(file, file_len < 64 ? file_len : 64, info, status);
+    if (rc != HH_OK) {
+        // a v1-sized index that does not fit is not an error yet: only the
+        // header itself was given to the v1 parse
+        if (!(rc == HH_ERR_ALGORITHM && file_len >= 64)) return rc;
     }
-    hipError_t he = hipSetDevice(ctx->device);
-    if (he != hipSuccess) return from_hip(he);
-    hipStream_t s = pick_stream(ctx, stream);
-    // Decode into d_out at the nominal block positions when they fit, else
-    // into a staging area of the context scratch; compact afterwards.
-    const bool direct = nominal <= out_cap;
-    const size_t tab = (size_t)m * (32 + 8 + 4 + 8 + 4);
-    const size_t stage_at = (tab + 255) & ~(size_t)255;
-    std::vector<hh_block_status> st(m);
-    if (m > 0) {
-        rc = ensure_scratch(ctx, stage_at + (direct ? 0 : nominal) + 16);
-        if (rc != HH_OK) return rc;
-        uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
-        hh_block_status *d_st = reinterpret_cast<hh_block_status *>(base);
-        uint64_t *d_in_off = reinterpret_cast<uint64_t *>(base + (size_t)m * 32);
-        uint64_t *d_out_off = d_in_off + m;
-        uint32_t *d_in_len = reinterpret_cast<uint32_t *>(d_out_off + m);
-        uint32_t *d_cap = d_in_len + m;
-        uint8_t *dst = direct ? d_out : base + stage_at;
-        he = hipMemcpyAsync(d_in_off, in_off.data(), 8 * (size_t)m, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess)
-            he = hipMemcpyAsync(d_out_off, out_off.data(), 8 * (size_t)m, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess)
-            he = hipMemcpyAsync(d_in_len, in_len.data(), 4 * (size_t)m, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess)
-            he = hipMemcpyAsync(d_cap, expect.data(), 4 * (size_t)m, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess)
-            he = hh::launch_lz4_batch(d_file, file_len, d_in_off, d_in_len, dst, d_out_off, d_cap, m,
-                                      d_st, s);
-        if (he == hipSuccess)
-            he = hipMemcpyAsync(st.data(), d_st, 32 * (size_t)m, hipMemcpyDeviceToHost, s);
-        if (he == hipSuccess) he = hipStreamSynchronize(s);
-        if (he != hipSuccess) return from_hip(he);
-        // the reference's loop: output cap, then the block's own result
-        uint64_t op = 0;
-        bool shifted = false;
-        for (uint32_t b = 0; b < m; b++) {
-            if (op + expect[b] > out_cap) {
-                if (failed_block) *failed_block = b;
-                return fail(status, HH_ERR_BUFFER_TOO_SMALL, HH_CORRUPT_NONE, 0, op + expect[b]);
-            }
-            if (st[b].code != HH_OK) {
-                if (failed_block) *failed_block = b;
-                if (status) *status = st[b];
-                return st[b].code;
-            }
-            if (op != out_off[b]) shifted = true;
-            op += st[b].written;
+    if (info->version >= 2 && (info->flags & 0x0001u) &&
+        hh::xxh3_64_host(file, 56) != rd_u64(file + 56))
+        return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_HEADER_CHECKSUM);
+    uint64_t at = 64;
+    if (info->flags & 0x0004u) {  // QuantizationMetadata (:868-876, :207-226)
+        if (file_len < at + 8) return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
+        const uint8_t *q = file + at;
+        if (q[0] > 4) return fail(status, HH_ERR_CORRUPTED_DATA, HH_CORRUPT_QUANT_SCHEME);
+        if (quant) {
+            quant->present = 1;
+            quant->scheme = q[0];
+            quant->has_per_group_scales = q[1] != 0;
+            quant->scale_bits = (uint16_t)(q[2] | (q[3] << 8));
+            quant->zero_point = (int8_t)q[4];
+            quant->group_size = (uint32_t)q[5] | ((uint32_t)q[6] << 8) | ((uint32_t)q[7] << 16);
         }
-        if (host_code == HH_OK && (shifted || !direct)) {
-            // a short block shifts the blocks after it (truncate, then extend)
-            if (direct) {  // bounce buffer for the overlapping moves to the left
-                uint64_t maxw = 0;
-                for (uint32_t b = 0; b < m; b++) maxw = st[b].written > maxw ? st[b].written : maxw;
-                rc = ensure_scratch(ctx, stage_at + maxw + 16);
-                if (rc != HH_OK) return rc;
-            }
-            uint64_t o = 0;
-            for (uint32_t b = 0; b < m && he == hipSuccess; b++) {
-                const uint64_t w = st[b].written;
-                if (w && (!direct || o != out_off[b])) {
-                    if (direct) {  // overlapping move to the left: bounce through scratch
-                        uint8_t *bounce = reinterpret_cast<uint8_t *>(ctx->d_scratch) + stage_at;
-                        he = hipMemcpyAsync(bounce, d_out + out_off[b], w, hipMemcpyDeviceToDevice, s);
-                        if (he == hipSuccess)
-                            he = hipMemcpyAsync(d_out + o, bounce, w, hipMemcpyDeviceToDevice, s);
-                    } else {
-                        he = hipMemcpyAsync(d_out + o,
-                                            reinterpret_cast<uint8_t *>(ctx->d_scratch) + stage_at + out_off[b],
-                                            w, hipMemcpyDeviceToDevice, s);
-                    }
-                }
-                o += w;
-            }
-            if (he == hipSuccess) he = hipStreamSynchronize(s);
-            if (he != hipSuccess) return from_hip(he);
-        }
-        if (written) *written = op;
+        at += 8;
     }
-    if (host_code != HH_OK) {
-        if (failed_block) *failed_block = m;
-        return fail(status, host_code, host_detail, host_code == HH_ERR_ALGORITHM ? file_len : 0);
-    }
-    if (status) {
-        std::memset(status, 0, sizeof(*status));
-        status->written = written ? *written : 0;
-    }
+    info->index_entry_size = (info->version >= 2 && (info->flags & 0x0002u)) ? 16u : 8u;
+    info->data_offset = at + (uint64_t)info->num_blocks * info->index_entry_size;
+    if (info->data_offset > file_len) return fail(status, HH_ERR_ALGORITHM, HH_CORRUPT_NONE, file_len);
+    if (status) std::memset(status, 0, sizeof(*status));
     return HH_OK;
+}
+
+int32_t hh_hct_decompress_all_validated(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                                        size_t file_len, uint8_t *d_out, size_t out_cap,
+                                        size_t *written, hh_block_status *status,
+                                        int64_t *failed_block, void *stream) {
+    if (written) *written = 0;
+    if (failed_block) *failed_block = -1;
+    if (!ctx || !h_file || !d_file || (!d_out && out_cap)) return HH_ERR_INVALID_ARGUMENT;
+    hh_hct_info info;
+    int32_t rc = hh_hct_read_header_v2(h_file, file_len, &info, nullptr, status);
+    if (rc != HH_OK) return rc;
+    return hct_blocks(ctx, h_file, d_file, file_len, info, true, true, d_out, out_cap, written, status,
+                      failed_block, stream);
+}
+
+int32_t hh_hct_validate_checksums(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                                  size_t file_len, hh_block_status *status, int64_t *failed_block,
+                                  void *stream) {
+    if (failed_block) *failed_block = -1;
+    if (!ctx || !h_file || !d_file) return HH_ERR_INVALID_ARGUMENT;
+    hh_hct_info info;
+    int32_t rc = hh_hct_read_header_v2(h_file, file_len, &info, nullptr, status);
+    if (rc != HH_OK) return rc;
+    return hct_blocks(ctx, h_file, d_file, file_len, info, true, false, nullptr, 0, nullptr, status,
+                      failed_block, stream);
 }
 
 }  // extern "C"

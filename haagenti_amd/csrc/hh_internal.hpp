@@ -67,6 +67,10 @@ hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t
                             const uint64_t *d_out_off, const uint32_t *d_out_cap,
                             uint32_t nblocks, hh_block_status *d_status, hipStream_t s);
 
+hipError_t launch_xxh3_batch(const uint8_t *d_data, size_t data_len, const uint64_t *d_off,
+                             const uint32_t *d_len, uint32_t n, uint64_t *d_out, hipStream_t s);
+uint64_t xxh3_64_host(const uint8_t *data, size_t len);
+
 // Build the MFMA basis fragments on the host (host_basis.cpp).
 size_t basis_table_bytes();
 void build_basis_table(void *host_buf);

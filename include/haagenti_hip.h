@@ -55,7 +55,10 @@ typedef enum hh_corrupt_kind {
     HH_CORRUPT_OFFSET_BEYOND = 2,  /* "offset beyond output at offset N" (block.rs:323-325) */
     HH_CORRUPT_BITMAP_COUNT = 3,   /* "bitmap has N set bits, expected K" (compressive.rs:630-636) */
     HH_CORRUPT_HEADER = 4,         /* invalid magic/version/algorithm/dtype (tensor.rs:311-331) */
-    HH_CORRUPT_SIZE = 5            /* sizes inconsistent with the header/shape */
+    HH_CORRUPT_SIZE = 5,           /* sizes inconsistent with the header/shape */
+    HH_CORRUPT_HEADER_CHECKSUM = 6,  /* "header checksum mismatch" (haagenti-hct/src/tensor.rs:857-865) */
+    HH_CORRUPT_BLOCK_CHECKSUM = 7,   /* "block N checksum mismatch" (tensor.rs:965-974) */
+    HH_CORRUPT_QUANT_SCHEME = 8      /* "unknown quantization scheme" (tensor.rs:158-173) */
 } hh_corrupt_kind;
 
 /* Output element types; values match haagenti_hct::DType (tensor.rs:99-105). */
@@ -200,10 +203,22 @@ typedef struct hh_hct_info {
     uint32_t block_size;
     uint32_t num_blocks;
     uint32_t rank;
-    uint32_t pad;
+    uint32_t index_entry_size; /* 8, or 16 for v2 files with block checksums */
     uint64_t shape[4];
-    uint64_t data_offset;   /* 64 + 8 * num_blocks */
+    uint64_t data_offset;   /* header + quantization metadata + index */
 } hh_hct_info;
+
+/* QuantizationMetadata of HCT v2 (tensor.rs:180-226), 8 bytes after the
+ * header when flags has 0x0004. */
+typedef struct hh_hct_quant {
+    uint8_t present;
+    uint8_t scheme;         /* QuantizationScheme 0..4 (tensor.rs:144-156) */
+    uint8_t has_per_group_scales;
+    int8_t zero_point;
+    uint16_t scale_bits;    /* f16 bits */
+    uint16_t pad;
+    uint32_t group_size;    /* 24 bits on disk */
+} hh_hct_quant;
 
 /* HctHeader::from_bytes (crates/haagenti-hct/src/tensor.rs:302-375) and the
  * index read of HctReader::new (:417-445) on host bytes.  Errors as the
@@ -229,6 +244,47 @@ int32_t hh_hct_read_header(const uint8_t *file, size_t file_len, hh_hct_info *in
 int32_t hh_hct_decompress_all(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
                               size_t file_len, uint8_t *d_out, size_t out_cap, size_t *written,
                               hh_block_status *status, int64_t *failed_block, void *stream);
+
+/* ---- HCT v2: XXH3-64 checksums (tensor.rs:45-271, 676-1021) ------------ */
+
+/* xxhash_rust::xxh3::xxh3_64 (xxhash-rust 0.8.15, seed 0) as called at
+ * tensor.rs:729,794,858,967, on host memory. */
+uint64_t hh_xxh3_64(const uint8_t *data, size_t len);
+
+/* The same hash of n device buffers data[off[i], off[i] + len[i]) in one
+ * launch (one wavefront per buffer), into d_out[i].  A range outside
+ * [0, data_len) yields 0.  Asynchronous on the stream.  Replaces the
+ * per-block xxh3_64 of HctReaderV2::read_block_validated (:965-974). */
+int32_t hh_xxh3_64_batch(hh_context *ctx, const uint8_t *d_data, size_t data_len,
+                         const uint64_t *d_off, const uint32_t *d_len, uint32_t n, uint64_t *d_out,
+                         void *stream);
+
+/* HctReaderV2::new (tensor.rs:841-920) on host bytes: the v1 header checks,
+ * then the header checksum (version >= 2 and flags & 0x0001: XXH3 of bytes
+ * 0..56 must equal bytes 56..64, else HH_ERR_CORRUPTED_DATA /
+ * HH_CORRUPT_HEADER_CHECKSUM), the quantization metadata (flags & 0x0004;
+ * short file HH_ERR_ALGORITHM, unknown scheme HH_CORRUPT_QUANT_SCHEME), and
+ * the index entry size (16 when version >= 2 and flags & 0x0002, else 8).
+ * quant may be NULL. */
+int32_t hh_hct_read_header_v2(const uint8_t *file, size_t file_len, hh_hct_info *info,
+                              hh_hct_quant *quant, hh_block_status *status);
+
+/* HctReaderV2::new + decompress_all_validated (tensor.rs:980-1012): as
+ * hh_hct_decompress_all, with every block's XXH3 (when its index entry
+ * holds a non-zero checksum) computed on the GPU in one launch and checked
+ * in the reference's per-block order: index range (HH_ERR_ALGORITHM), then
+ * checksum (HH_ERR_CORRUPTED_DATA / HH_CORRUPT_BLOCK_CHECKSUM), then size,
+ * output capacity and the block's LZ4 result.  Synchronous on the stream. */
+int32_t hh_hct_decompress_all_validated(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                                        size_t file_len, uint8_t *d_out, size_t out_cap,
+                                        size_t *written, hh_block_status *status,
+                                        int64_t *failed_block, void *stream);
+
+/* HctReaderV2::new + validate_checksums (tensor.rs:1014-1020): the header
+ * checks and every block's range and checksum, without decoding. */
+int32_t hh_hct_validate_checksums(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file,
+                                  size_t file_len, hh_block_status *status, int64_t *failed_block,
+                                  void *stream);
 
 #ifdef __cplusplus
 }

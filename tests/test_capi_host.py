@@ -144,3 +144,76 @@ def test_hct_header_errors_match_oracle():
         with pytest.raises(H.HaagentiError) as ei:
             H.HctReader(c)
         assert ei.value.code == e.kind, (c[:12], ei.value.code, e.kind)
+
+
+# ---------------------------------------------------------------- HCT v2 (host side)
+def test_xxh3_host_matches_xxhash_library():
+    xxhash = pytest.importorskip("xxhash")
+    rng = np.random.default_rng(21)
+    for n in list(range(0, 600)) + [1023, 1024, 1025, 4096, 16384, 65809]:
+        d = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert H.xxh3_64(d) == xxhash.xxh3_64_intdigest(d) == O.xxh3_64(d)
+
+
+def _v2_pair(data, block_size, dtype, shape, quant=None, checksums=True):
+    w = H.HctWriterV2(dtype, shape, block_size)
+    flags = O.FLAG_HEADER_CHECKSUM | (O.FLAG_BLOCK_CHECKSUMS if checksums else 0)
+    if quant:
+        w.with_quantization(**quant)
+        flags |= O.FLAG_QUANTIZATION
+    if not checksums:
+        w.without_block_checksums()
+    w.compress_data(data, H.Lz4Compressor())
+    mine = w.finish()
+    q8 = None
+    if quant:
+        q8 = mine[64:72]
+    ref = O.hct_write_v2_lz4(data, block_size, dtype, shape, flags=flags, quant8=q8)
+    return mine, ref
+
+
+def test_v2_writer_byte_identical_to_oracle():
+    rng = np.random.default_rng(22)
+    data = rng.integers(0, 6, 70001, dtype=np.uint8).tobytes()
+    mine, ref = _v2_pair(data, 16384, 3, [70001])
+    assert mine == ref
+    q = dict(scheme=1, group_size=128, scale_bits=0x3C00, zero_point=-8, has_per_group_scales=True)
+    mine, ref = _v2_pair(data, 16384, 4, [271, 259], quant=q)
+    assert mine == ref
+    mine, ref = _v2_pair(data, 20000, 3, [70001], checksums=False)
+    assert mine == ref
+
+
+def test_v2_header_parse_checksum_and_quantization():
+    data = bytes(i % 256 for i in range(4096))
+    q = dict(scheme=1, group_size=128, scale_bits=0x3C00, zero_point=0, has_per_group_scales=False)
+    f, _ = _v2_pair(data, 16384, 4, [4096], quant=q)
+    r = H.HctReaderV2(f)   # tensor.rs:1367-1410
+    assert r.quantization() == dict(scheme=1, group_size=128, scale_bits=0x3C00, zero_point=0,
+                                    has_per_group_scales=False)
+    assert r.header()["version"] == 2 and r.num_blocks() == 1
+    r.validate_checksums()
+    g = bytearray(f)
+    g[20] ^= 1   # header byte: checksum mismatch (:857-865)
+    with pytest.raises(H.HaagentiError) as e:
+        H.HctReaderV2(bytes(g))
+    assert e.value.code == H.CORRUPTED_DATA and e.value.status.detail == H.CORRUPT_HEADER_CHECKSUM
+    g = bytearray(f)
+    g[64] = 7    # unknown quantization scheme (:158-173); header checksum still valid
+    with pytest.raises(H.HaagentiError) as e:
+        H.HctReaderV2(bytes(g))
+    assert e.value.status.detail == H.CORRUPT_QUANT_SCHEME
+
+
+def test_v2_block_checksum_detects_corruption_on_host():
+    # tensor.rs:1324-1364: byte 100 is inside the data of the one block
+    data = bytes(i % 256 for i in range(16384))
+    f, _ = _v2_pair(data, 16384, 3, [16384])
+    g = bytearray(f)
+    g[100] ^= 0xFF
+    r = H.HctReaderV2(bytes(g))
+    with pytest.raises(H.HaagentiError) as e:
+        r.validate_checksums()
+    assert e.value.code == H.CORRUPTED_DATA
+    e2, fb = O.hct_validate_v2(bytes(g))
+    assert e2.sub == O.CORRUPT_BLOCK_CHECKSUM and fb == 0
