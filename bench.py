@@ -26,6 +26,10 @@ Other workloads (one JSON line each, same contract):
                    U[0.10, 0.50]; compressed layers in pinned host memory,
                    H2D copies on a copy stream overlapped with decode into a
                    double-buffered bf16 layer slot
+  xxh3-256mib      HCT v2 block validation: XXH3-64 of the 4096 compressed
+                   blocks of lz4-256mib (one wavefront per block), the
+                   checksum HctReaderV2 verifies per block; value = hashed
+                   bytes per second (the kernel reads its input once)
   hbm-copy         a plain 1 GiB device copy: the HBM reference rate and the
                    calibration for the FETCH_SIZE / WRITE_SIZE counters
 
@@ -625,7 +629,55 @@ def wl_copy(args, torch, H, O):
                 roofline("hbm-copy", "torch copy (calibration)", 2 * n, per), None)
 
 
-WORKLOADS = {"llama3-8b-layer": wl_llama3_8b_layer, "int4-4096": wl_int4, "lz4-256mib": wl_lz4,
+def wl_xxh3(args, torch, H, O):
+    nb = 4096
+    srcs, pick, blob, in_off, in_len = config2_blocks(H)
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    d_in = torch.from_numpy(blob.copy()).cuda()
+    d_off, d_len = devtab(torch, in_off), devtab(torch, in_len)
+    d_out = torch.zeros(nb, dtype=torch.int64, device="cuda")
+    launches = 10
+
+    def step():
+        for _ in range(launches):
+            ctx.xxh3_64_batch(d_in, d_in.numel(), d_off, d_len, nb, d_out, stream=sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    got = d_out.cpu().numpy().view(np.uint64)
+    exact = all(int(got[j]) == H.xxh3_64(blob[in_off[j]:in_off[j] + in_len[j]].tobytes())
+                for j in range(0, nb, 97))
+    log(f"spot check of every 97th block vs the host XXH3: {exact}")
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps):
+        step()
+    T.stop(e)
+    torch.cuda.synchronize()
+    ms_step = T.mean_s() * 1e3 / args.steps
+    per = ms_step / 1e3 / launches
+    in_b = int(blob.size)
+    cpu = None
+    if not args.no_cpu and O is not None:
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_budget:
+            O.xxh3_64_batch(blob, in_off, in_len, cpu_threads())
+            reps += 1
+        secs = time.perf_counter() - t0
+        cpu = {"value": round(reps * in_b / secs / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+               "kind": "port",
+               "sample": f"{reps} x all {nb} blocks ({in_b} bytes), {cpu_threads()} threads, {secs:.1f} s"}
+    return line("xxh3-256mib", in_b / per / 1e9, ms_step, args, "u64",
+                "synthetic (the lz4-256mib compressed blocks)",
+                {"blocks": nb, "in_bytes": in_b, "launches_per_step": launches},
+                roofline("xxh3-256mib", "xxh3_batch_kernel", in_b, per), cpu,
+                {"spot_check_exact": exact})
+
+
+WORKLOADS = {"llama3-8b-layer": wl_llama3_8b_layer, "xxh3-256mib": wl_xxh3, "int4-4096": wl_int4, "lz4-256mib": wl_lz4,
              "idct-8192": wl_idct, "llama70b-stream": wl_stream, "hbm-copy": wl_copy}
 
 

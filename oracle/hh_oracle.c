@@ -1447,3 +1447,19 @@ int hho_hct_validate_v2(const uint8_t *file, size_t file_len, hho_err *err,
     }
     return HHO_OK;
 }
+
+typedef struct {
+    const uint8_t *data;
+    const uint64_t *off;
+    const uint32_t *len;
+    uint64_t *out;
+} xxh_batch_ctx;
+static void xxh_batch_task(void *vctx, size_t i) {
+    xxh_batch_ctx *c = (xxh_batch_ctx *)vctx;
+    c->out[i] = hho_xxh3_64(c->data + c->off[i], c->len[i]);
+}
+void hho_xxh3_64_batch(const uint8_t *data, const uint64_t *off, const uint32_t *len, size_t n,
+                       uint64_t *out, int nthreads) {
+    xxh_batch_ctx c = {data, off, len, out};
+    hho_parallel_for(n, nthreads, xxh_batch_task, &c);
+}

@@ -161,6 +161,9 @@ int hho_hct_read_all_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
  * algorithm (xxHash 0.8: default 192-byte secret, 0-16 / 17-128 / 129-240 /
  * long-input paths); pinned against the xxhash library's outputs. */
 uint64_t hho_xxh3_64(const uint8_t *data, size_t len);
+/* The same over n buffers data[off[i], off[i] + len[i]) on nthreads threads. */
+void hho_xxh3_64_batch(const uint8_t *data, const uint64_t *off, const uint32_t *len, size_t n,
+                       uint64_t *out, int nthreads);
 
 /* ---------------- HCT v2 container (tensor.rs:45-271, 676-1021) ---------- */
 

@@ -94,6 +94,8 @@ def lib():
         L.hho_hct_read_all_lz4.argtypes = [u8p, sz, u8p, sz, C.POINTER(sz), C.POINTER(Err)]
         L.hho_xxh3_64.restype = C.c_uint64
         L.hho_xxh3_64.argtypes = [u8p, sz]
+        L.hho_xxh3_64_batch.restype = None
+        L.hho_xxh3_64_batch.argtypes = [u8p, u8p, u8p, sz, u8p, C.c_int]
         L.hho_hct_write_v2_lz4.restype = sz
         L.hho_hct_write_v2_lz4.argtypes = [u8p, sz, C.c_uint32, C.c_uint8, u8p, C.c_int, C.c_uint16,
                                            u8p, u8p, sz]
@@ -344,6 +346,15 @@ CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8
 def xxh3_64(data):
     d = _u8(data)
     return int(lib().hho_xxh3_64(_p(d), d.size))
+
+
+def xxh3_64_batch(data, offs, lens, nthreads=0):
+    d = _u8(data)
+    o = np.ascontiguousarray(offs, dtype=np.uint64)
+    ln = np.ascontiguousarray(lens, dtype=np.uint32)
+    out = np.zeros(o.size, dtype=np.uint64)
+    lib().hho_xxh3_64_batch(_p(d), _p(o), _p(ln), o.size, _p(out), nthreads)
+    return out
 
 
 def hct_write_v2_lz4(data, block_size, dtype, shape,
