@@ -62,10 +62,18 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 hipError_t launch_dequant_int4(const uint8_t *d_q, size_t n, size_t nscale_groups,
                                int dtype, void *d_out, int num_cus, hipStream_t s);
 
+// Batched LZ4: dispatches to the LDS-ring decoder (lz4_ring.hip) or, when
+// the environment sets HH_LZ4_KERNEL=window, to the register-window decoder
+// (lz4_decode.hip).  The ring is 8 KiB; HH_LZ4_KERNEL=ring16 / ring32 select
+// a 16 / 32 KiB ring.
 hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
                             const uint32_t *d_in_len, uint8_t *d_out,
                             const uint64_t *d_out_off, const uint32_t *d_out_cap,
                             uint32_t nblocks, hh_block_status *d_status, hipStream_t s);
+hipError_t launch_lz4_ring(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
+                           const uint32_t *d_in_len, uint8_t *d_out, const uint64_t *d_out_off,
+                           const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
+                           uint32_t ring_kib, hipStream_t s);
 
 hipError_t launch_xxh3_batch(const uint8_t *d_data, size_t data_len, const uint64_t *d_off,
                              const uint32_t *d_len, uint32_t n, uint64_t *d_out, hipStream_t s);

@@ -29,6 +29,9 @@
 // vector memory operations are performed in order, so no wait is needed
 // between those stores and loads (a wavefront-scope fence keeps the compiler
 // from reordering them).
+#include <cstdlib>
+#include <cstring>
+
 #include "hh_internal.hpp"
 
 namespace hh {
@@ -348,6 +351,12 @@ hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t
                             const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
                             hipStream_t s) {
     if (nblocks == 0) return hipSuccess;
+    const char *k = std::getenv("HH_LZ4_KERNEL");
+    if (k == nullptr || std::strcmp(k, "window") != 0) {
+        const uint32_t kib = k == nullptr ? 8u : std::strcmp(k, "ring16") == 0 ? 16u : std::strcmp(k, "ring32") == 0 ? 32u : 8u;
+        return launch_lz4_ring(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,
+                               d_status, kib, s);
+    }
     const uint32_t grid = (nblocks + kWaves - 1) / kWaves;
     hipLaunchKernelGGL(lz4_batch_kernel, dim3(grid), dim3(kThreads), 0, s, d_in,
                        (uint64_t)in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,

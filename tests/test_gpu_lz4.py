@@ -9,6 +9,17 @@ import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
 
+# Every test runs on each decoder the batched entry point can dispatch to:
+# the LDS-ring decoder with its 8 (default), 16 and 32 KiB rings, and the
+# register-window decoder.
+KERNELS = ["ring8", "ring16", "ring32", "window"]
+
+
+@pytest.fixture(autouse=True, params=KERNELS)
+def lz4_kernel(request, monkeypatch):
+    monkeypatch.setenv("HH_LZ4_KERNEL", request.param)
+    return request.param
+
 
 def gpu_batch(streams, caps, in_pad=0, out_pad=0, in_align=0, out_align=0):
     """Decode independent blocks in one launch.  Returns (outputs, statuses)."""
@@ -191,3 +202,26 @@ def test_corrupted_stream_fuzz():
         streams.append(bytes(b))
         caps.append(n if trial % 5 else int(rng.integers(0, n + 1)))
     check_against_oracle(streams, caps, out_pad=3)
+
+
+def test_ring_boundaries_far_long_and_periodic_copies():
+    # Streams from the oracle compressor whose matches sit on the ring
+    # decoder's limits: offsets just below / above what each ring serves
+    # (R - 32 for R = 8, 16, 32 KiB), literals longer than the input stage,
+    # matches longer than the ring (periodic and not), and far matches that
+    # overlap their own output.
+    rng = np.random.default_rng(6)
+    srcs = []
+    for L in [100, 992, 993, 2047, 2049, 8159, 8161, 8200, 16351, 16353, 32735, 32737, 40000]:
+        a = rng.integers(0, 256, L, dtype=np.uint8).tobytes()
+        srcs.append(a + a)                                     # one match at offset L
+    srcs.append(rng.integers(0, 256, 70000, dtype=np.uint8).tobytes())   # one 70 KB literal
+    srcs.append(bytes(200000))                                # offset-1 match of ~200 KB
+    srcs.append(bytes((i * 7) & 0xFF for i in range(40)) * 500)          # offset 40, 20 KB
+    a = rng.integers(0, 256, 10000, dtype=np.uint8).tobytes()
+    srcs.append(a * 6)                                        # offset 10000, 60 KB (overlapping)
+    streams = [O.lz4_compress_block(x)[0] for x in srcs]
+    for out_align in (0, 5, 11):
+        outs, st = check_against_oracle(streams, [len(x) for x in srcs], out_align=out_align,
+                                        in_align=out_align % 4, out_pad=17)
+        assert outs == srcs
