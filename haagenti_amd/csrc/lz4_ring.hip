@@ -62,7 +62,8 @@ __device__ __forceinline__ u32x4 realign(uint32_t d0, uint32_t d1, uint32_t d2, 
                  __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
 }
 
-constexpr uint32_t kNoWin = 0xffffffffu;
+// "no window": any stage offset minus it is >= 256 (see in_win)
+constexpr uint32_t kNoWin = 0x80000000u;
 
 template <uint32_t R, uint32_t S>
 struct RingDec {
@@ -84,7 +85,11 @@ struct RingDec {
     uint8_t *obase;       // 16-aligned, <= the block's output address
     uint32_t a0;          // output address - obase
     uint32_t cap;
-    int64_t sb;           // block-relative input position of stage byte 0
+    // Block-relative input position of stage byte 0, modulo 2^32 (it is up
+    // to 15 before the block start when the block starts unaligned); every
+    // use takes a difference x - sb, exact for x in or after the stage.
+    uint32_t sb;
+    bool at_end;          // the stage reaches the end of the input buffer
     uint32_t wso;         // stage offset of the window (4-aligned), or kNoWin
     uint32_t w;           // this lane's window dword
     uint32_t op;          // bytes decoded
@@ -95,8 +100,9 @@ struct RingDec {
     // is 16-aligned in memory, at most 15 bytes before x.
     __device__ __forceinline__ void restage(uint32_t x) {
         const uintptr_t addr = (uintptr_t)(gbuf + ioff + x);
-        sb = (int64_t)x - (int64_t)(addr & 15u);
-        const int64_t b0 = (int64_t)ioff + sb;  // buffer offset of stage byte 0 (may be < 0)
+        sb = x - (uint32_t)(addr & 15u);
+        const int64_t b0 = (int64_t)ioff + (int64_t)x - (int64_t)(addr & 15u);  // may be < 0
+        at_end = (uint64_t)(b0 + S) >= gsz;
         u32x4 v[S / 1024];
 #pragma unroll
         for (uint32_t i = 0; i < S / 1024; i++) {
@@ -124,21 +130,18 @@ struct RingDec {
     // bytes past it are then never used: every parse read is below the
     // block end).
     __device__ __forceinline__ void win_at(uint32_t x) {
-        int64_t so = (int64_t)x - sb;
-        if (so < 0 || (so + 256 > (int64_t)S && (uint64_t)((int64_t)ioff + sb + S) < gsz)) {
+        uint32_t so = x - sb;
+        if (so >= S || (so + 256 > S && !at_end)) {
             restage(x);
-            so = (int64_t)x - sb;
+            so = x - sb;
         }
-        wso = (uint32_t)so & ~3u;
+        wso = so & ~3u;
         w = *reinterpret_cast<const uint32_t *>(stage + wso + 4 * lane);
     }
-    __device__ __forceinline__ bool in_win(uint32_t x) const {
-        const int64_t so = (int64_t)x - sb;
-        return wso != kNoWin && so >= (int64_t)wso && so < (int64_t)wso + 256;
-    }
+    __device__ __forceinline__ bool in_win(uint32_t x) const { return x - sb - wso < 256u; }
     __device__ __forceinline__ uint32_t byte(uint32_t x) {
         if (!in_win(x)) win_at(x);
-        const uint32_t d = (uint32_t)((int64_t)x - sb) - wso;
+        const uint32_t d = x - sb - wso;
         return (__builtin_amdgcn_readlane(w, d >> 2) >> ((d & 3u) * 8u)) & 0xffu;
     }
 
@@ -155,10 +158,9 @@ struct RingDec {
             if (!in_win(p)) win_at(p);
             // window-relative positions (the window may start before the
             // block: the stage starts at a 16-aligned address)
-            const int64_t wb = sb + (int64_t)wso;
-            const uint32_t pr = (uint32_t)((int64_t)p - wb);  // < 256
-            const int64_t er64 = (int64_t)end - wb;
-            const uint32_t er = er64 > 256 ? 256u : (uint32_t)er64;  // > pr
+            const uint32_t wb = sb + wso;  // block-relative, modulo 2^32
+            const uint32_t pr = p - wb;    // < 256
+            const uint32_t er = end - wb > 256u ? 256u : end - wb;  // > pr
             const uint32_t r0 = 4u * (uint32_t)lane;
             uint32_t tmask = 0;
 #pragma unroll
@@ -179,23 +181,23 @@ struct RingDec {
                     return false;
                 }
                 len += (__builtin_amdgcn_readlane(w, tl) >> (8 * tb)) & 0xffu;
-                pp = (uint32_t)(wb + tr + 1);
+                pp = wb + tr + 1;
                 return true;
             }
             len += 255ull * (256u - pr);
-            p = (uint32_t)(wb + 256);
+            p = wb + 256;
         }
     }
 
     // 8 bytes from x on (block-relative; bytes past the block end are
     // don't-care and never used by the callers).
     __device__ __forceinline__ uint64_t read8(uint32_t x) {
-        int64_t so = (int64_t)x - sb;
-        if (wso == kNoWin || so < (int64_t)wso || so + 12 > (int64_t)wso + 256) {
+        uint32_t d = x - sb - wso;
+        if (d > 244u) {
             win_at(x);
-            so = (int64_t)x - sb;
+            d = x - sb - wso;
         }
-        const uint32_t d = (uint32_t)so - wso, k = d >> 2, sh = 8u * (d & 3u);
+        const uint32_t k = d >> 2, sh = 8u * (d & 3u);
         const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(w, k);
         const uint64_t mi = (uint32_t)__builtin_amdgcn_readlane(w, k + 1);
         const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(w, k + 2);
@@ -222,8 +224,14 @@ struct RingDec {
             const uint32_t cv = c0 + 16u * (uint32_t)lane;
             u32x4 o;
             if constexpr (K == 3) {
-                // (cv - v) mod off, with cv - v >= -15
-                uint32_t m = (cv + 16u * off - v) % off;
+                // (cv - v) mod off (cv - v >= -15, off < 16): x / off as
+                // (x * magic) >> 16 with magic = floor(65536 / off) + 1,
+                // exact for x < 4096 (x / off is never within 1/16 of an
+                // integer from below); rcp(off) is exact or far enough from
+                // an integer that the floor is exact
+                const uint32_t x = cv + 16u * off - v;
+                const uint32_t magic = (uint32_t)(65536.0f * __builtin_amdgcn_rcpf((float)off)) + 1u;
+                uint32_t m = x - ((x * magic) >> 16) * off;
                 uint32_t d[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
                 for (int b = 0; b < 16; b++) {
@@ -272,8 +280,8 @@ struct RingDec {
                 }
                 o = realign(d[0], d[1], d[2], d[3], d[4], sh);
             }
-            const uint32_t keep = lane == 0 ? (v & 15u) : 0u;  // bytes of the first chunk before the piece
-            if (keep != 0) {
+            if (v & 15u) {  // the first chunk keeps its bytes before the piece
+                const uint32_t keep = lane == 0 ? (v & 15u) : 0u;
                 const u32x4 old = *reinterpret_cast<const u32x4 *>(ring + (cv & kRM));
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -341,6 +349,7 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
     d.obase = out - d.a0;
     d.cap = out_cap[b];
     d.sb = 0;
+    d.at_end = false;
     d.wso = kNoWin;
     d.w = 0;
     d.op = 0;
@@ -390,15 +399,19 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
                     break;
                 }
                 uint32_t rem = (uint32_t)ll;
+                // read the window at the offset now when the stage already
+                // holds it, so its LDS latency overlaps the literal copy
+                const uint32_t so_end = ip - d.sb + rem;
+                if (so_end + 256u <= S || (d.at_end && so_end < S)) d.win_at(ip + rem);
                 while (rem > 0) {
-                    int64_t so = (int64_t)ip - d.sb;
-                    if (so < 0 || so >= (int64_t)S) {
+                    uint32_t so = ip - d.sb;
+                    if (so >= S) {
                         d.restage(ip);
-                        so = (int64_t)ip - d.sb;
+                        so = ip - d.sb;
                     }
                     uint32_t n = rem < D::kP ? rem : D::kP;
-                    if (n > S - (uint32_t)so) n = S - (uint32_t)so;
-                    d.template piece<0>((uint32_t)so, n, 0);
+                    if (n > S - so) n = S - so;
+                    d.template piece<0>(so, n, 0);
                     ip += n;
                     rem -= n;
                     d.check_flush();
