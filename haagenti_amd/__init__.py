@@ -7,7 +7,12 @@ libhaagenti_hip.so through ctypes:
                     (crates/haagenti-core/src/traits.rs:56-91,
                     crates/haagenti-lz4/src/decompress.rs:28-68), decoded on GPU
   Lz4Compressor     Compressor side (crates/haagenti-lz4/src/compress.rs:59-99)
-  HipContext        GpuContext / GpuDecompressor (crates/haagenti-cuda/src/lib.rs:89-230)
+  HipContext        GpuContext / GpuDctContext (crates/haagenti-cuda/src/lib.rs:89-230,
+                    dct_gpu.rs): idct_2d / dct_2d of whole matrices
+  GpuDecompressor   HCT V3 fragment containers decoded on the GPU
+                    (crates/haagenti-cuda/src/decompress.rs:108-443)
+  CompressiveSpectralDecoder / CompressiveSpectralEncoder
+                    crates/haagenti/src/compressive.rs:67-752
   HaagentiError     haagenti_core::Error (crates/haagenti-core/src/error.rs:10-135)
 
 Device entry points take torch tensors (or raw device addresses) for
@@ -128,6 +133,18 @@ _sig("hh_xxh3_64_batch", _i32, [_vp, _vp, _sz, _vp, _vp, _u32, _vp, _vp])
 _sig("hh_hct_decompress_all", _i32, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_sz),
                                       C.POINTER(BlockStatus), C.POINTER(C.c_int64), _vp])
 
+_sig("hh_hct3_coefficients", _i32, [_vp, _vp, _sz, C.c_uint64, _vp, _vp])
+_sig("hh_hct3_decompress", _i32, [_vp, _vp, _sz, _vp, _u32, _i32, _vp, _vp])
+_sig("hh_hct3_decompress_device", _i32, [_vp, _vp, _vp, _sz, _vp, _u32, _i32, _vp, _vp])
+_sig("hh_spectral_reconstruct", _i32, [_vp, _vp, _vp, _vp, _u32, _i32, _vp, C.c_uint64,
+                                       C.POINTER(_u32), C.POINTER(_u32), C.POINTER(BlockStatus), _vp])
+_sig("hh_idct_2d", _i32, [_vp, _vp, _u32, _u32, _i32, _vp, _vp])
+_sig("hh_dct_2d", _i32, [_vp, _vp, _u32, _u32, _vp, _vp])
+_sig("hh_spectral_encoded_size", _sz, [_u32, _u32, C.c_uint16, C.c_float, C.c_float,
+                                        C.POINTER(_u32), C.POINTER(_u32)])
+_sig("hh_spectral_encode_from_dct", _i32, [_vp, _u32, _u32, C.c_uint16, C.c_float, C.c_float, _vp,
+                                           _sz, _vp, C.POINTER(_sz)])
+
 # Every symbol include/haagenti_hip.h declares (checked by the tests).
 EXPORTS = [
     "hh_status_category", "hh_status_is_recoverable", "hh_version", "hh_device_count",
@@ -138,7 +155,9 @@ EXPORTS = [
     "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_encode",
     "hh_hct_read_header", "hh_hct_decompress_all",
     "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
-    "hh_hct_validate_checksums",
+    "hh_hct_validate_checksums", "hh_hct3_coefficients", "hh_hct3_decompress", "hh_hct3_decompress_device",
+    "hh_spectral_reconstruct", "hh_idct_2d", "hh_dct_2d", "hh_spectral_encoded_size",
+    "hh_spectral_encode_from_dct",
 ]
 
 CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8
@@ -590,3 +609,219 @@ def hctt_encode(w, k, threads=0):
     _check(_lib.hh_hctt_encode(w.ctypes.data, rows, cols, int(k), out.ctypes.data, int(threads)),
            "hh_hctt_encode")
     return out
+
+
+# ------------------------------------------------------------- HCT3 spectral
+
+def _shape_arr(shape):
+    shape = [int(d) for d in shape]
+    return (C.c_uint64 * max(len(shape), 1))(*shape), len(shape)
+
+
+def _dims(shape):
+    """GpuDecompressor::calculate_dimensions (decompress.rs:430-442)."""
+    shape = [int(d) for d in shape]
+    if not shape:
+        return 1, 1
+    w = shape[-1]
+    n = 1
+    for d in shape:
+        n *= d
+    return w, (n // w if w else 0)
+
+
+def _torch_dtype(dtype):
+    import torch
+    return {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[dtype]
+
+
+class GpuDecompressor:
+    """GpuDecompressor (crates/haagenti-cuda/src/decompress.rs:108-443) for HCT
+    V3 fragment containers: decompress(), decompress_to_gpu(),
+    decompress_batch(), plus reconstruct_coefficients_gpu() (the dense DCT
+    coefficient matrix before the transform).  zstd-framed input raises
+    UNSUPPORTED."""
+
+    def __init__(self, ctx=None):
+        self.ctx = ctx if ctx is not None else HipContext(0)
+
+    def reconstruct_coefficients_gpu(self, compressed, total, stream=None):
+        import torch
+        b = bytes(compressed)
+        out = torch.empty(max(int(total), 1), dtype=torch.float32, device="cuda")
+        _check(_lib.hh_hct3_coefficients(self.ctx.handle, b, len(b), int(total), _addr(out), stream),
+               "hh_hct3_coefficients")
+        return out[:int(total)]
+
+    def decompress_to_gpu(self, compressed, shape, dtype=F32, d_out=None, stream=None):
+        import torch
+        b = bytes(compressed)
+        w, h = _dims(shape)
+        n = w * h
+        if d_out is None:
+            d_out = torch.empty(max(n, 1), dtype=_torch_dtype(dtype), device="cuda")
+        arr, rank = _shape_arr(shape)
+        _check(_lib.hh_hct3_decompress(self.ctx.handle, b, len(b), arr, rank, int(dtype), _addr(d_out),
+                                       stream), "hh_hct3_decompress")
+        return d_out[:n]
+
+    def decompress_device(self, h_data, d_data, shape, d_out, dtype=F32, stream=None):
+        """Decode with the container already on the device (d_data, a copy of
+        h_data): asynchronous on the stream (hh_hct3_decompress_device)."""
+        b = bytes(h_data)
+        arr, rank = _shape_arr(shape)
+        _check(_lib.hh_hct3_decompress_device(self.ctx.handle, b, _addr(d_data), len(b), arr, rank, int(dtype),
+                                              _addr(d_out), stream), "hh_hct3_decompress_device")
+        return d_out
+
+    def decompress(self, compressed, shape):
+        """Reconstructed tensor as a flat float32 numpy array."""
+        return self.decompress_to_gpu(compressed, shape).cpu().numpy()
+
+    def decompress_batch(self, tensors):
+        return [self.decompress(c, s) for c, s in tensors]
+
+
+class CompressiveSpectralDecoder:
+    """CompressiveSpectralDecoder (compressive.rs:420-752): add_essentials()
+    (fragment 0) then add_detail() for any subset of the detail fragments;
+    reconstruct() runs the scatter and the whole-matrix IDCT on the GPU.
+    Fragments are (index, bytes) pairs or objects with .index and .data."""
+
+    def __init__(self, ctx=None):
+        self.ctx = ctx if ctx is not None else HipContext(0)
+        self._frags = []
+
+    @staticmethod
+    def _split(fragment):
+        if isinstance(fragment, tuple):
+            return int(fragment[0]), bytes(fragment[1])
+        return int(fragment.index), bytes(fragment.data)
+
+    def add_essentials(self, fragment):
+        idx, data = self._split(fragment)
+        if idx != 0:
+            raise HaagentiError(CORRUPTED_DATA, "fragment 0 must be added first for CompressiveSpectralDecoder")
+        self._frags = [(0, data)]
+        self._probe()
+
+    def add_detail(self, fragment):
+        if not self._frags:
+            raise HaagentiError(CORRUPTED_DATA, "must add fragment 0 (essentials) first")
+        idx, data = self._split(fragment)
+        if idx == 0:
+            return
+        self._frags.append((idx, data))
+        self._probe()
+
+    def can_reconstruct(self):
+        return bool(self._frags)
+
+    def _call(self, dtype=F32, d_out=None, out_cap=0, stream=None):
+        n = len(self._frags)
+        bufs = [d for _, d in self._frags]
+        ptrs = (_vp * n)(*[C.cast(C.c_char_p(d), _vp) for d in bufs])
+        lens = (_sz * n)(*[len(d) for d in bufs])
+        idx = (C.c_uint16 * n)(*[i for i, _ in self._frags])
+        w, h, st = _u32(0), _u32(0), BlockStatus()
+        rc = _lib.hh_spectral_reconstruct(self.ctx.handle, ptrs, lens, idx, n, int(dtype), _addr(d_out),
+                                          int(out_cap), C.byref(w), C.byref(h), C.byref(st), stream)
+        return rc, w.value, h.value, st
+
+    def _probe(self):
+        # parse and validate without reconstructing (no output buffer)
+        rc, w, h, st = self._call()
+        if rc not in (OK, INVALID_ARGUMENT):
+            raise HaagentiError(rc, "compressive spectral fragment", st)
+        self.width, self.height = w, h
+
+    def reconstruct_gpu(self, dtype=F32, d_out=None, stream=None):
+        import torch
+        if not self._frags:
+            raise HaagentiError(CORRUPTED_DATA, "need essentials fragment to reconstruct")
+        n = self.width * self.height
+        if d_out is None:
+            d_out = torch.empty(max(n, 1), dtype=_torch_dtype(dtype), device="cuda")
+        rc, w, h, st = self._call(dtype, d_out, d_out.numel(), stream)
+        if rc != OK:
+            raise HaagentiError(rc, "compressive spectral reconstruct", st)
+        return d_out[:n]
+
+    def reconstruct(self):
+        return self.reconstruct_gpu().cpu().numpy()
+
+
+class CompressiveSpectralEncoder:
+    """CompressiveSpectralEncoder (compressive.rs:67-340), producer: the DCT of
+    the tensor on the GPU (GpuDctContext::dct_2d, as the turbo encoder uses),
+    then retention, bitmap and f16 fragments on the host
+    (hh_spectral_encode_from_dct).  Fragments are returned as (index, bytes);
+    the forward DCT's rounding differs from the reference's FFT DCT, so
+    near-tied magnitudes may be retained differently."""
+
+    def __init__(self, num_fragments, retention_ratio, ctx=None):
+        self.num_fragments = int(num_fragments)
+        self.retention_ratio = float(retention_ratio)
+        self.essential_ratio = 0.2
+        self.ctx = ctx
+
+    def with_essential_ratio(self, ratio):
+        self.essential_ratio = float(ratio)
+        return self
+
+    def encode_2d_from_dct(self, dct_coeffs, width, height):
+        import numpy as np
+        c = np.ascontiguousarray(dct_coeffs, dtype=np.float32).ravel()
+        if c.size != width * height:
+            raise HaagentiError(CORRUPTED_DATA, "DCT coefficients size mismatch")
+        size = int(_lib.hh_spectral_encoded_size(width, height, self.num_fragments, self.retention_ratio,
+                                                 self.essential_ratio, None, None))
+        out = C.create_string_buffer(max(size, 1))
+        offs = (C.c_uint64 * (self.num_fragments + 1))()
+        w = _sz(0)
+        _check(_lib.hh_spectral_encode_from_dct(c.ctypes.data, width, height, self.num_fragments,
+                                                self.retention_ratio, self.essential_ratio, out, size,
+                                                offs, C.byref(w)), "hh_spectral_encode_from_dct")
+        raw = out.raw
+        return [(f, raw[offs[f]:offs[f + 1]]) for f in range(self.num_fragments)]
+
+    def encode_2d(self, data, width, height):
+        import numpy as np
+        import torch
+        ctx = self.ctx if self.ctx is not None else HipContext(0)
+        x = torch.as_tensor(np.ascontiguousarray(data, dtype=np.float32).ravel()).cuda()
+        if x.numel() != width * height:
+            raise HaagentiError(CORRUPTED_DATA, "data size mismatch")
+        c = torch.empty_like(x)
+        ctx.dct_2d(x, height, width, c)
+        torch.cuda.synchronize()
+        return self.encode_2d_from_dct(c.cpu().numpy(), width, height)
+
+
+def hct3_container(fragments):
+    """The fragment container the turbo pipeline serializes before its zstd
+    wrapper (crates/haagenti/src/pipeline/turbo.rs:378-387): [u16 n] then per
+    fragment index, flags (0), XXH3-64 of the data, u32 length, data."""
+    import struct
+    out = struct.pack("<H", len(fragments))
+    for idx, data in fragments:
+        data = bytes(data)
+        out += struct.pack("<HHQI", idx, 0, xxh3_64(data), len(data)) + data
+    return out
+
+
+def _hip_dct(self, d_in, rows, cols, d_out, stream=None):
+    """Orthonormal 2-D DCT-II of a row-major rows x cols f32 device matrix
+    (hh_dct_2d; GpuDctContext::dct_2d)."""
+    _check(_lib.hh_dct_2d(self.handle, _addr(d_in), int(rows), int(cols), _addr(d_out), stream), "hh_dct_2d")
+
+
+def _hip_idct(self, d_in, rows, cols, d_out, dtype=F32, stream=None):
+    """Orthonormal 2-D DCT-III of a row-major rows x cols f32 device matrix
+    (hh_idct_2d; GpuDctContext::idct_2d_gpu)."""
+    _check(_lib.hh_idct_2d(self.handle, _addr(d_in), int(rows), int(cols), int(dtype), _addr(d_out), stream),
+           "hh_idct_2d")
+
+
+HipContext.dct_2d = _hip_dct
+HipContext.idct_2d = _hip_idct

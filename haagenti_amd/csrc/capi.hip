@@ -7,14 +7,7 @@
 
 #include "hh_internal.hpp"
 
-namespace {
-
-// The caller's stream is used as given; NULL is HIP's null stream (torch's
-// default stream is that null stream).  hh_context_stream() returns the
-// context's own stream for callers that want it.
-hipStream_t pick_stream(hh_context *, void *stream) {
-    return reinterpret_cast<hipStream_t>(stream);
-}
+namespace hh {
 
 int32_t from_hip(hipError_t e) {
     switch (e) {
@@ -46,6 +39,20 @@ int32_t ensure_scratch(hh_context *ctx, size_t bytes) {
     }
     ctx->scratch_bytes = sz;
     return HH_OK;
+}
+
+}  // namespace hh
+
+namespace {
+
+using hh::ensure_scratch;
+using hh::from_hip;
+
+// The caller's stream is used as given; NULL is HIP's null stream (torch's
+// default stream is that null stream).  hh_context_stream() returns the
+// context's own stream for callers that want it.
+hipStream_t pick_stream(hh_context *, void *stream) {
+    return reinterpret_cast<hipStream_t>(stream);
 }
 
 }  // namespace
@@ -154,6 +161,7 @@ void hh_context_destroy(hh_context *ctx) {
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     if (ctx->d_basis) hipFree(ctx->d_basis);
     if (ctx->d_scratch) hipFree(ctx->d_scratch);
+    hh::release_dct_resources(ctx);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
     delete ctx;
 }

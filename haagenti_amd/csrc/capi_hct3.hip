@@ -1,0 +1,448 @@
+// C-ABI of the HCT3 whole-tensor spectral path: fragment parsing on the
+// host, coefficient scatter and whole-matrix DCTs on the GPU
+// (hct3_decode.hip).  Declarations and the reference interfaces replaced
+// are in include/haagenti_hip.h.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "hh_internal.hpp"
+
+namespace {
+
+using hh::ensure_scratch;
+using hh::from_hip;
+
+constexpr uint32_t kMagicHct2 = 0x48435432u;  // "HCT2" (compressive.rs:23)
+constexpr uint32_t kMagicHct3 = 0x48435433u;  // "HCT3" (compressive.rs:26)
+
+uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+uint32_t rd32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+void wr16(std::vector<uint8_t> &o, uint16_t v) {
+    o.push_back((uint8_t)v);
+    o.push_back((uint8_t)(v >> 8));
+}
+void wr32(std::vector<uint8_t> &o, uint32_t v) {
+    for (int i = 0; i < 4; i++) o.push_back((uint8_t)(v >> (8 * i)));
+}
+size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+bool valid_dtype(int32_t d) { return d == HH_F32 || d == HH_F16 || d == HH_BF16; }
+
+// One scatter pass: a bitmap of `total` bits and its coefficient values
+// (host pointers), values in rank order.
+struct Layer {
+    const uint8_t *bitmap;
+    const void *coef;
+    uint32_t ncoef;
+};
+
+// Scatters the layers in order into d_dense (total f32), staging each
+// layer's bitmap and values through ctx scratch at d_stage.  Returns after
+// enqueueing on s.
+int32_t scatter_layers(const std::vector<Layer> &layers, uint64_t total, int coef_f32, float *d_dense,
+                       uint8_t *d_stage, hipStream_t s) {
+    if (layers.empty()) return from_hip(hipMemsetAsync(d_dense, 0, total * sizeof(float), s));
+    const size_t bm = (size_t)((total + 7) / 8);
+    const size_t words = align16(bm);
+    uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
+    uint8_t *d_bits = d_stage + align16(hh::hct3_block_sums_bytes(total));
+    uint8_t *d_coef = d_bits + words;
+    const size_t csz = coef_f32 ? 4 : 2;
+    for (size_t i = 0; i < layers.size(); i++) {
+        const Layer &L = layers[i];
+        hipError_t e = hipMemcpyAsync(d_bits, L.bitmap, bm, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess && L.ncoef)
+            e = hipMemcpyAsync(d_coef, L.coef, (size_t)L.ncoef * csz, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hh::launch_hct3_scatter(reinterpret_cast<const uint64_t *>(d_bits), total, d_sums, d_coef,
+                                        L.ncoef, coef_f32, d_dense, i == 0 ? 1 : 0, s);
+        if (e != hipSuccess) return from_hip(e);
+    }
+    return HH_OK;
+}
+
+// The same with the container already in device memory: each layer's
+// bitmap is repacked into aligned words; values are read in place.
+int32_t scatter_layers_device(const std::vector<Layer> &layers, const uint8_t *h_base, const uint8_t *d_base,
+                              uint64_t total, float *d_dense, uint8_t *d_stage, hipStream_t s) {
+    if (layers.empty()) return from_hip(hipMemsetAsync(d_dense, 0, total * sizeof(float), s));
+    const size_t bm = (size_t)((total + 7) / 8);
+    uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
+    uint64_t *d_bits = reinterpret_cast<uint64_t *>(d_stage + align16(hh::hct3_block_sums_bytes(total)));
+    for (size_t i = 0; i < layers.size(); i++) {
+        const Layer &L = layers[i];
+        const uint8_t *bits = d_base + (L.bitmap - h_base);
+        const uint8_t *coef = d_base + (reinterpret_cast<const uint8_t *>(L.coef) - h_base);
+        hipError_t e = hh::launch_pack_bits(bits, bm, d_bits, s);
+        if (e == hipSuccess)
+            e = hh::launch_hct3_scatter(d_bits, total, d_sums, coef, L.ncoef, 0, d_dense, i == 0 ? 1 : 0, s);
+        if (e != hipSuccess) return from_hip(e);
+    }
+    return HH_OK;
+}
+
+size_t stage_bytes(uint64_t total, uint32_t max_coef, int coef_f32) {
+    return align16(hh::hct3_block_sums_bytes(total)) + align16((size_t)((total + 7) / 8)) +
+           align16((size_t)max_coef * (coef_f32 ? 4 : 2)) + 16;
+}
+
+// width = last dimension, height = product of the others
+// (GpuDecompressor::calculate_dimensions, decompress.rs:430-442).
+int32_t dims_of(const uint64_t *shape, uint32_t rank, uint64_t *total, uint32_t *rows, uint32_t *cols) {
+    if (rank > 8 || (rank > 0 && !shape)) return HH_ERR_INVALID_ARGUMENT;
+    uint64_t t = 1;
+    for (uint32_t i = 0; i < rank; i++) {
+        if (shape[i] != 0 && t > UINT64_MAX / shape[i]) return HH_ERR_INVALID_ARGUMENT;
+        t *= shape[i];
+    }
+    const uint64_t w = rank == 0 ? 1 : shape[rank - 1];
+    const uint64_t h = w == 0 ? 0 : t / w;
+    // ranks are 32-bit on the device; GEMM dimensions are int
+    if (t > 0xffffffffull || w > 0x7fffffffull || h > 0x7fffffffull) return HH_ERR_INVALID_ARGUMENT;
+    *total = t;
+    *rows = (uint32_t)h;
+    *cols = (uint32_t)w;
+    return HH_OK;
+}
+
+// GpuDecompressor::parse_hct_fragments (decompress.rs:322-397): the
+// coefficient count of a fragment is the number of whole f16 values after
+// its bitmap (its num_coefficients field is not used).
+int32_t parse_container(const uint8_t *data, size_t len, uint64_t total, std::vector<Layer> &out) {
+    if (len < 2) return HH_ERR_INVALID_ARGUMENT;  // "HCT data too short"
+    const uint32_t nf = rd16(data);
+    size_t off = 2;
+    const uint64_t bm = (total + 7) / 8;
+    for (uint32_t f = 0; f < nf; f++) {
+        if (off + 16 > len) break;
+        off += 12;  // index, flags, checksum
+        const uint32_t dl = rd32(data + off);
+        off += 4;
+        if ((size_t)dl > len - off) return HH_ERR_INVALID_ARGUMENT;  // "Fragment N extends past data end"
+        const uint8_t *fd = data + off;
+        off += dl;
+        if (dl < 4 || (uint64_t)dl < 4 + bm) continue;
+        const uint64_t nc = ((uint64_t)dl - 4 - bm) / 2;
+        out.push_back(Layer{fd + 4, fd + 4 + bm, (uint32_t)nc});
+    }
+    return HH_OK;
+}
+
+bool zstd_framed(const uint8_t *d, size_t len) {
+    return len >= 4 && d[0] == 0x28 && d[1] == 0xB5 && d[2] == 0x2F && d[3] == 0xFD;
+}
+
+// IDCT of d_dense into d_out (dtype), with d_tmp as the GEMM intermediate;
+// d_dense is overwritten for 16-bit outputs.
+int32_t inverse_to(hh_context *ctx, float *d_dense, float *d_tmp, uint32_t rows, uint32_t cols,
+                   int32_t dtype, void *d_out, hipStream_t s) {
+    const uint64_t total = (uint64_t)rows * cols;
+    float *x = dtype == HH_F32 ? reinterpret_cast<float *>(d_out) : d_dense;
+    int32_t rc = hh::dct2d_full(ctx, true, d_dense, d_tmp, x, rows, cols, s);
+    if (rc != HH_OK) return rc;
+    if (dtype != HH_F32) return from_hip(hh::launch_f32_convert(x, total, dtype, d_out, s));
+    return HH_OK;
+}
+
+// f32 -> f16 bits, round to nearest even (half::f16::from_f32).
+uint16_t f32_to_f16_rne(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));  // NaN (quiet)
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);                          // overflow -> inf
+    if (a < 0x38800000u) {                                                             // subnormal / zero
+        if (a < 0x33000000u) return (uint16_t)sign;
+        const uint32_t e = a >> 23, m = (a & 0x7fffffu) | 0x800000u;
+        const uint32_t sh = 126 - e;  // 14..24
+        uint32_t r = m >> sh;
+        const uint32_t rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (r & 1))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((a - 0x38000000u) >> 13);
+    const uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1))) r++;
+    return (uint16_t)(sign | r);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t hh_hct3_coefficients(hh_context *ctx, const uint8_t *data, size_t len, uint64_t total,
+                             float *d_coeffs, void *stream) {
+    if (!ctx || !data || (total && !d_coeffs) || total > 0xffffffffull) return HH_ERR_INVALID_ARGUMENT;
+    if (zstd_framed(data, len)) return HH_ERR_UNSUPPORTED;
+    std::vector<Layer> layers;
+    int32_t rc = parse_container(data, len, total, layers);
+    if (rc != HH_OK || total == 0) return rc;
+    uint32_t mc = 0;
+    for (const Layer &L : layers) mc = std::max(mc, L.ncoef);
+    hipSetDevice(ctx->device);
+    rc = ensure_scratch(ctx, stage_bytes(total, mc, 0));
+    if (rc != HH_OK) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = scatter_layers(layers, total, 0, d_coeffs, reinterpret_cast<uint8_t *>(ctx->d_scratch), s);
+    if (rc != HH_OK) return rc;
+    return from_hip(hipStreamSynchronize(s));
+}
+
+int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, const uint64_t *shape,
+                           uint32_t rank, int32_t out_dtype, void *d_out, void *stream) {
+    if (!ctx || !data || !valid_dtype(out_dtype)) return HH_ERR_INVALID_ARGUMENT;
+    uint64_t total;
+    uint32_t rows, cols;
+    int32_t rc = dims_of(shape, rank, &total, &rows, &cols);
+    if (rc != HH_OK) return rc;
+    if (zstd_framed(data, len)) return HH_ERR_UNSUPPORTED;
+    std::vector<Layer> layers;
+    rc = parse_container(data, len, total, layers);
+    if (rc != HH_OK || total == 0) return rc;
+    if (!d_out) return HH_ERR_INVALID_ARGUMENT;
+    uint32_t mc = 0;
+    for (const Layer &L : layers) mc = std::max(mc, L.ncoef);
+    hipSetDevice(ctx->device);
+    const size_t mat = align16((size_t)total * sizeof(float));
+    rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, mc, 0));
+    if (rc != HH_OK) return rc;
+    uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+    float *d_dense = reinterpret_cast<float *>(base);
+    float *d_tmp = reinterpret_cast<float *>(base + mat);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = scatter_layers(layers, total, 0, d_dense, base + 2 * mat, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s);
+    if (rc != HH_OK) return rc;
+    return from_hip(hipStreamSynchronize(s));
+}
+
+int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const uint8_t *d_data, size_t len,
+                                  const uint64_t *shape, uint32_t rank, int32_t out_dtype, void *d_out,
+                                  void *stream) {
+    if (!ctx || !h_data || !d_data || !valid_dtype(out_dtype)) return HH_ERR_INVALID_ARGUMENT;
+    uint64_t total;
+    uint32_t rows, cols;
+    int32_t rc = dims_of(shape, rank, &total, &rows, &cols);
+    if (rc != HH_OK) return rc;
+    if (zstd_framed(h_data, len)) return HH_ERR_UNSUPPORTED;
+    std::vector<Layer> layers;
+    rc = parse_container(h_data, len, total, layers);
+    if (rc != HH_OK || total == 0) return rc;
+    if (!d_out) return HH_ERR_INVALID_ARGUMENT;
+    hipSetDevice(ctx->device);
+    const size_t mat = align16((size_t)total * sizeof(float));
+    rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, 0, 0));
+    if (rc != HH_OK) return rc;
+    uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+    float *d_dense = reinterpret_cast<float *>(base);
+    float *d_tmp = reinterpret_cast<float *>(base + mat);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = scatter_layers_device(layers, h_data, d_data, total, d_dense, base + 2 * mat, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s);
+    return rc;
+}
+
+int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, const size_t *frag_lens,
+                                const uint16_t *frag_index, uint32_t nfrags, int32_t out_dtype,
+                                void *d_out, uint64_t out_cap, uint32_t *width, uint32_t *height,
+                                hh_block_status *status, void *stream) {
+    if (status) std::memset(status, 0, sizeof(*status));
+    auto corrupt = [&](int32_t detail) {
+        if (status) {
+            status->code = HH_ERR_CORRUPTED_DATA;
+            status->detail = detail;
+        }
+        return (int32_t)HH_ERR_CORRUPTED_DATA;
+    };
+    if (!ctx || !frags || !frag_lens || !frag_index || nfrags == 0 || !valid_dtype(out_dtype))
+        return HH_ERR_INVALID_ARGUMENT;
+    // add_essentials (compressive.rs:438-465)
+    if (frag_index[0] != 0) return corrupt(HH_CORRUPT_HEADER);  // "fragment 0 must be added first"
+    const uint8_t *f0 = frags[0];
+    const size_t l0 = frag_lens[0];
+    if (!f0 || l0 < 24) return corrupt(HH_CORRUPT_SIZE);  // "fragment 0 too short"
+    const uint32_t magic = rd32(f0);
+    // V1 (explicit index array, compressive.rs:467-520) is not decoded here
+    if (magic != kMagicHct3 && magic != kMagicHct2) return HH_ERR_UNSUPPORTED;
+    const int f32c = magic == kMagicHct2;
+    const size_t csz = f32c ? 4 : 2;
+    const uint32_t w = rd32(f0 + 4), h = rd32(f0 + 8), ntot = rd32(f0 + 12), ness = rd32(f0 + 16),
+                   dpf = rd32(f0 + 20);
+    const uint64_t n = (uint64_t)w * h;
+    if (width) *width = w;
+    if (height) *height = h;
+    if (n > 0xffffffffull || w > 0x7fffffffu || h > 0x7fffffffu) return HH_ERR_INVALID_ARGUMENT;
+    const uint64_t bm = (n + 7) / 8;
+    if (24 + bm > l0) return corrupt(HH_CORRUPT_SIZE);  // "truncated bitmap"
+    uint64_t cnt = 0;
+    for (uint64_t i = 0; i < bm; i++) {
+        uint32_t b = f0[24 + i];
+        if (i == bm - 1 && (n & 7)) b &= (1u << (n & 7)) - 1;  // bits past n are not scanned
+        cnt += (uint64_t)__builtin_popcount(b);
+    }
+    if (cnt != ntot) return corrupt(HH_CORRUPT_BITMAP_COUNT);  // compressive.rs:630-636
+    // coefficients in index-map order; unset entries stay 0.0
+    std::vector<uint8_t> coef((size_t)ntot * csz, 0);
+    size_t off = 24 + (size_t)bm;
+    for (uint32_t i = 0; i < ness; i++) {
+        if (off + csz > l0) return corrupt(HH_CORRUPT_SIZE);  // "truncated essential coefficients"
+        if (i >= ntot) return corrupt(HH_CORRUPT_SIZE);       // the reference indexes past its array
+        std::memcpy(&coef[(size_t)i * csz], f0 + off, csz);
+        off += csz;
+    }
+    // add_detail (compressive.rs:653-700)
+    for (uint32_t f = 1; f < nfrags; f++) {
+        if (frag_index[f] == 0) continue;
+        const uint8_t *d = frags[f];
+        const size_t l = frag_lens[f];
+        if (!d || l < 8) return corrupt(HH_CORRUPT_SIZE);  // "detail fragment too short"
+        const uint32_t fi = rd16(d);
+        const uint32_t count = rd32(d + 4);
+        if (fi == 0) return corrupt(HH_CORRUPT_HEADER);  // start would underflow in the reference
+        const uint64_t start = (uint64_t)ness + (uint64_t)(fi - 1) * dpf;
+        size_t o = 8;
+        for (uint32_t i = 0; i < count; i++) {
+            if (o + csz > l) break;
+            const uint64_t idx = start + i;
+            if (idx < ntot) std::memcpy(&coef[(size_t)idx * csz], d + o, csz);
+            o += csz;
+        }
+    }
+    if (n == 0) return HH_OK;
+    if (!d_out) return HH_ERR_INVALID_ARGUMENT;
+    if (out_cap < n) {
+        if (status) {
+            status->code = HH_ERR_BUFFER_TOO_SMALL;
+            status->required = n;
+        }
+        return HH_ERR_BUFFER_TOO_SMALL;
+    }
+    // reconstruct (compressive.rs:728-752): one scatter with fragment 0's bitmap
+    hipSetDevice(ctx->device);
+    const size_t mat = align16((size_t)n * sizeof(float));
+    int32_t rc = ensure_scratch(ctx, 2 * mat + stage_bytes(n, ntot, f32c));
+    if (rc != HH_OK) return rc;
+    uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+    float *d_dense = reinterpret_cast<float *>(base);
+    float *d_tmp = reinterpret_cast<float *>(base + mat);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    std::vector<Layer> layers{Layer{f0 + 24, coef.data(), ntot}};
+    rc = scatter_layers(layers, n, f32c, d_dense, base + 2 * mat, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, h, w, out_dtype, d_out, s);
+    if (rc != HH_OK) return rc;
+    if (status) status->written = n;
+    return from_hip(hipStreamSynchronize(s));
+}
+
+int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, int32_t out_dtype,
+                   void *d_out, void *stream) {
+    if (!ctx || !valid_dtype(out_dtype) || rows > 0x7fffffffu || cols > 0x7fffffffu) return HH_ERR_INVALID_ARGUMENT;
+    const uint64_t total = (uint64_t)rows * cols;
+    if (total == 0) return HH_OK;
+    if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
+    hipSetDevice(ctx->device);
+    const size_t mat = align16((size_t)total * sizeof(float));
+    int32_t rc = ensure_scratch(ctx, out_dtype == HH_F32 ? mat : 2 * mat);
+    if (rc != HH_OK) return rc;
+    float *d_tmp = reinterpret_cast<float *>(ctx->d_scratch);
+    float *x = out_dtype == HH_F32 ? reinterpret_cast<float *>(d_out)
+                                   : reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->d_scratch) + mat);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = hh::dct2d_full(ctx, true, d_in, d_tmp, x, rows, cols, s);
+    if (rc == HH_OK && out_dtype != HH_F32) rc = from_hip(hh::launch_f32_convert(x, total, out_dtype, d_out, s));
+    return rc;
+}
+
+int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, float *d_out,
+                  void *stream) {
+    if (!ctx || rows > 0x7fffffffu || cols > 0x7fffffffu) return HH_ERR_INVALID_ARGUMENT;
+    const uint64_t total = (uint64_t)rows * cols;
+    if (total == 0) return HH_OK;
+    if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
+    hipSetDevice(ctx->device);
+    int32_t rc = ensure_scratch(ctx, align16((size_t)total * sizeof(float)));
+    if (rc != HH_OK) return rc;
+    return hh::dct2d_full(ctx, false, d_in, reinterpret_cast<float *>(ctx->d_scratch), d_out, rows, cols,
+                          reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t hh_spectral_encoded_size(uint32_t width, uint32_t height, uint16_t num_fragments, float retention,
+                                float essential_ratio, uint32_t *retain_count, uint32_t *essential_count) {
+    const uint64_t n = (uint64_t)width * height;
+    const float rr = std::min(std::max(retention, 0.05f), 1.0f);
+    const float er = std::min(std::max(essential_ratio, 0.05f), 1.0f);
+    uint64_t keep = (uint64_t)((float)n * rr);
+    if (keep < 1) keep = 1;
+    if (keep > n) keep = n;
+    uint64_t ess = (uint64_t)((float)keep * er);
+    if (ess < 1) ess = 1;
+    if (retain_count) *retain_count = (uint32_t)keep;
+    if (essential_count) *essential_count = (uint32_t)ess;
+    const uint64_t det = keep > ess ? keep - ess : 0;
+    const uint64_t nf = num_fragments ? num_fragments : 1;
+    const uint64_t dpf = nf > 1 ? (det + nf - 2) / (nf - 1) : det;
+    uint64_t size = 24 + (n + 7) / 8 + 2 * ess;
+    for (uint64_t f = 1; f < nf; f++) {
+        const uint64_t start = ess + (f - 1) * dpf;
+        const uint64_t end = std::min(start + dpf, keep);
+        size += 8 + 2 * (end > start ? end - start : 0);
+    }
+    return (size_t)size;
+}
+
+int32_t hh_spectral_encode_from_dct(const float *coeffs, uint32_t width, uint32_t height, uint16_t num_fragments,
+                                    float retention, float essential_ratio, uint8_t *out, size_t out_cap,
+                                    uint64_t *frag_offsets, size_t *written) {
+    if (!coeffs || num_fragments == 0 || !out || !frag_offsets) return HH_ERR_INVALID_ARGUMENT;
+    const uint64_t n = (uint64_t)width * height;
+    if (n == 0 || n > 0xffffffffull) return HH_ERR_INVALID_ARGUMENT;
+    uint32_t keep, ess;
+    const size_t need = hh_spectral_encoded_size(width, height, num_fragments, retention, essential_ratio, &keep, &ess);
+    if (written) *written = need;
+    if (out_cap < need) return HH_ERR_BUFFER_TOO_SMALL;
+    // stable descending sort by |c| (compressive.rs:263-268); NaN sorts last
+    std::vector<uint32_t> order(n);
+    std::iota(order.begin(), order.end(), 0u);
+    auto mag = [&](uint32_t i) {
+        const float a = std::fabs(coeffs[i]);
+        return std::isnan(a) ? -1.0f : a;
+    };
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return mag(a) > mag(b); });
+    std::vector<uint32_t> kept(order.begin(), order.begin() + keep);
+    std::sort(kept.begin(), kept.end());  // index order (:290-296)
+    const uint64_t det = keep - ess;
+    const uint64_t dpf = num_fragments > 1 ? (det + num_fragments - 2) / (num_fragments - 1) : det;
+    std::vector<uint8_t> o;
+    o.reserve(need);
+    wr32(o, kMagicHct3);
+    wr32(o, width);
+    wr32(o, height);
+    wr32(o, keep);
+    wr32(o, ess);
+    wr32(o, (uint32_t)dpf);
+    const size_t bm0 = o.size();
+    o.resize(bm0 + (size_t)((n + 7) / 8), 0);
+    for (uint32_t i : kept) o[bm0 + i / 8] |= (uint8_t)(1u << (i % 8));
+    for (uint32_t i = 0; i < ess; i++) wr16(o, f32_to_f16_rne(coeffs[kept[i]]));
+    frag_offsets[0] = 0;
+    for (uint32_t f = 1; f < num_fragments; f++) {
+        frag_offsets[f] = o.size();
+        wr16(o, (uint16_t)f);
+        wr16(o, num_fragments);
+        const uint64_t start = ess + (uint64_t)(f - 1) * dpf;
+        const uint64_t end = std::min<uint64_t>(start + dpf, keep);
+        wr32(o, (uint32_t)(end > start ? end - start : 0));
+        for (uint64_t i = start; i < end; i++) wr16(o, f32_to_f16_rne(coeffs[kept[i]]));
+    }
+    frag_offsets[num_fragments] = o.size();
+    std::memcpy(out, o.data(), o.size());
+    return HH_OK;
+}
+
+}  // extern "C"

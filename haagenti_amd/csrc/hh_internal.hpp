@@ -13,12 +13,28 @@ struct hh_context {
     // 64x64 inverse-DCT basis, pre-split into f16 hi/lo MFMA fragments in
     // per-lane order (see hctt_decode.hip), uploaded once per context.
     void *d_basis = nullptr;
-    // Small device scratch used by the host-pointer entry points.
+    // Device scratch used by the host-pointer and whole-tensor entry points
+    // (grown on demand, kept until the context is destroyed).
     void *d_scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Whole-matrix DCT bases B_n (hct3_decode.hip), two sizes cached, and the
+    // rocBLAS handle of the whole-matrix transforms, created on first use.
+    struct Basis {
+        uint32_t n = 0;
+        float *d = nullptr;
+        uint64_t stamp = 0;
+    };
+    Basis dct_basis[2];
+    uint64_t dct_stamp = 0;
+    void *blas = nullptr;
 };
 
 namespace hh {
+
+// hipError_t -> hh_status; grows ctx->d_scratch to at least `bytes`
+// (capi.hip).
+int32_t from_hip(hipError_t e);
+int32_t ensure_scratch(hh_context *ctx, size_t bytes);
 
 // ---- device helpers -------------------------------------------------------
 
@@ -82,6 +98,25 @@ uint64_t xxh3_64_host(const uint8_t *data, size_t len);
 // Build the MFMA basis fragments on the host (host_basis.cpp).
 size_t basis_table_bytes();
 void build_basis_table(void *host_buf);
+
+// HCT3 whole-tensor decode (hct3_decode.hip).  Scatter: the set bits of the
+// nbits-bit bitmap (64-bit words, 8-byte aligned) take coefficients (f16 or
+// f32, little-endian at any byte address) in rank order while rank < ncoef; `first` writes every output (zeros where no
+// value lands), otherwise only the assigned ones.  d_block_sums needs
+// hct3_block_sums_bytes(nbits).
+hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t *d_block_sums,
+                               const void *d_coef, uint32_t ncoef, int coef_f32, float *d_dense,
+                               int first, hipStream_t s);
+size_t hct3_block_sums_bytes(uint64_t nbits);
+// Bitmap bytes at any device address -> zero-padded 64-bit words.
+hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_words, hipStream_t s);
+hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_out, hipStream_t s);
+// Orthonormal 2-D DCT-III (inverse) or DCT-II (forward) of a row-major
+// rows x cols f32 matrix: two GEMMs through d_tmp (rows*cols f32); d_out may
+// not alias d_in or d_tmp.
+int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
+                   uint32_t rows, uint32_t cols, hipStream_t s);
+void release_dct_resources(hh_context *ctx);
 
 // Decodes n tensors (validated by the caller) in ceil(n/8) launches.
 hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dtype,

@@ -286,6 +286,81 @@ int32_t hh_hct_validate_checksums(hh_context *ctx, const uint8_t *h_file, const 
                                   size_t file_len, hh_block_status *status, int64_t *failed_block,
                                   void *stream);
 
+/* ------------------------------------------- HCT3 whole-tensor spectral */
+
+/* HCT V3 fragment container (the layout GpuDecompressor and the reference C
+ * decoder read): [u16 n] then n x {u16 index, u16 flags, u64 checksum,
+ * u32 len, len bytes}; a fragment's bytes are [u32 count][ceil(total/8)
+ * bitmap][f16 values]. */
+
+/* GpuDecompressor::parse_hct_fragments + reconstruct_coefficients
+ * (crates/haagenti-cuda/src/decompress.rs:322-427) on the GPU: the dense
+ * DCT coefficient matrix (total f32) of a container held in host memory.
+ * A fragment that ends past the data is HH_ERR_INVALID_ARGUMENT
+ * (CudaError::InvalidData); fragments shorter than 4 + bitmap bytes are
+ * skipped; each fragment's values fill its set bits in ascending order
+ * while they last, later fragments overwriting earlier ones.  zstd-framed
+ * input (magic 28 B5 2F FD) is HH_ERR_UNSUPPORTED.  Synchronous. */
+int32_t hh_hct3_coefficients(hh_context *ctx, const uint8_t *data, size_t len, uint64_t total,
+                             float *d_coeffs, void *stream);
+
+/* GpuDecompressor::decompress / decompress_to_gpu (decompress.rs:153-192):
+ * the coefficients as above, then the orthonormal inverse DCT of the whole
+ * height x width matrix (width = last dimension, height = product of the
+ * others, decompress.rs:430-442; idct_2d, haagenti-core/src/dct.rs:311-337)
+ * into d_out (product(shape) elements of out_dtype).  Synchronous. */
+int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, const uint64_t *shape,
+                           uint32_t rank, int32_t out_dtype, void *d_out, void *stream);
+
+/* hh_hct3_decompress with the container also resident in device memory
+ * (d_data, a copy of h_data; h_data is parsed on the host): no host-device
+ * copies, asynchronous on the stream. */
+int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const uint8_t *d_data, size_t len,
+                                  const uint64_t *shape, uint32_t rank, int32_t out_dtype, void *d_out,
+                                  void *stream);
+
+/* CompressiveSpectralDecoder::{add_essentials, add_detail, reconstruct}
+ * (crates/haagenti/src/compressive.rs:438-752) for the V3 (HCT3, f16) and V2
+ * (HCT2, f32) layouts: fragment 0 (frag_index[0] must be 0) holds
+ * [magic][width][height][retain][essential][detail_per_frag][bitmap][values],
+ * detail fragments [u16 idx][u16 total][u32 count][values]; fragments with
+ * frag_index 0 after the first are ignored.  Errors as the reference
+ * (HH_ERR_CORRUPTED_DATA with detail SIZE / BITMAP_COUNT / HEADER); the V1
+ * index-array layout is HH_ERR_UNSUPPORTED.  Writes width * height elements
+ * of out_dtype (HH_ERR_BUFFER_TOO_SMALL when out_cap is less).
+ * Synchronous. */
+int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, const size_t *frag_lens,
+                                const uint16_t *frag_index, uint32_t nfrags, int32_t out_dtype,
+                                void *d_out, uint64_t out_cap, uint32_t *width, uint32_t *height,
+                                hh_block_status *status, void *stream);
+
+/* GpuDctContext::idct_2d_gpu / idct_2d for a whole rows x cols matrix
+ * (crates/haagenti-cuda/src/dct_gpu.rs:1163-1227, 1404-1412): orthonormal
+ * 2-D DCT-III of the row-major f32 d_in into d_out (out_dtype), as two fp32
+ * GEMMs against cached DCT bases.  Asynchronous on the stream. */
+int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, int32_t out_dtype,
+                   void *d_out, void *stream);
+
+/* GpuDctContext::dct_2d (dct_gpu.rs, used by the turbo encoder,
+ * crates/haagenti/src/pipeline/turbo.rs:351-369): orthonormal 2-D DCT-II of
+ * a row-major f32 matrix (dct_2d, dct.rs:282-308).  Asynchronous. */
+int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, float *d_out,
+                  void *stream);
+
+/* Bytes of CompressiveSpectralEncoder's fragments for a width x height
+ * tensor (compressive.rs:94-238); *retain_count / *essential_count receive
+ * the coefficient counts (either may be NULL). */
+size_t hh_spectral_encoded_size(uint32_t width, uint32_t height, uint16_t num_fragments, float retention,
+                                float essential_ratio, uint32_t *retain_count, uint32_t *essential_count);
+
+/* CompressiveSpectralEncoder::encode_2d_from_dct (compressive.rs:240-340) on
+ * the host: top retention of the coefficients by magnitude (stable sort),
+ * fragment 0 and num_fragments - 1 detail fragments, concatenated into out;
+ * fragment f is out[frag_offsets[f] .. frag_offsets[f + 1]). */
+int32_t hh_spectral_encode_from_dct(const float *coeffs, uint32_t width, uint32_t height, uint16_t num_fragments,
+                                    float retention, float essential_ratio, uint8_t *out, size_t out_cap,
+                                    uint64_t *frag_offsets, size_t *written);
+
 #ifdef __cplusplus
 }
 #endif

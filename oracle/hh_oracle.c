@@ -1463,3 +1463,202 @@ void hho_xxh3_64_batch(const uint8_t *data, const uint64_t *off, const uint32_t 
     xxh_batch_ctx c = {data, off, len, out};
     hho_parallel_for(n, nthreads, xxh_batch_task, &c);
 }
+
+/* =====================================================================
+ * HCT3 whole-tensor spectral decode
+ * ===================================================================== */
+
+static uint16_t rd16le(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static uint32_t rd32le(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* half::f16::from_f32 (round to nearest even; NaN stays NaN). */
+uint16_t hho_f32_to_f16_rne(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (a < 0x38800000u) {
+        if (a < 0x33000000u) return (uint16_t)sign;
+        uint32_t e = a >> 23, m = (a & 0x7fffffu) | 0x800000u, sh = 126 - e;
+        uint32_t r = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (r & 1))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = (a - 0x38000000u) >> 13, rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1))) r++;
+    return (uint16_t)(sign | r);
+}
+
+/* parse_hct_fragments + reconstruct_coefficients
+ * (crates/haagenti-cuda/src/decompress.rs:322-427). */
+int hho_hct3_coefficients(const uint8_t *data, size_t len, size_t total, float *dense) {
+    if (len < 2) return HHO_INVALID_DATA;                 /* :324-326 */
+    for (size_t i = 0; i < total; i++) dense[i] = 0.0f;   /* :405 */
+    size_t nf = rd16le(data), off = 2, bm = (total + 7) / 8;
+    for (size_t f = 0; f < nf; f++) {
+        if (off + 16 > len) break;                        /* :335-337 */
+        off += 12;                                        /* index, flags, checksum */
+        size_t dl = rd32le(data + off);
+        off += 4;
+        if (off + dl > len) return HHO_INVALID_DATA;      /* :362-367 */
+        const uint8_t *fd = data + off;
+        off += dl;
+        if (dl < 4) continue;                             /* :373-375 */
+        if (dl < 4 + bm) continue;                        /* :380-383 */
+        const uint8_t *bits = fd + 4, *cd = fd + 4 + bm;
+        size_t nc = (dl - 4 - bm) / 2;                    /* chunks_exact(2), :388-394 */
+        size_t ci = 0;
+        for (size_t b = 0; b < bm; b++)                   /* :408-424 */
+            for (int k = 0; k < 8; k++) {
+                size_t e = b * 8 + (size_t)k;
+                if (e >= total) break;
+                if (((bits[b] >> k) & 1) && ci < nc) {
+                    dense[e] = hho_f16_bits_to_f32(rd16le(cd + 2 * ci));
+                    ci++;
+                }
+            }
+    }
+    return HHO_OK;
+}
+
+/* GpuDecompressor::decompress with the CPU transform: coefficients, then
+ * idct_2d (dct.rs:311-337) over width = last dimension, height = the rest
+ * (decompress.rs:430-442). */
+int hho_hct3_decode(const uint8_t *data, size_t len, const uint64_t *shape, size_t rank, float *out) {
+    size_t total = 1;
+    for (size_t i = 0; i < rank; i++) total *= (size_t)shape[i];
+    size_t w = rank == 0 ? 1 : (size_t)shape[rank - 1], h = w ? total / w : 0;
+    float *dense = (float *)malloc(sizeof(float) * (total ? total : 1));
+    int rc = hho_hct3_coefficients(data, len, total, dense);
+    if (rc == HHO_OK && total) hho_idct_2d(dense, out, w, h);
+    free(dense);
+    return rc;
+}
+
+/* CompressiveSpectralEncoder::encode_2d_from_dct (compressive.rs:240-340):
+ * fragment f is out[offsets[f] .. offsets[f+1]).  Returns the bytes
+ * written (0 when cap is short). */
+size_t hho_spectral_encode_from_dct(const float *dct, uint32_t width, uint32_t height, uint16_t nfrag,
+                                    float retention, float essential_ratio, uint8_t *out, size_t cap,
+                                    uint64_t *offsets) {
+    size_t n = (size_t)width * height;
+    float rr = retention < 0.05f ? 0.05f : retention > 1.0f ? 1.0f : retention;   /* :98 */
+    float er = essential_ratio < 0.05f ? 0.05f : essential_ratio > 1.0f ? 1.0f : essential_ratio; /* :107 */
+    size_t keep = (size_t)((float)n * rr);
+    if (keep < 1) keep = 1;
+    if (keep > n) keep = n;
+    size_t ess = (size_t)((float)keep * er);
+    if (ess < 1) ess = 1;
+    size_t det = keep - ess;
+    size_t dpf = nfrag > 1 ? (det + nfrag - 2) / (nfrag - 1) : det;
+    uint8_t *bm = (uint8_t *)malloc((n + 7) / 8 + 1);
+    uint32_t *idx = (uint32_t *)malloc(sizeof(uint32_t) * (keep ? keep : 1));
+    hho_topk_bitmap(dct, n, keep, bm, idx);
+    size_t need = 24 + (n + 7) / 8 + 2 * ess;
+    for (size_t f = 1; f < nfrag; f++) {
+        size_t s = ess + (f - 1) * dpf, e = s + dpf < keep ? s + dpf : keep;
+        need += 8 + 2 * (e > s ? e - s : 0);
+    }
+    if (need > cap) {
+        free(bm);
+        free(idx);
+        return 0;
+    }
+    uint8_t *p = out;
+#define W32(v) do { uint32_t t_ = (uint32_t)(v); for (int i_ = 0; i_ < 4; i_++) *p++ = (uint8_t)(t_ >> (8 * i_)); } while (0)
+#define W16(v) do { uint16_t t_ = (uint16_t)(v); *p++ = (uint8_t)t_; *p++ = (uint8_t)(t_ >> 8); } while (0)
+    offsets[0] = 0;
+    W32(0x48435433u);
+    W32(width);
+    W32(height);
+    W32(keep);
+    W32(ess);
+    W32(dpf);
+    memcpy(p, bm, (n + 7) / 8);
+    p += (n + 7) / 8;
+    for (size_t i = 0; i < ess; i++) W16(hho_f32_to_f16_rne(dct[idx[i]]));
+    for (size_t f = 1; f < nfrag; f++) {
+        offsets[f] = (uint64_t)(p - out);
+        W16(f);
+        W16(nfrag);
+        size_t s = ess + (f - 1) * dpf, e = s + dpf < keep ? s + dpf : keep;
+        W32(e > s ? e - s : 0);
+        for (size_t i = s; i < e; i++) W16(hho_f32_to_f16_rne(dct[idx[i]]));
+    }
+#undef W32
+#undef W16
+    offsets[nfrag] = (uint64_t)(p - out);
+    free(bm);
+    free(idx);
+    return (size_t)(p - out);
+}
+
+/* CompressiveSpectralDecoder::add_essentials (V2/V3, compressive.rs:438-651),
+ * add_detail (:653-700) and reconstruct (:728-752).  Fragments after the
+ * first with index 0 are ignored; a detail fragment whose own index field
+ * is 0 is rejected (the reference's start position underflows). */
+int hho_spectral_reconstruct(const uint8_t *const *frags, const size_t *lens, const uint16_t *fidx, uint32_t nf,
+                             float *out, size_t out_cap, uint32_t *width, uint32_t *height, hho_err *err) {
+    memset(err, 0, sizeof(*err));
+    err->kind = HHO_CORRUPTED_DATA;
+    if (nf == 0 || fidx[0] != 0) { err->sub = HHO_CORRUPT_HEADER; return err->kind; }
+    const uint8_t *d = frags[0];
+    size_t l = lens[0];
+    if (l < 24) { err->sub = HHO_CORRUPT_SIZE; return err->kind; }
+    uint32_t magic = rd32le(d);
+    if (magic != 0x48435433u && magic != 0x48435432u) { err->kind = HHO_UNSUPPORTED; return err->kind; }
+    int v3 = magic == 0x48435433u;
+    size_t csz = v3 ? 2 : 4;
+    uint32_t w = rd32le(d + 4), h = rd32le(d + 8), ntot = rd32le(d + 12), ness = rd32le(d + 16), dpf = rd32le(d + 20);
+    *width = w;
+    *height = h;
+    size_t n = (size_t)w * h, bm = (n + 7) / 8;
+    if (24 + bm > l) { err->sub = HHO_CORRUPT_SIZE; return err->kind; }
+    uint32_t *map = (uint32_t *)malloc(sizeof(uint32_t) * (n ? n : 1));
+    size_t cnt = hho_bitmap_index_map(d + 24, n, map);
+    if (cnt != ntot) { free(map); err->sub = HHO_CORRUPT_BITMAP_COUNT; return err->kind; }
+    float *coef = (float *)calloc(ntot ? ntot : 1, sizeof(float));
+    size_t off = 24 + bm;
+    for (uint32_t i = 0; i < ness; i++) {
+        if (off + csz > l || i >= ntot) { free(map); free(coef); err->sub = HHO_CORRUPT_SIZE; return err->kind; }
+        if (v3) coef[i] = hho_f16_bits_to_f32(rd16le(d + off));
+        else memcpy(&coef[i], d + off, 4);
+        off += csz;
+    }
+    for (uint32_t f = 1; f < nf; f++) {
+        if (fidx[f] == 0) continue;
+        const uint8_t *q = frags[f];
+        size_t ql = lens[f];
+        if (ql < 8) { free(map); free(coef); err->sub = HHO_CORRUPT_SIZE; return err->kind; }
+        uint32_t fi = rd16le(q), count = rd32le(q + 4);
+        if (fi == 0) { free(map); free(coef); err->sub = HHO_CORRUPT_HEADER; return err->kind; }
+        size_t start = (size_t)ness + (size_t)(fi - 1) * dpf, o = 8;
+        for (uint32_t i = 0; i < count; i++) {
+            if (o + csz > ql) break;
+            size_t ci = start + i;
+            if (ci < ntot) {
+                if (v3) coef[ci] = hho_f16_bits_to_f32(rd16le(q + o));
+                else memcpy(&coef[ci], q + o, 4);
+            }
+            o += csz;
+        }
+    }
+    if (out_cap < n) {
+        free(map); free(coef);
+        err->kind = HHO_BUFFER_TOO_SMALL;
+        err->required = n;
+        err->provided = out_cap;
+        return err->kind;
+    }
+    float *dense = (float *)calloc(n ? n : 1, sizeof(float));
+    for (size_t i = 0; i < ntot; i++) dense[map[i]] = coef[i];
+    if (n) hho_idct_2d(dense, out, w, h);
+    free(dense);
+    free(map);
+    free(coef);
+    err->kind = HHO_OK;
+    return HHO_OK;
+}

@@ -29,7 +29,9 @@ enum {
     HHO_CORRUPTED_DATA = 1,
     HHO_BUFFER_TOO_SMALL = 2,
     HHO_UNEXPECTED_EOF = 3,
+    HHO_UNSUPPORTED = 5, /* Error::Unsupported */
     HHO_ALGORITHM = 6,   /* Error::Algorithm ("hct" read failures, tensor.rs:421-431,470-480) */
+    HHO_INVALID_DATA = 7, /* CudaError::InvalidData (crates/haagenti-cuda/src/error.rs) */
 };
 
 /* Sub-kinds of CorruptedData raised by decompress_block / the HCT parsers. */
@@ -186,6 +188,24 @@ int hho_hct_read_all_v2_lz4(const uint8_t *file, size_t file_len, uint8_t *out,
 /* HctReaderV2::new + validate_checksums (:1014-1020). */
 int hho_hct_validate_v2(const uint8_t *file, size_t file_len, hho_err *err,
                         int64_t *failed_block);
+
+/* ---------------- HCT3 whole-tensor spectral ------------------------------
+ * Fragment container of GpuDecompressor (crates/haagenti-cuda/src/
+ * decompress.rs:322-427) and CompressiveSpectral{Encoder,Decoder}
+ * (crates/haagenti/src/compressive.rs:67-752).  Parity: the coefficient
+ * scatter is pinned bit-exactly against the reference's own C decoder
+ * (ref/c/hct_decoder.h: hct_decode == hct_idct_2d of these coefficients,
+ * built into oracle/_ref) on well-formed containers; the encoder and
+ * decoder against each other (round trips, the reference's own MSE bounds,
+ * compressive.rs:777-980) and the f16 rounding against numpy (IEEE RNE). */
+uint16_t hho_f32_to_f16_rne(float v);
+int hho_hct3_coefficients(const uint8_t *data, size_t len, size_t total, float *dense);
+int hho_hct3_decode(const uint8_t *data, size_t len, const uint64_t *shape, size_t rank, float *out);
+size_t hho_spectral_encode_from_dct(const float *dct, uint32_t width, uint32_t height, uint16_t nfrag,
+                                    float retention, float essential_ratio, uint8_t *out, size_t cap,
+                                    uint64_t *offsets);
+int hho_spectral_reconstruct(const uint8_t *const *frags, const size_t *lens, const uint16_t *fidx, uint32_t nf,
+                             float *out, size_t out_cap, uint32_t *width, uint32_t *height, hho_err *err);
 
 #ifdef __cplusplus
 }

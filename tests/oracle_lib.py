@@ -104,6 +104,18 @@ def lib():
                                               C.POINTER(C.c_int64)]
         L.hho_hct_validate_v2.restype = C.c_int
         L.hho_hct_validate_v2.argtypes = [u8p, sz, C.POINTER(Err), C.POINTER(C.c_int64)]
+        L.hho_f32_to_f16_rne.restype = C.c_uint16
+        L.hho_f32_to_f16_rne.argtypes = [C.c_float]
+        L.hho_hct3_coefficients.restype = C.c_int
+        L.hho_hct3_coefficients.argtypes = [u8p, sz, sz, f32p]
+        L.hho_hct3_decode.restype = C.c_int
+        L.hho_hct3_decode.argtypes = [u8p, sz, u8p, sz, f32p]
+        L.hho_spectral_encode_from_dct.restype = sz
+        L.hho_spectral_encode_from_dct.argtypes = [f32p, C.c_uint32, C.c_uint32, C.c_uint16, C.c_float,
+                                                   C.c_float, u8p, sz, u8p]
+        L.hho_spectral_reconstruct.restype = C.c_int
+        L.hho_spectral_reconstruct.argtypes = [u8p, u8p, u8p, C.c_uint32, f32p, sz, C.POINTER(C.c_uint32),
+                                               C.POINTER(C.c_uint32), C.POINTER(Err)]
         _lib = L
     return _lib
 
@@ -438,3 +450,56 @@ def ref_hct_decode(data, rows, cols):
     out = np.ctypeslib.as_array(ptr, shape=(rows * cols,)).copy().reshape(rows, cols)
     ref()._free(C.cast(ptr, C.c_void_p))
     return out
+
+
+# ------------------------------------------------------------- HCT3 spectral
+INVALID_DATA, UNSUPPORTED = 7, 5
+
+
+def f32_to_f16_rne(v):
+    return int(lib().hho_f32_to_f16_rne(float(v)))
+
+
+def hct3_coefficients(data, total):
+    d = _u8(data)
+    out = np.zeros(max(int(total), 1), np.float32)
+    rc = lib().hho_hct3_coefficients(_p(d), d.size, int(total), _p(out))
+    return rc, out[:int(total)]
+
+
+def hct3_decode(data, shape):
+    d = _u8(data)
+    shp = np.ascontiguousarray(shape, dtype=np.uint64)
+    total = int(np.prod(shape)) if len(shape) else 1
+    out = np.zeros(max(total, 1), np.float32)
+    rc = lib().hho_hct3_decode(_p(d), d.size, _p(shp), len(shape), _p(out))
+    return rc, out[:total]
+
+
+def spectral_encode_from_dct(dct, width, height, nfrag, retention, essential_ratio=0.2):
+    c = np.ascontiguousarray(dct, dtype=np.float32).ravel()
+    n = width * height
+    cap = 24 + (n + 7) // 8 + 2 * n + 8 * nfrag + 16
+    out = np.zeros(cap, np.uint8)
+    offs = np.zeros(nfrag + 1, np.uint64)
+    w = lib().hho_spectral_encode_from_dct(_p(c), width, height, nfrag, retention, essential_ratio,
+                                           _p(out), cap, _p(offs))
+    assert w > 0
+    raw = out[:w].tobytes()
+    return [(f, raw[int(offs[f]):int(offs[f + 1])]) for f in range(nfrag)]
+
+
+def spectral_reconstruct(fragments, out_cap=None):
+    """fragments: list of (index, bytes).  Returns (out, Err, width, height)."""
+    bufs = [np.frombuffer(bytes(d), np.uint8).copy() if len(d) else np.zeros(1, np.uint8) for _, d in fragments]
+    ptrs = np.array([b.ctypes.data for b in bufs], np.uint64)
+    lens = np.array([len(d) for _, d in fragments], np.uint64)
+    idx = np.array([i for i, _ in fragments], np.uint16)
+    w, h, e = C.c_uint32(0), C.c_uint32(0), Err()
+    if out_cap is None:
+        d0 = bytes(fragments[0][1])
+        out_cap = int.from_bytes(d0[4:8], "little") * int.from_bytes(d0[8:12], "little") if len(d0) >= 12 else 0
+    out = np.zeros(max(out_cap, 1), np.float32)
+    lib().hho_spectral_reconstruct(_p(ptrs), _p(lens), _p(idx), len(fragments), _p(out), out_cap,
+                                   C.byref(w), C.byref(h), C.byref(e))
+    return out[:w.value * h.value], e, w.value, h.value
