@@ -30,6 +30,11 @@ Other workloads (one JSON line each, same contract):
                    blocks of lz4-256mib (one wavefront per block), the
                    checksum HctReaderV2 verifies per block; value = hashed
                    bytes per second (the kernel reads its input once)
+  hct3-4096        one 4096x4096 N(0, 0.02) tensor as an HCT V3 fragment
+                   container (whole-tensor DCT, turbo defaults: top 20 %,
+                   f16 coefficients); GPU bitmap scatter + whole-matrix
+                   inverse DCT as two fp32 GEMMs, bf16 out; roofline against
+                   the fp32 MFMA peak
   hbm-copy         a plain 1 GiB device copy: the HBM reference rate and the
                    calibration for the FETCH_SIZE / WRITE_SIZE counters
 
@@ -510,6 +515,79 @@ def wl_idct(args, torch, H, O):
                 cpu, {"spot_check_max_err_over_rms": check})
 
 
+def wl_hct3(args, torch, H, O):
+    """Whole-tensor HCT3 spectral decode (GpuDecompressor::decompress_to_gpu)
+    of one 4096x4096 N(0, 0.02) tensor encoded with the turbo defaults
+    (retention 0.20, 4 fragments, essential ratio 0.20,
+    crates/haagenti/src/pipeline/turbo.rs:88-96), the container resident in
+    HBM, bf16 output."""
+    import struct
+    n = 4096
+    ctx = H.HipContext(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    w = torch.randn(n, n, device="cuda", generator=g) * 0.02
+    c = torch.empty_like(w)
+    t0 = time.time()
+    ctx.dct_2d(w, n, n, c, stream=sp)
+    torch.cuda.synchronize()
+    frags = H.CompressiveSpectralEncoder(4, 0.20).with_essential_ratio(0.20).encode_2d_from_dct(
+        c.cpu().numpy(), n, n)
+    del w, c
+    # one container fragment: fragment 0's bitmap and every retained value
+    f0 = frags[0][1]
+    keep = struct.unpack_from("<I", f0, 12)[0]
+    bm = n * n // 8
+    payload = struct.pack("<I", keep) + f0[24:24 + bm] + f0[24 + bm:] + b"".join(d[8:] for _, d in frags[1:])
+    data = struct.pack("<H", 1) + struct.pack("<HHQI", 0, 0, H.xxh3_64(payload), len(payload)) + payload
+    log(f"encoded {n}x{n} in {time.time() - t0:.1f}s: {keep} coefficients, container {len(data) / 1e6:.1f} MB")
+    d_data = torch.from_numpy(np.frombuffer(data, np.uint8).copy()).cuda()
+    out = torch.empty(n * n, dtype=torch.bfloat16, device="cuda")
+    dec = H.GpuDecompressor(ctx)
+
+    def step():
+        dec.decompress_device(data, d_data, [n, n], out, dtype=H.BF16, stream=sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    check, cpu = None, None
+    if O is not None:
+        t0 = time.perf_counter()
+        rc, ref = O.hct3_decode(data, [n, n])
+        secs = time.perf_counter() - t0
+        assert rc == 0
+        got = out.float().cpu().numpy()
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        check = float(np.abs(got - ref).max() / rms)
+        log(f"full tensor: max|bf16 - oracle f32| = {check:.2e} x RMS")
+        if not args.no_cpu:
+            cpu = {"value": round(n * n * 2 / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                   "sample": f"one full {n}x{n} decode by the oracle (container scatter + the reference's "
+                             f"FFT-based idct_2d in f32), bf16-equivalent output bytes, 1 thread, {secs:.1f} s"}
+    T = Timed(torch, stream)
+    e = T.start()
+    for _ in range(args.steps):
+        step()
+    T.stop(e)
+    torch.cuda.synchronize()
+    ms_step = T.mean_s() * 1e3 / args.steps
+    per = ms_step / 1e3
+    flop = 4.0 * n ** 3          # two n x n x n GEMMs
+    achieved = flop / per / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": 157.3, "unit": "TFLOP/s",
+            "frac": round(achieved / 157.3, 4), "traffic": traffic_for("hct3-4096"),
+            "kernel": "rocBLAS sgemm x2 (+ bitmap scatter, bf16 conversion)", "avg_launch_us": round(per * 1e6, 1),
+            "algorithmic_flop_per_launch": flop, "mfma_type": "fp32"}
+    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, "f32",
+                "synthetic (4096x4096 N(0,0.02), torch seed 17, turbo defaults)",
+                {"rows": n, "cols": n, "retention": 0.20, "coefficients": int(keep),
+                 "container_bytes": len(data), "out_dtype": "bf16"}, roof, cpu,
+                {"spot_check_max_err_over_rms": check})
+
+
 def wl_stream(args, torch, H, O):
     rng = np.random.default_rng(70)
     rhos = rng.uniform(0.10, 0.50, len(L70B))
@@ -678,7 +756,7 @@ def wl_xxh3(args, torch, H, O):
 
 
 WORKLOADS = {"llama3-8b-layer": wl_llama3_8b_layer, "xxh3-256mib": wl_xxh3, "int4-4096": wl_int4, "lz4-256mib": wl_lz4,
-             "idct-8192": wl_idct, "llama70b-stream": wl_stream, "hbm-copy": wl_copy}
+             "idct-8192": wl_idct, "llama70b-stream": wl_stream, "hbm-copy": wl_copy, "hct3-4096": wl_hct3}
 
 
 def main():

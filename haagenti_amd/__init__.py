@@ -668,7 +668,7 @@ class GpuDecompressor:
     def decompress_device(self, h_data, d_data, shape, d_out, dtype=F32, stream=None):
         """Decode with the container already on the device (d_data, a copy of
         h_data): asynchronous on the stream (hh_hct3_decompress_device)."""
-        b = bytes(h_data)
+        b = h_data if isinstance(h_data, bytes) else bytes(h_data)
         arr, rank = _shape_arr(shape)
         _check(_lib.hh_hct3_decompress_device(self.ctx.handle, b, _addr(d_data), len(b), arr, rank, int(dtype),
                                               _addr(d_out), stream), "hh_hct3_decompress_device")
