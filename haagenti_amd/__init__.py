@@ -140,6 +140,8 @@ _sig("hh_spectral_reconstruct", _i32, [_vp, _vp, _vp, _vp, _u32, _i32, _vp, C.c_
                                        C.POINTER(_u32), C.POINTER(_u32), C.POINTER(BlockStatus), _vp])
 _sig("hh_idct_2d", _i32, [_vp, _vp, _u32, _u32, _i32, _vp, _vp])
 _sig("hh_dct_2d", _i32, [_vp, _vp, _u32, _u32, _vp, _vp])
+_sig("hh_zstd_decompress", _i32, [_vp, _sz, _vp, _sz, C.POINTER(_sz)])
+_sig("hh_xxh64", C.c_uint64, [_vp, _sz, C.c_uint64])
 _sig("hh_spectral_encoded_size", _sz, [_u32, _u32, C.c_uint16, C.c_float, C.c_float,
                                         C.POINTER(_u32), C.POINTER(_u32)])
 _sig("hh_spectral_encode_from_dct", _i32, [_vp, _u32, _u32, C.c_uint16, C.c_float, C.c_float, _vp,
@@ -157,6 +159,7 @@ EXPORTS = [
     "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
     "hh_hct_validate_checksums", "hh_hct3_coefficients", "hh_hct3_decompress", "hh_hct3_decompress_device",
     "hh_spectral_reconstruct", "hh_idct_2d", "hh_dct_2d", "hh_spectral_encoded_size",
+    "hh_zstd_decompress", "hh_xxh64",
     "hh_spectral_encode_from_dct",
 ]
 
@@ -172,6 +175,26 @@ def xxh3_64(data):
 
 def lib():
     return _lib
+
+
+def zstd_decompress(data):
+    """zstd::decode_all (RFC 8878 frames) on the host (hh_zstd_decompress).
+    Raises HaagentiError(CORRUPTED_DATA) on a malformed stream."""
+    b = bytes(data)
+    n = _sz(0)
+    rc = _lib.hh_zstd_decompress(b, len(b), None, 0, C.byref(n))
+    if rc == OK:
+        return b""
+    if rc != BUFFER_TOO_SMALL:
+        raise HaagentiError(rc, "zstd decode")
+    out = C.create_string_buffer(n.value)
+    _check(_lib.hh_zstd_decompress(b, len(b), out, n.value, C.byref(n)), "zstd decode")
+    return out.raw[:n.value]
+
+
+def xxh64(data, seed=0):
+    b = bytes(data)
+    return int(_lib.hh_xxh64(b, len(b), int(seed)))
 
 
 class HaagentiError(Exception):

@@ -137,6 +137,16 @@ bool zstd_framed(const uint8_t *d, size_t len) {
     return len >= 4 && d[0] == 0x28 && d[1] == 0xB5 && d[2] == 0x2F && d[3] == 0xFD;
 }
 
+// GpuDecompressor::try_zstd_decompress (decompress.rs:296-319): zstd-framed
+// input is decoded on the host; if that fails the bytes are parsed as a raw
+// container.  Returns whether `hold` now holds the decoded container.
+bool unwrap_zstd(const uint8_t *&data, size_t &len, std::vector<uint8_t> &hold) {
+    if (!zstd_framed(data, len) || !hh::zstd_decode_all(data, len, hold)) return false;
+    data = hold.data();
+    len = hold.size();
+    return true;
+}
+
 // IDCT of d_dense into d_out (dtype), with d_tmp as the GEMM intermediate;
 // d_dense is overwritten for 16-bit outputs.
 int32_t inverse_to(hh_context *ctx, float *d_dense, float *d_tmp, uint32_t rows, uint32_t cols,
@@ -179,7 +189,8 @@ extern "C" {
 int32_t hh_hct3_coefficients(hh_context *ctx, const uint8_t *data, size_t len, uint64_t total,
                              float *d_coeffs, void *stream) {
     if (!ctx || !data || (total && !d_coeffs) || total > 0xffffffffull) return HH_ERR_INVALID_ARGUMENT;
-    if (zstd_framed(data, len)) return HH_ERR_UNSUPPORTED;
+    std::vector<uint8_t> hold;
+    unwrap_zstd(data, len, hold);
     std::vector<Layer> layers;
     int32_t rc = parse_container(data, len, total, layers);
     if (rc != HH_OK || total == 0) return rc;
@@ -201,7 +212,8 @@ int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, con
     uint32_t rows, cols;
     int32_t rc = dims_of(shape, rank, &total, &rows, &cols);
     if (rc != HH_OK) return rc;
-    if (zstd_framed(data, len)) return HH_ERR_UNSUPPORTED;
+    std::vector<uint8_t> hold;
+    unwrap_zstd(data, len, hold);
     std::vector<Layer> layers;
     rc = parse_container(data, len, total, layers);
     if (rc != HH_OK || total == 0) return rc;
@@ -230,7 +242,10 @@ int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const 
     uint32_t rows, cols;
     int32_t rc = dims_of(shape, rank, &total, &rows, &cols);
     if (rc != HH_OK) return rc;
-    if (zstd_framed(h_data, len)) return HH_ERR_UNSUPPORTED;
+    // a zstd-wrapped container is decoded on the host and taken the
+    // host-staged way (the device copy holds the compressed frame)
+    if (zstd_framed(h_data, len))
+        return hh_hct3_decompress(ctx, h_data, len, shape, rank, out_dtype, d_out, stream);
     std::vector<Layer> layers;
     rc = parse_container(h_data, len, total, layers);
     if (rc != HH_OK || total == 0) return rc;

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "../../include/haagenti_hip.h"
 
 struct hh_context {
@@ -117,6 +119,8 @@ hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_o
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
                    uint32_t rows, uint32_t cols, hipStream_t s);
 void release_dct_resources(hh_context *ctx);
+// zstd::decode_all on the host (host_zstd.cpp): false on a malformed stream.
+bool zstd_decode_all(const uint8_t *in, size_t len, std::vector<uint8_t> &out);
 
 // Decodes n tensors (validated by the caller) in ceil(n/8) launches.
 hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dtype,

@@ -300,7 +300,10 @@ int32_t hh_hct_validate_checksums(hh_context *ctx, const uint8_t *h_file, const 
  * (CudaError::InvalidData); fragments shorter than 4 + bitmap bytes are
  * skipped; each fragment's values fill its set bits in ascending order
  * while they last, later fragments overwriting earlier ones.  zstd-framed
- * input (magic 28 B5 2F FD) is HH_ERR_UNSUPPORTED.  Synchronous. */
+ * input (magic 28 B5 2F FD, the turbo wrapper) is first decoded on the host
+ * (hh_zstd_decompress); when that fails the bytes are parsed as a raw
+ * container, as try_zstd_decompress does (decompress.rs:296-319).
+ * Synchronous. */
 int32_t hh_hct3_coefficients(hh_context *ctx, const uint8_t *data, size_t len, uint64_t total,
                              float *d_coeffs, void *stream);
 
@@ -314,7 +317,8 @@ int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, con
 
 /* hh_hct3_decompress with the container also resident in device memory
  * (d_data, a copy of h_data; h_data is parsed on the host): no host-device
- * copies, asynchronous on the stream. */
+ * copies, asynchronous on the stream.  A zstd-framed h_data is decoded on
+ * the host and taken as hh_hct3_decompress does (synchronous). */
 int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const uint8_t *d_data, size_t len,
                                   const uint64_t *shape, uint32_t rank, int32_t out_dtype, void *d_out,
                                   void *stream);
@@ -346,6 +350,16 @@ int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t c
  * a row-major f32 matrix (dct_2d, dct.rs:282-308).  Asynchronous. */
 int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, float *d_out,
                   void *stream);
+
+/* zstd::decode_all (zstd crate 0.13.3 / libzstd; RFC 8878 frames) on the
+ * host: every frame of in[0..in_len) decoded and concatenated into out.
+ * *written receives the decoded size (also when it exceeds out_cap:
+ * HH_ERR_BUFFER_TOO_SMALL); a malformed stream, a dictionary frame or a
+ * window above 2^27 bytes is HH_ERR_CORRUPTED_DATA.  Content checksums are
+ * verified. */
+int32_t hh_zstd_decompress(const uint8_t *in, size_t in_len, uint8_t *out, size_t out_cap, size_t *written);
+/* XXH64 (the zstd content checksum, RFC 8878 section 3.1.1). */
+uint64_t hh_xxh64(const uint8_t *data, size_t len, uint64_t seed);
 
 /* Bytes of CompressiveSpectralEncoder's fragments for a width x height
  * tensor (compressive.rs:94-238); *retain_count / *essential_count receive

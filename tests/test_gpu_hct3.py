@@ -67,9 +67,36 @@ def test_coefficients_container_edges():
             dec().reconstruct_coefficients_gpu(bad, total)
         assert e.value.code == Hm.INVALID_ARGUMENT
         assert O.hct3_coefficients(bad, total)[0] == O.INVALID_DATA
-    with pytest.raises(Hm.HaagentiError) as e:
-        dec().decompress_to_gpu(b"\x28\xb5\x2f\xfd" + ok, [total])
-    assert e.value.code == Hm.UNSUPPORTED
+    # zstd magic that is not a zstd stream: parsed as a raw container, as
+    # try_zstd_decompress falls back (decompress.rs:306-316)
+    fake = b"\x28\xb5\x2f\xfd" + ok
+    rc, _ = O.hct3_coefficients(fake, total)
+    if rc == O.OK:
+        got = dec().reconstruct_coefficients_gpu(fake, total).cpu().numpy()
+        assert np.array_equal(got, O.hct3_coefficients(fake, total)[1])
+    else:
+        with pytest.raises(Hm.HaagentiError) as e:
+            dec().decompress_to_gpu(fake, [total])
+        assert e.value.code == Hm.INVALID_ARGUMENT
+
+
+def test_zstd_wrapped_container():
+    # the turbo wrapper: zstd level 1 over the container (turbo.rs:389-391)
+    pa = pytest.importorskip("pyarrow")
+    T = G.torch()
+    rng = np.random.default_rng(13)
+    shape = (96, 160)
+    total = 96 * 160
+    data = container([random_fragment(rng, total, 0.2), random_fragment(rng, total, 0.1)])
+    wrapped = pa.Codec("zstd", compression_level=1).compress(data, asbytes=True)
+    assert wrapped[:4] == b"\x28\xb5\x2f\xfd"
+    raw = dec().decompress_to_gpu(data, shape).cpu().numpy()
+    got = dec().decompress_to_gpu(wrapped, shape).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), raw.view(np.uint32))
+    out = T.empty(total, dtype=T.float32, device="cuda")
+    dec().decompress_device(wrapped, G.dev(np.frombuffer(wrapped, np.uint8)), shape, out)
+    G.sync()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), raw.view(np.uint32))
 
 
 @pytest.mark.parametrize("shape", [(64, 64), (37, 53), (1, 1000), (1000,), (3, 5, 17), (256, 512), (96, 4)])
