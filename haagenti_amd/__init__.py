@@ -140,6 +140,8 @@ _sig("hh_spectral_reconstruct", _i32, [_vp, _vp, _vp, _vp, _u32, _i32, _vp, C.c_
                                        C.POINTER(_u32), C.POINTER(_u32), C.POINTER(BlockStatus), _vp])
 _sig("hh_idct_2d", _i32, [_vp, _vp, _u32, _u32, _i32, _vp, _vp])
 _sig("hh_dct_2d", _i32, [_vp, _vp, _u32, _u32, _vp, _vp])
+_sig("hh_turbo_tensor_decode", _i32, [_vp, _vp, _sz, _i32, _i32, _vp, C.c_uint64, C.POINTER(_u32),
+                                      C.POINTER(_u32), C.POINTER(BlockStatus), _vp])
 _sig("hh_zstd_decompress", _i32, [_vp, _sz, _vp, _sz, C.POINTER(_sz)])
 _sig("hh_xxh64", C.c_uint64, [_vp, _sz, C.c_uint64])
 _sig("hh_spectral_encoded_size", _sz, [_u32, _u32, C.c_uint16, C.c_float, C.c_float,
@@ -159,7 +161,7 @@ EXPORTS = [
     "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
     "hh_hct_validate_checksums", "hh_hct3_coefficients", "hh_hct3_decompress", "hh_hct3_decompress_device",
     "hh_spectral_reconstruct", "hh_idct_2d", "hh_dct_2d", "hh_spectral_encoded_size",
-    "hh_zstd_decompress", "hh_xxh64",
+    "hh_zstd_decompress", "hh_xxh64", "hh_turbo_tensor_decode",
     "hh_spectral_encode_from_dct",
 ]
 
@@ -708,12 +710,24 @@ class GpuDecompressor:
 class CompressiveSpectralDecoder:
     """CompressiveSpectralDecoder (compressive.rs:420-752): add_essentials()
     (fragment 0) then add_detail() for any subset of the detail fragments;
-    reconstruct() runs the scatter and the whole-matrix IDCT on the GPU.
-    Fragments are (index, bytes) pairs or objects with .index and .data."""
+    quality() as the reference computes it (:716-729); reconstruct() runs the
+    scatter and the whole-matrix IDCT on the GPU.  Fragments are
+    (index, bytes) pairs or objects with .index and .data."""
 
     def __init__(self, ctx=None):
-        self.ctx = ctx if ctx is not None else HipContext(0)
+        self._ctx = ctx
         self._frags = []
+        self.has_essentials = False
+        self.total_coeffs = self.essential_count = 0
+        self.total_fragments = 0
+        self.detail_fragments_loaded = 0
+        self.width = self.height = 0
+
+    @property
+    def ctx(self):
+        if self._ctx is None:
+            self._ctx = HipContext(0)
+        return self._ctx
 
     @staticmethod
     def _split(fragment):
@@ -722,23 +736,43 @@ class CompressiveSpectralDecoder:
         return int(fragment.index), bytes(fragment.data)
 
     def add_essentials(self, fragment):
+        import struct
         idx, data = self._split(fragment)
         if idx != 0:
             raise HaagentiError(CORRUPTED_DATA, "fragment 0 must be added first for CompressiveSpectralDecoder")
         self._frags = [(0, data)]
         self._probe()
+        self.total_coeffs, self.essential_count = struct.unpack_from("<II", data, 12)
+        self.has_essentials = True
 
     def add_detail(self, fragment):
-        if not self._frags:
+        import struct
+        if not self.has_essentials:
             raise HaagentiError(CORRUPTED_DATA, "must add fragment 0 (essentials) first")
         idx, data = self._split(fragment)
         if idx == 0:
             return
         self._frags.append((idx, data))
         self._probe()
+        self.total_fragments = struct.unpack_from("<H", data, 2)[0]
+        self.detail_fragments_loaded += 1
 
     def can_reconstruct(self):
-        return bool(self._frags)
+        return self.has_essentials
+
+    def quality(self):
+        """compressive.rs:716-729 (f32 arithmetic)."""
+        import numpy as np
+        if not self.has_essentials:
+            return 0.0
+        if self.total_fragments <= 1:
+            return 1.0
+        f = np.float32
+        detail = self.total_fragments - 1
+        loaded = min(self.detail_fragments_loaded, detail)
+        eq = f(self.essential_count) / f(self.total_coeffs)
+        dq = f(self.total_coeffs - self.essential_count) / f(self.total_coeffs)
+        return float(eq + dq * (f(loaded) / f(detail)))
 
     def _call(self, dtype=F32, d_out=None, out_cap=0, stream=None):
         n = len(self._frags)
@@ -760,7 +794,7 @@ class CompressiveSpectralDecoder:
 
     def reconstruct_gpu(self, dtype=F32, d_out=None, stream=None):
         import torch
-        if not self._frags:
+        if not self.has_essentials:
             raise HaagentiError(CORRUPTED_DATA, "need essentials fragment to reconstruct")
         n = self.width * self.height
         if d_out is None:

@@ -355,6 +355,68 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
     return from_hip(hipStreamSynchronize(s));
 }
 
+int32_t hh_turbo_tensor_decode(hh_context *ctx, const uint8_t *data, size_t len, int32_t verify,
+                               int32_t out_dtype, void *d_out, uint64_t out_cap, uint32_t *width,
+                               uint32_t *height, hh_block_status *status, void *stream) {
+    if (status) std::memset(status, 0, sizeof(*status));
+    if (!ctx || !data) return HH_ERR_INVALID_ARGUMENT;
+    // zstd wrapper (turbo.rs:389-391); the container inside (:378-387)
+    std::vector<uint8_t> hold;
+    if (zstd_framed(data, len)) {
+        if (!hh::zstd_decode_all(data, len, hold)) {
+            if (status) status->code = HH_ERR_CORRUPTED_DATA;
+            return HH_ERR_CORRUPTED_DATA;
+        }
+        data = hold.data();
+        len = hold.size();
+    }
+    auto bad = [&](int32_t detail) {
+        if (status) {
+            status->code = HH_ERR_CORRUPTED_DATA;
+            status->detail = detail;
+        }
+        return (int32_t)HH_ERR_CORRUPTED_DATA;
+    };
+    if (len < 2) return bad(HH_CORRUPT_SIZE);
+    const uint32_t nf = rd16(data);
+    std::vector<const uint8_t *> ptrs;
+    std::vector<size_t> lens;
+    std::vector<uint16_t> idx;
+    size_t off = 2;
+    for (uint32_t f = 0; f < nf; f++) {
+        if (len - off < 16) return bad(HH_CORRUPT_SIZE);
+        const uint16_t fi = rd16(data + off);
+        uint64_t sum = 0;
+        for (int i = 0; i < 8; i++) sum |= (uint64_t)data[off + 4 + i] << (8 * i);
+        const uint32_t dl = rd32(data + off + 12);
+        off += 16;
+        if ((size_t)dl > len - off) return bad(HH_CORRUPT_SIZE);
+        // HoloFragment::new stores xxh3_64 of the fragment data (holotensor.rs:285)
+        if (verify && hh::xxh3_64_host(data + off, dl) != sum) {
+            if (status) {
+                status->code = HH_ERR_CHECKSUM_MISMATCH;
+                status->position = f;
+            }
+            return HH_ERR_CHECKSUM_MISMATCH;
+        }
+        ptrs.push_back(data + off);
+        lens.push_back(dl);
+        idx.push_back(fi);
+        off += dl;
+    }
+    if (nf == 0) return bad(HH_CORRUPT_HEADER);
+    // fragment 0 (the essentials) goes in first, the details keep their order
+    for (uint32_t f = 1; f < nf; f++)
+        if (idx[f] == 0 && idx[0] != 0) {
+            std::rotate(ptrs.begin(), ptrs.begin() + f, ptrs.begin() + f + 1);
+            std::rotate(lens.begin(), lens.begin() + f, lens.begin() + f + 1);
+            std::rotate(idx.begin(), idx.begin() + f, idx.begin() + f + 1);
+            break;
+        }
+    return hh_spectral_reconstruct(ctx, ptrs.data(), lens.data(), idx.data(), nf, out_dtype, d_out, out_cap,
+                                   width, height, status, stream);
+}
+
 int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, int32_t out_dtype,
                    void *d_out, void *stream) {
     if (!ctx || !valid_dtype(out_dtype) || rows > 0x7fffffffu || cols > 0x7fffffffu) return HH_ERR_INVALID_ARGUMENT;

@@ -338,6 +338,20 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
                                 void *d_out, uint64_t out_cap, uint32_t *width, uint32_t *height,
                                 hh_block_status *status, void *stream);
 
+/* One tensor of the turbo pipeline's output file (crates/haagenti/src/
+ * pipeline/turbo.rs:315-419): a zstd frame around a fragment container
+ * ([u16 n] then {u16 index, u16 flags, u64 XXH3-64 of the data, u32 len,
+ * data} per fragment, :378-387) of CompressiveSpectralEncoder fragments,
+ * decoded with every fragment as hh_spectral_reconstruct does.  With verify,
+ * each fragment's XXH3-64 (HoloFragment::new, holotensor.rs:283-292) is
+ * checked first (HH_ERR_CHECKSUM_MISMATCH, status->position = fragment).
+ * The reference writes these files but has no decoder for them outside its
+ * examples (GpuDecompressor reads the other fragment layout); this is the
+ * loader entry for them.  Synchronous. */
+int32_t hh_turbo_tensor_decode(hh_context *ctx, const uint8_t *data, size_t len, int32_t verify,
+                               int32_t out_dtype, void *d_out, uint64_t out_cap, uint32_t *width,
+                               uint32_t *height, hh_block_status *status, void *stream);
+
 /* GpuDctContext::idct_2d_gpu / idct_2d for a whole rows x cols matrix
  * (crates/haagenti-cuda/src/dct_gpu.rs:1163-1227, 1404-1412): orthonormal
  * 2-D DCT-III of the row-major f32 d_in into d_out (out_dtype), as two fp32
