@@ -121,22 +121,48 @@ class Timed:
     """HIP events on one stream around a region (torch.cuda.Event records on
     the stream it is given, which is the stream the kernels are launched on)."""
 
-    def __init__(self, torch, stream):
+    def __init__(self, torch, stream, reserve=0):
         self.torch, self.stream = torch, stream
         self.pairs = []
+        # HIP creates an event's signal at its first record, and growing the
+        # runtime's signal pool can stall the host for milliseconds while the
+        # GPU runs dry: events used inside a timed loop are created and
+        # recorded once beforehand
+        self.free = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reserve)]
+        for e in self.free:
+            e.record(stream)
+        if reserve:
+            torch.cuda.synchronize()
+
+    def _event(self):
+        return self.free.pop() if self.free else self.torch.cuda.Event(enable_timing=True)
 
     def start(self):
-        e = self.torch.cuda.Event(enable_timing=True)
+        e = self._event()
         e.record(self.stream)
         return e
 
     def stop(self, e0):
-        e1 = self.torch.cuda.Event(enable_timing=True)
+        e1 = self._event()
         e1.record(self.stream)
         self.pairs.append((e0, e1))
 
     def mean_s(self):
         return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) / 1e3
+
+    def spread(self):
+        """(min, median, max) launch time in microseconds."""
+        t = np.array([a.elapsed_time(b) for a, b in self.pairs]) * 1e3
+        return float(t.min()), float(np.median(t)), float(t.max())
+
+
+def warm(step, args):
+    """Untimed steps right before the timed region: the checks before it
+    leave the GPU idle and its clocks fall back."""
+    import torch
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
 
 
 def devtab(torch, a):
@@ -243,7 +269,8 @@ def wl_llama3_8b_layer(args, torch, H, O):
                for _ in range(2)]
     status = torch.zeros(max(t["n"] for t in tabs) * 32, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
-    t_lz4, t_tile = Timed(torch, stream), Timed(torch, stream)
+    t_lz4, t_tile = (Timed(torch, stream, args.steps * args.layers),
+                     Timed(torch, stream, args.steps * args.layers))
 
     def run_layer(l, timed):
         L = layers_host[l % args.distinct]
@@ -266,8 +293,7 @@ def wl_llama3_8b_layer(args, torch, H, O):
         for l in range(args.layers):
             run_layer(l, timed)
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     codes = status.cpu().numpy().view(np.int32)[0::8][:tabs[-1]["n"]]
     assert (codes == 0).all(), "LZ4 block errors"
@@ -282,7 +308,7 @@ def wl_llama3_8b_layer(args, torch, H, O):
         check = float(np.abs(got - ref).max() / rms)
         log(f"spot check layer0/q rows 0..{sub}: max|bf16 - oracle f32| = {check:.2e} x RMS")
 
-    torch.cuda.synchronize()
+    warm(step, args)
     ta, tz = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ta.record(stream)
     for _ in range(args.steps):
@@ -297,6 +323,10 @@ def wl_llama3_8b_layer(args, torch, H, O):
     log(f"per layer: lz4 {lz4_s * 1e6:.1f} us ({(comp_bytes + in_tile) / lz4_s / 1e9:.0f} GB/s "
         f"in+out), tiles {tile_s * 1e6:.1f} us ({(in_tile + out_bytes_layer) / tile_s / 1e9:.0f} "
         f"GB/s in+out)")
+    log("tile launch us min/median/max %.1f / %.1f / %.1f; per step (ms): %s" % (
+        *t_tile.spread(), " ".join("%.2f" % (sum(a.elapsed_time(b) for a, b in
+                                                  t_tile.pairs[i * args.layers:(i + 1) * args.layers]))
+                                   for i in range(args.steps))))
     cpu = None
     if not args.no_cpu and O is not None:
         log("cpu baseline ...")
@@ -338,14 +368,14 @@ def wl_int4(args, torch, H, O):
         for _ in range(launches):
             ctx.dequant_int4(dq, q.size, n, out, dtype=H.F32, stream=sp)
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     exact = None
     if O is not None:
         ref = O.dequantize_int4(q, n, threads=cpu_threads())
         exact = bool((out.cpu().numpy().view(np.uint32) == ref.view(np.uint32)).all())
         log(f"bit-exact vs oracle: {exact}")
+    warm(step, args)
     T = Timed(torch, stream)
     e = T.start()
     for _ in range(args.steps):
@@ -410,14 +440,14 @@ def wl_lz4(args, torch, H, O):
         for _ in range(launches):
             assert ctx.lz4_decompress_batch(*a, stream=sp) == H.OK
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     codes = st.cpu().numpy().view(np.int32)[0::8]
     assert (codes == 0).all()
     o = d_out.cpu().numpy()
     exact = all(o[j * 65536:(j + 1) * 65536].tobytes() == srcs[pick[j]] for j in range(nb))
     log(f"all {nb} blocks bit-exact: {exact}")
+    warm(step, args)
     T = Timed(torch, stream)
     e = T.start()
     for _ in range(args.steps):
@@ -468,8 +498,7 @@ def wl_idct(args, torch, H, O):
         for _ in range(launches):
             ctx.hctt_decode(dt, tiles.size, rows, cols, k, out, dtype=H.BF16, stream=sp)
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     check = None
     if O is not None:
@@ -480,6 +509,7 @@ def wl_idct(args, torch, H, O):
         rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
         check = float(np.abs(got - ref).max() / rms)
         log(f"spot check rows 0..{sub}: max|bf16 - oracle f32| = {check:.2e} x RMS")
+    warm(step, args)
     T = Timed(torch, stream)
     e = T.start()
     for _ in range(args.steps):
@@ -550,8 +580,7 @@ def wl_hct3(args, torch, H, O):
     def step():
         dec.decompress_device(data, d_data, [n, n], out, dtype=H.BF16, stream=sp)
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     check, cpu = None, None
     if O is not None:
@@ -567,6 +596,7 @@ def wl_hct3(args, torch, H, O):
             cpu = {"value": round(n * n * 2 / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                    "sample": f"one full {n}x{n} decode by the oracle (container scatter + the reference's "
                              f"FFT-based idct_2d in f32), bf16-equivalent output bytes, 1 thread, {secs:.1f} s"}
+    warm(step, args)
     T = Timed(torch, stream)
     e = T.start()
     for _ in range(args.steps):
@@ -614,7 +644,8 @@ def wl_stream(args, torch, H, O):
     status = torch.zeros(T["n"] * 32, dtype=torch.uint8, device="cuda")
     copied = [torch.cuda.Event() for _ in range(2)]
     consumed = [torch.cuda.Event() for _ in range(2)]
-    t_dec, t_h2d = Timed(torch, comp_stream), Timed(torch, copy_stream)
+    t_dec, t_h2d = (Timed(torch, comp_stream, args.stream_layers),
+                    Timed(torch, copy_stream, args.stream_layers))
     torch.cuda.synchronize()
 
     def run(nlayers, timed):
@@ -639,10 +670,11 @@ def wl_stream(args, torch, H, O):
             if timed:
                 t_dec.stop(e)
 
-    run(2 * args.warmup, False)
+    run(2, False)                            # correctness pass (checked below)
     torch.cuda.synchronize()
     codes = status.cpu().numpy().view(np.int32)[0::8]
     assert (codes == 0).all()
+    warm(lambda: run(2, False), args)
     ta, tz = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ta.record(comp_stream)
     copy_stream.wait_event(ta)
@@ -722,13 +754,13 @@ def wl_xxh3(args, torch, H, O):
         for _ in range(launches):
             ctx.xxh3_64_batch(d_in, d_in.numel(), d_off, d_len, nb, d_out, stream=sp)
 
-    for _ in range(args.warmup):
-        step()
+    step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
     got = d_out.cpu().numpy().view(np.uint64)
     exact = all(int(got[j]) == H.xxh3_64(blob[in_off[j]:in_off[j] + in_len[j]].tobytes())
                 for j in range(0, nb, 97))
     log(f"spot check of every 97th block vs the host XXH3: {exact}")
+    warm(step, args)
     T = Timed(torch, stream)
     e = T.start()
     for _ in range(args.steps):
@@ -762,8 +794,9 @@ WORKLOADS = {"llama3-8b-layer": wl_llama3_8b_layer, "xxh3-256mib": wl_xxh3, "int
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20,
+                    help="untimed steps first (the clocks settle within ~50 ms of load)")
     ap.add_argument("--workload", default="llama3-8b-layer", choices=sorted(WORKLOADS))
     ap.add_argument("--layers", type=int, default=32, help="llama3-8b-layer: layers per step")
     ap.add_argument("--stream-layers", type=int, default=80, help="llama70b-stream: layers")
