@@ -82,8 +82,8 @@ hipError_t launch_dequant_int4(const uint8_t *d_q, size_t n, size_t nscale_group
 
 // Batched LZ4: dispatches to the LDS-ring decoder (lz4_ring.hip) or, when
 // the environment sets HH_LZ4_KERNEL=window, to the register-window decoder
-// (lz4_decode.hip).  The ring is 8 KiB; HH_LZ4_KERNEL=ring16 / ring32 select
-// a 16 / 32 KiB ring.
+// (lz4_decode.hip).  The ring is 4 KiB with a 4 KiB input stage;
+// HH_LZ4_KERNEL=ring8 / ring16 / ring32 select an 8 / 16 / 32 KiB ring.
 hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
                             const uint32_t *d_in_len, uint8_t *d_out,
                             const uint64_t *d_out_off, const uint32_t *d_out_cap,

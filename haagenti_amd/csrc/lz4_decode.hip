@@ -353,7 +353,10 @@ hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t
     if (nblocks == 0) return hipSuccess;
     const char *k = std::getenv("HH_LZ4_KERNEL");
     if (k == nullptr || std::strcmp(k, "window") != 0) {
-        const uint32_t kib = k == nullptr ? 8u : std::strcmp(k, "ring16") == 0 ? 16u : std::strcmp(k, "ring32") == 0 ? 32u : 8u;
+        uint32_t kib = 4u;
+        if (k != nullptr && std::strcmp(k, "ring8") == 0) kib = 8u;
+        if (k != nullptr && std::strcmp(k, "ring16") == 0) kib = 16u;
+        if (k != nullptr && std::strcmp(k, "ring32") == 0) kib = 32u;
         return launch_lz4_ring(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,
                                d_status, kib, s);
     }

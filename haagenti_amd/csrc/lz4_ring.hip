@@ -239,18 +239,34 @@ struct RingDec {
                     m = m + 1 == off ? 0u : m + 1;
                 }
                 o = u32x4{d[0], d[1], d[2], d[3]};
+            } else if constexpr (K <= 1) {
+                // the source of chunk byte 0 (lane 0: up to 15 before src)
+                // is at the same offset within a 16-byte chunk for every
+                // lane: two aligned 16-byte LDS reads per lane (no bank
+                // conflicts) and a funnel shift by that uniform offset
+                const uint32_t sp = src + cv - v;
+                const uint32_t q16 = sp & ~15u;
+                const uint32_t sh = __builtin_amdgcn_readfirstlane((src - (v & 15u)) & 15u);
+                u32x4 x0, x1;
+                if constexpr (K == 0) {
+                    x0 = *reinterpret_cast<const u32x4 *>(stage + (int32_t)q16);
+                    x1 = *reinterpret_cast<const u32x4 *>(stage + (int32_t)q16 + 16);
+                } else {
+                    x0 = *reinterpret_cast<const u32x4 *>(ring + (q16 & kRM));
+                    x1 = *reinterpret_cast<const u32x4 *>(ring + ((q16 + 16u) & kRM));
+                }
+                const uint32_t r = sh & 3u;
+                switch (sh >> 2) {
+                    case 0: o = realign(x0[0], x0[1], x0[2], x0[3], x1[0], r); break;
+                    case 1: o = realign(x0[1], x0[2], x0[3], x1[0], x1[1], r); break;
+                    case 2: o = realign(x0[2], x0[3], x1[0], x1[1], x1[2], r); break;
+                    default: o = realign(x0[3], x1[0], x1[1], x1[2], x1[3], r); break;
+                }
             } else {
                 const uint32_t sp = src + cv - v;  // source of chunk byte 0 (lane 0: up to 15 before src)
-                const uint32_t sb4 = sp & ~3u, sh = sp & 3u;
+                const uint32_t sh = sp & 3u;
                 uint32_t d[5];
-                if constexpr (K == 0) {
-                    const uint32_t *q = reinterpret_cast<const uint32_t *>(stage + (int32_t)sb4);
-#pragma unroll
-                    for (int i = 0; i < 5; i++) d[i] = q[i];
-                } else if constexpr (K == 1) {
-#pragma unroll
-                    for (int i = 0; i < 5; i++) d[i] = *reinterpret_cast<const uint32_t *>(ring + ((sb4 + 4u * i) & kRM));
-                } else {
+                {
                     // output bytes [a0, a0 + cap) only; the first chunk's
                     // source may start before the block's output
                     const int64_t lo = a0, hi = (int64_t)a0 + cap;
@@ -525,11 +541,13 @@ hipError_t launch_lz4_ring(const uint8_t *d_in, size_t in_total, const uint64_t 
                            uint32_t ring_kib, hipStream_t s) {
     if (nblocks == 0) return hipSuccess;
     switch (ring_kib) {
+        case 8: return launch_ring<8192, 2048>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
+                                               d_out_cap, nblocks, d_status, s);
         case 16: return launch_ring<16384, 3072>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
                                                  d_out_cap, nblocks, d_status, s);
         case 32: return launch_ring<32768, 4096>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
                                                  d_out_cap, nblocks, d_status, s);
-        default: return launch_ring<8192, 2048>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
+        default: return launch_ring<4096, 4096>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
                                                 d_out_cap, nblocks, d_status, s);
     }
 }

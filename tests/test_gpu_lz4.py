@@ -10,9 +10,9 @@ import oracle_lib as O
 pytestmark = pytest.mark.gpu
 
 # Every test runs on each decoder the batched entry point can dispatch to:
-# the LDS-ring decoder with its 8 (default), 16 and 32 KiB rings, and the
+# the LDS-ring decoder with its 4 (default), 8, 16 and 32 KiB rings, and the
 # register-window decoder.
-KERNELS = ["ring8", "ring16", "ring32", "window"]
+KERNELS = ["ring4", "ring8", "ring16", "ring32", "window"]
 
 
 @pytest.fixture(autouse=True, params=KERNELS)
@@ -207,12 +207,13 @@ def test_corrupted_stream_fuzz():
 def test_ring_boundaries_far_long_and_periodic_copies():
     # Streams from the oracle compressor whose matches sit on the ring
     # decoder's limits: offsets just below / above what each ring serves
-    # (R - 32 for R = 8, 16, 32 KiB), literals longer than the input stage,
+    # (R - 32 for R = 4, 8, 16, 32 KiB), literals longer than the input stage,
     # matches longer than the ring (periodic and not), and far matches that
     # overlap their own output.
     rng = np.random.default_rng(6)
     srcs = []
-    for L in [100, 992, 993, 2047, 2049, 8159, 8161, 8200, 16351, 16353, 32735, 32737, 40000]:
+    for L in [100, 992, 993, 2047, 2049, 4063, 4065, 4097, 8159, 8161, 8200, 16351, 16353, 32735, 32737,
+              40000]:
         a = rng.integers(0, 256, L, dtype=np.uint8).tobytes()
         srcs.append(a + a)                                     # one match at offset L
     srcs.append(rng.integers(0, 256, 70000, dtype=np.uint8).tobytes())   # one 70 KB literal
