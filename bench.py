@@ -345,7 +345,7 @@ def wl_llama3_8b_layer(args, torch, H, O):
                 roofline("llama3-8b-layer", "hctt_decode_kernel<bf16>", in_tile + out_bytes_layer,
                          tile_s),
                 cpu,
-                {"kernels_us": {"lz4_batch_kernel": round(lz4_s * 1e6, 2),
+                {"kernels_us": {"lz4_ring_kernel": round(lz4_s * 1e6, 2),
                                 "hctt_decode_kernel": round(tile_s * 1e6, 2)},
                  "lz4_roofline": {"achieved": round((comp_bytes + in_tile) / lz4_s / 1e9, 1),
                                   "frac": round((comp_bytes + in_tile) / lz4_s / 1e9 / HBM_PEAK_GBS, 4)},
@@ -474,7 +474,7 @@ def wl_lz4(args, torch, H, O):
                 "synthetic (64 distinct seeded blocks, seeded coin per block)",
                 {"blocks": nb, "block_bytes": 65536, "in_bytes": int(blob.size),
                  "launches_per_step": launches},
-                roofline("lz4-256mib", "lz4_batch_kernel", blob.size + out_b, per), cpu,
+                roofline("lz4-256mib", "lz4_ring_kernel<4096, 4096>", blob.size + out_b, per), cpu,
                 {"bit_exact": exact})
 
 
@@ -708,7 +708,7 @@ def wl_stream(args, torch, H, O):
                  "rho": [round(float(r), 4) for r in rhos], "k": ks,
                  "compressed_bytes_per_layer": int(nin), "out_dtype": "bf16",
                  "source": "pinned host memory", "value_is": "decode-only (inputs in HBM)"},
-                roofline("llama70b-stream", "lz4_batch_kernel + hctt_decode_kernel<bf16>",
+                roofline("llama70b-stream", "lz4_ring_kernel + hctt_decode_kernel<bf16>",
                          L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
                 cpu,
                 {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
