@@ -11,7 +11,11 @@ block size, 16 KiB, rounded down to whole tiles;
 crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes 32 such layers
 back to back into bf16 tensors: per layer one batched LZ4 launch (compressed
 -> tile bytes) and one batched tile launch (dequant + scatter + inverse DCT
-on MFMA -> bf16).  Inputs are resident in HBM before timing starts.
+on MFMA -> bf16).  Inputs are resident in HBM before timing starts.  The
+step time brackets all 32 layers; per-kernel launch times (the roofline's
+average launch) come from HIP events around the launches of every 8th layer
+of the timed steps (--kernel-sample), since an event record between every
+pair of launches would itself cost the stream ~5 % of the step.
 
 Other workloads (one JSON line each, same contract):
   int4-4096        4096x4096 f32 N(0, 0.02) through quantize_int4 (block 32,
@@ -269,13 +273,18 @@ def wl_llama3_8b_layer(args, torch, H, O):
                for _ in range(2)]
     status = torch.zeros(max(t["n"] for t in tabs) * 32, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
-    t_lz4, t_tile = (Timed(torch, stream, args.steps * args.layers),
-                     Timed(torch, stream, args.steps * args.layers))
+    # per-kernel HIP events bracket the launches of every kernel_sample-th
+    # layer of the timed steps (an event record between two launches costs
+    # the stream a few microseconds)
+    sampled = [l for l in range(args.layers) if l % args.kernel_sample == 0]
+    t_lz4, t_tile = (Timed(torch, stream, args.steps * len(sampled)),
+                     Timed(torch, stream, args.steps * len(sampled)))
 
     def run_layer(l, timed):
         L = layers_host[l % args.distinct]
         T = tabs[l % args.distinct]
         s = scratch[l % 2]
+        timed = timed and l % args.kernel_sample == 0
         e = t_lz4.start() if timed else None
         rc = ctx.lz4_decompress_batch(d_comp[l], d_comp[l].numel(), T["in_off"], T["in_len"], s,
                                       T["out_off"], T["out_cap"], T["n"], status, stream=sp)
@@ -323,9 +332,9 @@ def wl_llama3_8b_layer(args, torch, H, O):
     log(f"per layer: lz4 {lz4_s * 1e6:.1f} us ({(comp_bytes + in_tile) / lz4_s / 1e9:.0f} GB/s "
         f"in+out), tiles {tile_s * 1e6:.1f} us ({(in_tile + out_bytes_layer) / tile_s / 1e9:.0f} "
         f"GB/s in+out)")
-    log("tile launch us min/median/max %.1f / %.1f / %.1f; per step (ms): %s" % (
+    log("tile launch us min/median/max %.1f / %.1f / %.1f; sampled tile time per step (ms): %s" % (
         *t_tile.spread(), " ".join("%.2f" % (sum(a.elapsed_time(b) for a, b in
-                                                  t_tile.pairs[i * args.layers:(i + 1) * args.layers]))
+                                                  t_tile.pairs[i * len(sampled):(i + 1) * len(sampled)]))
                                    for i in range(args.steps))))
     cpu = None
     if not args.no_cpu and O is not None:
@@ -803,6 +812,8 @@ def main():
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-sample", type=int, default=8,
+                    help="llama3-8b-layer: per-kernel events on every n-th layer of the timed steps")
     ap.add_argument("--lz4-block", type=int, default=16384,
                     help="LZ4 block size in bytes before rounding down to whole tiles "
                          "(the reference HctWriter default is 16 KiB)")
