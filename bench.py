@@ -29,7 +29,9 @@ Other workloads (one JSON line each, same contract):
                    gate,up,down 28672x8192 / 8192x28672), per-tensor retention
                    U[0.10, 0.50]; compressed layers in pinned host memory,
                    H2D copies on a copy stream overlapped with decode into a
-                   double-buffered bf16 layer slot
+                   double-buffered bf16 layer slot; --from-file reads every
+                   layer from its seven HCT v2 files (mmap) into double-
+                   buffered pinned staging instead
   xxh3-256mib      HCT v2 block validation: XXH3-64 of the 4096 compressed
                    blocks of lz4-256mib (one wavefront per block), the
                    checksum HctReaderV2 verifies per block; value = hashed
@@ -627,6 +629,25 @@ def wl_hct3(args, torch, H, O):
                 {"spot_check_max_err_over_rms": check})
 
 
+def write_layer_files(H, L, shapes, d):
+    """The layer's tensors as HCT v2 files (one per tensor, its LZ4 blocks
+    with their XXH3 in the index: HctWriterV2), in d.  Returns, per file,
+    (path, offset of its first block in the layer blob, payload bytes)."""
+    out = []
+    for T, (name, rows, cols) in zip(L["tensors"], shapes):
+        sel = np.flatnonzero((L["out_off"] >= T["soff"]) & (L["out_off"] < T["soff"] + T["tlen"]))
+        w = H.HctWriterV2(2, [rows, cols], int(L["out_cap"][sel[0]]))      # dtype 2 = BF16
+        for j in sel:
+            a = int(L["in_off"][j])
+            w.add_block(L["blob"][a:a + int(L["in_len"][j])].tobytes(), int(L["out_cap"][j]))
+        path = os.path.join(d, f"{name}.hct")
+        with open(path, "wb") as f:
+            f.write(w.finish())
+        first = int(L["in_off"][sel[0]])
+        out.append((path, first, int(L["in_off"][sel[-1]]) + int(L["in_len"][sel[-1]]) - first))
+    return out
+
+
 def wl_stream(args, torch, H, O):
     rng = np.random.default_rng(70)
     rhos = rng.uniform(0.10, 0.50, len(L70B))
@@ -643,6 +664,39 @@ def wl_stream(args, torch, H, O):
     csp, ysp = comp_stream.cuda_stream, copy_stream.cuda_stream
     host = torch.from_numpy(L["blob"].copy()).pin_memory()
     nin = host.numel()
+    files, maps, pool, host_b = None, [], None, None
+    if args.from_file:
+        # the layer as HCT v2 files, memory-mapped; each layer's payloads are
+        # copied from the maps into one of two pinned staging buffers (by
+        # host threads) while the other buffer's H2D copy and decode run
+        import concurrent.futures as cf
+        import mmap
+        import tempfile
+        d = tempfile.mkdtemp(prefix="hct70b_", dir=os.environ.get("TMPDIR", "/tmp"))
+        files = write_layer_files(H, L, L70B, d)
+        for path, first, nbytes in files:
+            f = open(path, "rb")
+            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+            r = H.HctReaderV2(mm[:])                  # header checksum, block index
+            r.validate_checksums()
+            start = r.data_offset()
+            assert mm[start:start + nbytes] == L["blob"][first:first + nbytes].tobytes()
+            maps.append((f, mm, start, first, nbytes))
+        host_b = [torch.empty(nin, dtype=torch.uint8).pin_memory() for _ in range(2)]
+        pool = cf.ThreadPoolExecutor(max_workers=8)
+        log(f"wrote {len(files)} HCT v2 files ({sum(x[2] for x in files) / 1e6:.1f} MB of blocks) to {d}")
+
+    def read_layer(b):
+        dst = host_b[b].numpy()
+        jobs = []
+        for _, mm, start, first, nbytes in maps:
+            step = 8 << 20
+            for o in range(0, nbytes, step):
+                n = min(step, nbytes - o)
+                jobs.append(pool.submit(np.copyto, dst[first + o:first + o + n],
+                                        np.frombuffer(mm, np.uint8, n, start + o)))
+        for j in jobs:
+            j.result()
     d_in = [torch.empty(nin, dtype=torch.uint8, device="cuda") for _ in range(2)]
     scratch = torch.empty(L["scratch_bytes"], dtype=torch.uint8, device="cuda")
     slot = [[torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L70B]
@@ -657,13 +711,22 @@ def wl_stream(args, torch, H, O):
                     Timed(torch, copy_stream, args.stream_layers))
     torch.cuda.synchronize()
 
+    read_s = [0.0]
+
     def run(nlayers, timed):
         for l in range(nlayers):
             b = l % 2
+            src = host
+            if args.from_file:
+                copied[b].synchronize()              # layer l - 2's H2D has read host_b[b]
+                r0 = time.perf_counter()
+                read_layer(b)
+                read_s[0] += time.perf_counter() - r0 if timed else 0.0
+                src = host_b[b]
             copy_stream.wait_event(consumed[b])      # layer l - 2 has finished reading d_in[b]
             e = t_h2d.start() if timed else None
             with torch.cuda.stream(copy_stream):
-                d_in[b].copy_(host, non_blocking=True)
+                d_in[b].copy_(src, non_blocking=True)
             if timed:
                 t_h2d.stop(e)
             copied[b].record(copy_stream)
@@ -700,6 +763,15 @@ def wl_stream(args, torch, H, O):
     # fraction of the shorter stage hidden under the longer one
     per_layer = e2e_s / args.stream_layers
     overlap = max(0.0, min(1.0, (dec_s + h2d_s - per_layer) / min(dec_s, h2d_s)))
+    file_info = None
+    if args.from_file:
+        file_info = {"files": len(files), "host_read_gbs": round(nin * args.stream_layers / read_s[0] / 1e9, 2),
+                     "source": "HCT v2 files (mmap, page cache) -> pinned staging -> H2D"}
+        log(f"from files: host reads {file_info['host_read_gbs']} GB/s")
+        for f, mm, *_ in maps:
+            mm.close()
+            f.close()
+        pool.shutdown()
     log(f"per layer: decode {dec_s * 1e3:.2f} ms ({value:.0f} GB/s out), H2D {h2d_s * 1e3:.2f} ms "
         f"({h2d_gbs:.1f} GB/s), end to end {e2e_s / args.stream_layers * 1e3:.2f} ms/layer "
         f"({e2e:.0f} GB/s out); wall {wall:.2f}s")
@@ -716,14 +788,15 @@ def wl_stream(args, torch, H, O):
                 {"layers": args.stream_layers, "elements_per_layer": n_elem,
                  "rho": [round(float(r), 4) for r in rhos], "k": ks,
                  "compressed_bytes_per_layer": int(nin), "out_dtype": "bf16",
-                 "source": "pinned host memory", "value_is": "decode-only (inputs in HBM)"},
+                 "source": file_info["source"] if file_info else "pinned host memory",
+                 "value_is": "decode-only (inputs in HBM)"},
                 roofline("llama70b-stream", "lz4_ring_kernel + hctt_decode_kernel<bf16>",
                          L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
                 cpu,
                 {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
                  "decode_ms_per_layer": round(dec_s * 1e3, 3),
                  "h2d_ms_per_layer": round(h2d_s * 1e3, 3),
-                 "overlap_fraction": round(overlap, 3)})
+                 "overlap_fraction": round(overlap, 3), "from_file": file_info})
 
 
 def wl_copy(args, torch, H, O):
@@ -812,6 +885,8 @@ def main():
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--from-file", action="store_true",
+                    help="llama70b-stream: read each layer from HCT v2 files (mmap) into pinned staging")
     ap.add_argument("--kernel-sample", type=int, default=8,
                     help="llama3-8b-layer: per-kernel events on every n-th layer of the timed steps")
     ap.add_argument("--lz4-block", type=int, default=16384,

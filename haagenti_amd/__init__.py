@@ -350,6 +350,10 @@ class HctReader:
     def num_blocks(self):
         return int(self._info.num_blocks)
 
+    def data_offset(self):
+        """File offset of the first compressed block (blocks follow each other)."""
+        return int(self._info.data_offset)
+
     def _entry(self, idx):
         import struct
         off, csz = struct.unpack_from("<II", self._data, 64 + 8 * idx)
