@@ -148,12 +148,13 @@ bool unwrap_zstd(const uint8_t *&data, size_t &len, std::vector<uint8_t> &hold) 
 }
 
 // IDCT of d_dense into d_out (dtype), with d_tmp as the GEMM intermediate;
-// d_dense is overwritten for 16-bit outputs.
+// d_dense is overwritten for 16-bit outputs; f16_exact when its values came
+// from f16 coefficients.
 int32_t inverse_to(hh_context *ctx, float *d_dense, float *d_tmp, uint32_t rows, uint32_t cols,
-                   int32_t dtype, void *d_out, hipStream_t s) {
+                   int32_t dtype, void *d_out, hipStream_t s, bool f16_exact) {
     const uint64_t total = (uint64_t)rows * cols;
     float *x = dtype == HH_F32 ? reinterpret_cast<float *>(d_out) : d_dense;
-    int32_t rc = hh::dct2d_full(ctx, true, d_dense, d_tmp, x, rows, cols, s);
+    int32_t rc = hh::dct2d_full(ctx, true, d_dense, d_tmp, x, rows, cols, s, f16_exact);
     if (rc != HH_OK) return rc;
     if (dtype != HH_F32) return from_hip(hh::launch_f32_convert(x, total, dtype, d_out, s));
     return HH_OK;
@@ -229,7 +230,7 @@ int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, con
     float *d_tmp = reinterpret_cast<float *>(base + mat);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     rc = scatter_layers(layers, total, 0, d_dense, base + 2 * mat, s);
-    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s, true);
     if (rc != HH_OK) return rc;
     return from_hip(hipStreamSynchronize(s));
 }
@@ -259,7 +260,7 @@ int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const 
     float *d_tmp = reinterpret_cast<float *>(base + mat);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     rc = scatter_layers_device(layers, h_data, d_data, total, d_dense, base + 2 * mat, s);
-    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s, true);
     return rc;
 }
 
@@ -349,7 +350,7 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     std::vector<Layer> layers{Layer{f0 + 24, coef.data(), ntot}};
     rc = scatter_layers(layers, n, f32c, d_dense, base + 2 * mat, s);
-    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, h, w, out_dtype, d_out, s);
+    if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, h, w, out_dtype, d_out, s, !f32c);
     if (rc != HH_OK) return rc;
     if (status) status->written = n;
     return from_hip(hipStreamSynchronize(s));

@@ -25,6 +25,17 @@
 // from an exact integer reduction of the cosine argument and cached per
 // context.  fp32 GEMMs with K = n accumulate to ~1e-6 x RMS, against the
 // 1e-3 x RMS bar of the tolerance-based IDCT parity.
+//
+// The inverse runs on the f16 MFMA instead (16x the fp32 MFMA rate): every
+// operand is split into f16 hi + lo (x = hi + lo to ~2^-22 relative) and each
+// product of two split operands is three f16 GEMMs with f32 accumulation
+// (hi*hi + hi*lo + lo*hi; the dropped lo*lo is ~2^-22 relative).  C is first
+// scaled by a power of two 2^e chosen from max|C| so that |C 2^e| and the
+// intermediate T = B_w^T C 2^e stay below 2^14 (|T| <= max|C| sqrt(w)), far
+// from f16 overflow; a last elementwise pass multiplies by 2^-e (exact).
+// HH_DCT_F32=1 selects the fp32 GEMMs.
+#include <cstdlib>
+
 #include <rocblas/rocblas.h>
 
 #include "hh_internal.hpp"
@@ -193,6 +204,70 @@ __global__ __launch_bounds__(256) void f32_convert_kernel(const float *__restric
 
 uint32_t blocks_for(uint64_t n, uint32_t per) { return (uint32_t)((n + per - 1) / per); }
 
+// Per-block max |x| over a grid-stride range.
+__global__ __launch_bounds__(256) void amax_kernel(const float *__restrict__ x, uint64_t n,
+                                                   float *__restrict__ partial) {
+    __shared__ float sm[256];
+    float m = 0.0f;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256)
+        m = fmaxf(m, fabsf(x[i]));
+    sm[threadIdx.x] = m;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) sm[threadIdx.x] = fmaxf(sm[threadIdx.x], sm[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = sm[0];
+}
+
+// consts = {0, 1, 2^e, 2^-e} with e the largest integer for which
+// max|C| 2^e sqrt(w) <= 2^14 (e = 0 for an all-zero or non-finite C).
+__global__ __launch_bounds__(256) void split_scale_kernel(const float *__restrict__ partial, uint32_t np,
+                                                          uint32_t w, float *__restrict__ consts) {
+    __shared__ float sm[256];
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < np; i += 256) m = fmaxf(m, partial[i]);
+    sm[threadIdx.x] = m;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) sm[threadIdx.x] = fmaxf(sm[threadIdx.x], sm[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float mx = sm[0];
+        int e = 0;
+        if (mx > 0.0f && isfinite(mx)) {
+            int q;
+            frexpf(16384.0f / (mx * sqrtf((float)w)), &q);  // 2^(q-1) <= ratio < 2^q
+            e = q - 1;
+            e = e < -120 ? -120 : e > 120 ? 120 : e;
+        }
+        consts[0] = 0.0f;
+        consts[1] = 1.0f;
+        consts[2] = ldexpf(1.0f, e);
+        consts[3] = ldexpf(1.0f, -e);
+    }
+}
+
+// hi = f16(x s), lo = f16(x s - hi) (round to nearest even; x s - hi is
+// exact in f32); s = *scale, or 1 without one.
+__global__ __launch_bounds__(256) void split_f16_kernel(const float *__restrict__ x, uint64_t n,
+                                                        const float *__restrict__ scale,
+                                                        _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = scale ? x[i] * scale[0] : x[i];
+    const _Float16 h = (_Float16)v;
+    hi[i] = h;
+    lo[i] = (_Float16)(v - (float)h);
+}
+
+// x *= *scale, in place
+__global__ __launch_bounds__(256) void scale_kernel(float *__restrict__ x, uint64_t n, const float *__restrict__ scale) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] *= scale[0];
+}
+
 }  // namespace
 
 hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t *d_block_sums,
@@ -239,7 +314,9 @@ static int32_t basis_for(hh_context *ctx, uint32_t n, hipStream_t s, const float
     hh_context::Basis &b = ctx->dct_basis[v];
     if (b.d) {
         hipError_t e = hipFree(b.d);
+        if (b.hl && e == hipSuccess) e = hipFree(b.hl);
         b.d = nullptr;
+        b.hl = nullptr;
         b.n = 0;
         if (e != hipSuccess) return from_hip(e);
     }
@@ -255,6 +332,32 @@ static int32_t basis_for(hh_context *ctx, uint32_t n, hipStream_t s, const float
     if (e != hipSuccess) return from_hip(e);
     *out = b.d;
     return HH_OK;
+}
+
+// The f16 hi / lo halves of the cached basis B_n (made on first use).
+static int32_t basis_split_for(hh_context *ctx, uint32_t n, const float *bd, hipStream_t s, const _Float16 **hi,
+                               const _Float16 **lo) {
+    for (int i = 0; i < 2; i++) {
+        hh_context::Basis &b = ctx->dct_basis[i];
+        if (b.d != bd) continue;
+        const uint64_t nn = (uint64_t)n * n;
+        if (!b.hl) {
+            hipError_t e = hipMalloc(&b.hl, 2 * nn * sizeof(uint16_t));
+            if (e != hipSuccess) {
+                b.hl = nullptr;
+                return from_hip(e);
+            }
+            _Float16 *h = reinterpret_cast<_Float16 *>(b.hl);
+            hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(nn, 256)), dim3(256), 0, s, b.d, nn,
+                               (const float *)nullptr, h, h + nn);
+            e = hipGetLastError();
+            if (e != hipSuccess) return from_hip(e);
+        }
+        *hi = reinterpret_cast<const _Float16 *>(b.hl);
+        *lo = *hi + nn;
+        return HH_OK;
+    }
+    return HH_ERR_INVALID_ARGUMENT;
 }
 
 static int32_t blas_for(hh_context *ctx, hipStream_t s, rocblas_handle *h) {
@@ -278,8 +381,78 @@ static int32_t blas_status(rocblas_status st) {
     }
 }
 
+// X = B_h^T C B_w on the f16 MFMA (see the header): d_tmp holds T in f32.
+static int32_t idct_split(hh_context *ctx, rocblas_handle h, const float *d_in, float *d_tmp, float *d_out,
+                          uint32_t rows, uint32_t cols, const float *bw, const float *bh, hipStream_t s,
+                          bool f16_exact) {
+    const uint64_t total = (uint64_t)rows * cols;
+    const _Float16 *bw_hi, *bw_lo, *bh_hi, *bh_lo;
+    int32_t rc = basis_split_for(ctx, cols, bw, s, &bw_hi, &bw_lo);
+    if (rc != HH_OK) return rc;
+    rc = basis_split_for(ctx, rows, bh, s, &bh_hi, &bh_lo);
+    if (rc != HH_OK) return rc;
+    // split scratch: hi and lo operand halves, block maxima, constants
+    const uint32_t np = 1024;
+    const size_t need = 2 * total * sizeof(uint16_t) + (np + 4) * sizeof(float) + 256;
+    if (ctx->split_bytes < need) {
+        if (ctx->d_split) {
+            hipError_t e = hipFree(ctx->d_split);
+            ctx->d_split = nullptr;
+            ctx->split_bytes = 0;
+            if (e != hipSuccess) return from_hip(e);
+        }
+        hipError_t e = hipMalloc(&ctx->d_split, need);
+        if (e != hipSuccess) {
+            ctx->d_split = nullptr;
+            return from_hip(e);
+        }
+        ctx->split_bytes = need;
+    }
+    _Float16 *ohi = reinterpret_cast<_Float16 *>(ctx->d_split);
+    _Float16 *olo = ohi + total;
+    float *partial = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->d_split) +
+                                               ((2 * total * sizeof(uint16_t) + 255) & ~(size_t)255));
+    float *consts = partial + np;
+    hipLaunchKernelGGL(amax_kernel, dim3(np), dim3(256), 0, s, d_in, total, partial);
+    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, partial, np, cols, consts);
+    hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_in, total,
+                       (const float *)(consts + 2), ohi, olo);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e);
+    const int m = (int)cols, n = (int)rows;
+    // host scalars (rocBLAS reads device scalars back to the host per call);
+    // 2^-e is applied by a last elementwise pass
+    const float c0 = 0.0f, c1 = 1.0f;
+    const float *k0 = &c0, *k1 = &c1;
+    const rocblas_datatype f16 = rocblas_datatype_f16_r, f32 = rocblas_datatype_f32_r;
+    auto gemm = [&](rocblas_operation ta, rocblas_operation tb, int k, const float *alpha, const void *a, int lda,
+                    const void *b, int ldb, const float *beta, float *c) {
+        return rocblas_gemm_ex(h, ta, tb, m, n, k, alpha, a, f16, lda, b, f16, ldb, beta, c, f32, m, c, f32, m, f32,
+                               rocblas_gemm_algo_standard, 0, 0);
+    };
+    const rocblas_operation N = rocblas_operation_none, T = rocblas_operation_transpose;
+    // T^T = B_w^T (C 2^e)^T, three passes (column-major views as below)
+    rocblas_status st = gemm(N, N, m, k1, bw_hi, m, ohi, m, k0, d_tmp);
+    if (st == rocblas_status_success) st = gemm(N, N, m, k1, bw_lo, m, ohi, m, k1, d_tmp);
+    // (an input of f16 values scaled by 2^e has no low half)
+    if (st == rocblas_status_success && !f16_exact) st = gemm(N, N, m, k1, bw_hi, m, olo, m, k1, d_tmp);
+    if (st == rocblas_status_success) {
+        hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_tmp, total,
+                           (const float *)nullptr, ohi, olo);
+        if (hipGetLastError() != hipSuccess) st = rocblas_status_internal_error;
+    }
+    // X^T 2^e = T^T B_h, three passes; then X = 2^-e (X 2^e)
+    if (st == rocblas_status_success) st = gemm(N, T, n, k1, ohi, m, bh_hi, n, k0, d_out);
+    if (st == rocblas_status_success) st = gemm(N, T, n, k1, ohi, m, bh_lo, n, k1, d_out);
+    if (st == rocblas_status_success) st = gemm(N, T, n, k1, olo, m, bh_hi, n, k1, d_out);
+    if (st != rocblas_status_success) return blas_status(st);
+    hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
+                       (const float *)(consts + 3));
+    return from_hip(hipGetLastError());
+}
+
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
-                   uint32_t rows, uint32_t cols, hipStream_t s) {
+                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact) {
     if (rows == 0 || cols == 0) return HH_OK;
     const float *bw = nullptr, *bh = nullptr;
     int32_t rc = basis_for(ctx, cols, s, &bw);
@@ -298,6 +471,8 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
     //   forward:  T^T = B_w X^T       (m = w, n = h, k = w)
     //             C^T = T^T B_h^T     (m = w, n = h, k = h)
     const int m = (int)cols, n = (int)rows;
+    const char *f32env = std::getenv("HH_DCT_F32");
+    if (inverse && !(f32env && f32env[0] == '1')) return idct_split(ctx, h, d_in, d_tmp, d_out, rows, cols, bw, bh, s, f16_exact);
     rocblas_status st = rocblas_sgemm(h, inverse ? rocblas_operation_none : rocblas_operation_transpose,
                                       rocblas_operation_none, m, n, m, &one, bw, m, d_in, m, &zero,
                                       d_tmp, m);
@@ -310,9 +485,14 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
 void release_dct_resources(hh_context *ctx) {
     for (int i = 0; i < 2; i++) {
         if (ctx->dct_basis[i].d) hipFree(ctx->dct_basis[i].d);
+        if (ctx->dct_basis[i].hl) hipFree(ctx->dct_basis[i].hl);
         ctx->dct_basis[i].d = nullptr;
+        ctx->dct_basis[i].hl = nullptr;
         ctx->dct_basis[i].n = 0;
     }
+    if (ctx->d_split) hipFree(ctx->d_split);
+    ctx->d_split = nullptr;
+    ctx->split_bytes = 0;
     if (ctx->blas) rocblas_destroy_handle(reinterpret_cast<rocblas_handle>(ctx->blas));
     ctx->blas = nullptr;
 }

@@ -24,11 +24,15 @@ struct hh_context {
     struct Basis {
         uint32_t n = 0;
         float *d = nullptr;
+        uint16_t *hl = nullptr;  // the same as f16 hi (n x n) then lo (n x n)
         uint64_t stamp = 0;
     };
     Basis dct_basis[2];
     uint64_t dct_stamp = 0;
     void *blas = nullptr;
+    // f16 split operands of the whole-matrix inverse DCT (grown on demand)
+    void *d_split = nullptr;
+    size_t split_bytes = 0;
 };
 
 namespace hh {
@@ -115,9 +119,10 @@ hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_w
 hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_out, hipStream_t s);
 // Orthonormal 2-D DCT-III (inverse) or DCT-II (forward) of a row-major
 // rows x cols f32 matrix: two GEMMs through d_tmp (rows*cols f32); d_out may
-// not alias d_in or d_tmp.
+// not alias d_in or d_tmp.  f16_exact: every input value is an f16 value
+// (the inverse then skips the GEMM pass of the input's low f16 half).
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
-                   uint32_t rows, uint32_t cols, hipStream_t s);
+                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact = false);
 void release_dct_resources(hh_context *ctx);
 // zstd::decode_all on the host (host_zstd.cpp): false on a malformed stream.
 bool zstd_decode_all(const uint8_t *in, size_t len, std::vector<uint8_t> &out);
