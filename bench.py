@@ -779,6 +779,8 @@ def wl_stream(args, torch, H, O):
             mm.close()
             f.close()
         pool.shutdown()
+        import shutil
+        shutil.rmtree(os.path.dirname(files[0][0]), ignore_errors=True)
     log(f"per layer: decode {dec_s * 1e3:.2f} ms ({value:.0f} GB/s out), H2D {h2d_s * 1e3:.2f} ms "
         f"({h2d_gbs:.1f} GB/s), end to end {e2e_s / args.stream_layers * 1e3:.2f} ms/layer "
         f"({e2e:.0f} GB/s out); wall {wall:.2f}s")
