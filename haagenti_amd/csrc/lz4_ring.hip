@@ -240,28 +240,18 @@ struct RingDec {
                 }
                 o = u32x4{d[0], d[1], d[2], d[3]};
             } else if constexpr (K <= 1) {
-                // the source of chunk byte 0 (lane 0: up to 15 before src)
-                // is at the same offset within a 16-byte chunk for every
-                // lane: two aligned 16-byte LDS reads per lane (no bank
-                // conflicts) and a funnel shift by that uniform offset
-                const uint32_t sp = src + cv - v;
-                const uint32_t q16 = sp & ~15u;
-                const uint32_t sh = __builtin_amdgcn_readfirstlane((src - (v & 15u)) & 15u);
-                u32x4 x0, x1;
+                const uint32_t sp = src + cv - v;  // source of chunk byte 0 (lane 0: up to 15 before src)
+                const uint32_t sb4 = sp & ~3u, sh = sp & 3u;
+                uint32_t d[5];
                 if constexpr (K == 0) {
-                    x0 = *reinterpret_cast<const u32x4 *>(stage + (int32_t)q16);
-                    x1 = *reinterpret_cast<const u32x4 *>(stage + (int32_t)q16 + 16);
+                    const uint32_t *q = reinterpret_cast<const uint32_t *>(stage + (int32_t)sb4);
+#pragma unroll
+                    for (int i = 0; i < 5; i++) d[i] = q[i];
                 } else {
-                    x0 = *reinterpret_cast<const u32x4 *>(ring + (q16 & kRM));
-                    x1 = *reinterpret_cast<const u32x4 *>(ring + ((q16 + 16u) & kRM));
+#pragma unroll
+                    for (int i = 0; i < 5; i++) d[i] = *reinterpret_cast<const uint32_t *>(ring + ((sb4 + 4u * i) & kRM));
                 }
-                const uint32_t r = sh & 3u;
-                switch (sh >> 2) {
-                    case 0: o = realign(x0[0], x0[1], x0[2], x0[3], x1[0], r); break;
-                    case 1: o = realign(x0[1], x0[2], x0[3], x1[0], x1[1], r); break;
-                    case 2: o = realign(x0[2], x0[3], x1[0], x1[1], x1[2], r); break;
-                    default: o = realign(x0[3], x1[0], x1[1], x1[2], x1[3], r); break;
-                }
+                o = realign(d[0], d[1], d[2], d[3], d[4], sh);
             } else {
                 const uint32_t sp = src + cv - v;  // source of chunk byte 0 (lane 0: up to 15 before src)
                 const uint32_t sh = sp & 3u;
