@@ -373,7 +373,11 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
             // bytes usually lie in the 7 bytes after the token
             const uint64_t t8 = d.read8(ip);
             const uint32_t token = (uint32_t)t8 & 0xffu;
-            uint64_t ll = token >> 4;
+            // lengths are 32-bit: one longer than the block input (only a
+            // run of > 2^24 0xFF bytes makes it) fails the input-length check
+            // below as the reference's 64-bit length does, so it is reported
+            // right away
+            uint32_t ll = token >> 4;
             ip++;
             if (ll == 15) {
                 const uint64_t x = t8 >> 8;
@@ -385,21 +389,30 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
                         pos = ilen;
                         break;
                     }
-                    ll += 255ull * e + ((x >> (8 * e)) & 0xffu);
+                    ll += 255u * e + (uint32_t)((x >> (8 * e)) & 0xffu);
                     ip += e + 1;
-                } else if (end - ip < 7 || (ll += 255ull * 7, ip += 7, !d.extension(ip, end, ll))) {
-                    code = HH_ERR_UNEXPECTED_EOF;
-                    pos = ilen;
-                    break;
+                } else {
+                    uint64_t l64 = ll;
+                    if (end - ip < 7 || (l64 += 255ull * 7, ip += 7, !d.extension(ip, end, l64))) {
+                        code = HH_ERR_UNEXPECTED_EOF;
+                        pos = ilen;
+                        break;
+                    }
+                    if (l64 > 0xffffffffull) {
+                        code = HH_ERR_UNEXPECTED_EOF;
+                        pos = ip;
+                        break;
+                    }
+                    ll = (uint32_t)l64;
                 }
             }
             if (ll > 0) {
-                if ((uint64_t)(end - ip) < ll) {
+                if (end - ip < ll) {
                     code = HH_ERR_UNEXPECTED_EOF;
                     pos = ip;
                     break;
                 }
-                if ((uint64_t)d.op + ll > d.cap) {
+                if (ll > d.cap - d.op) {  // op <= cap throughout
                     code = HH_ERR_BUFFER_TOO_SMALL;
                     req = (uint64_t)d.op + ll;
                     break;
@@ -444,7 +457,7 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
                 pos = d.op;
                 break;
             }
-            uint64_t ml = (token & 15u) + 4u;
+            uint32_t ml = (token & 15u) + 4u;
             if ((token & 15u) == 15u) {
                 const uint64_t x = o8 >> 16;
                 const uint64_t nz = ~x & 0x0000ffffffffffffull;
@@ -455,15 +468,24 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
                         pos = ilen;
                         break;
                     }
-                    ml += 255ull * e + ((x >> (8 * e)) & 0xffu);
+                    ml += 255u * e + (uint32_t)((x >> (8 * e)) & 0xffu);
                     ip += e + 1;
-                } else if (end - ip < 6 || (ml += 255ull * 6, ip += 6, !d.extension(ip, end, ml))) {
-                    code = HH_ERR_UNEXPECTED_EOF;
-                    pos = ilen;
-                    break;
+                } else {
+                    uint64_t m64 = ml;
+                    if (end - ip < 6 || (m64 += 255ull * 6, ip += 6, !d.extension(ip, end, m64))) {
+                        code = HH_ERR_UNEXPECTED_EOF;
+                        pos = ilen;
+                        break;
+                    }
+                    if (m64 > 0xffffffffull) {  // more than any capacity
+                        code = HH_ERR_BUFFER_TOO_SMALL;
+                        req = (uint64_t)d.op + m64;
+                        break;
+                    }
+                    ml = (uint32_t)m64;
                 }
             }
-            if ((uint64_t)d.op + ml > d.cap) {
+            if (ml > d.cap - d.op) {
                 code = HH_ERR_BUFFER_TOO_SMALL;
                 req = (uint64_t)d.op + ml;
                 break;
