@@ -226,3 +226,18 @@ def test_ring_boundaries_far_long_and_periodic_copies():
         outs, st = check_against_oracle(streams, [len(x) for x in srcs], out_align=out_align,
                                         in_align=out_align % 4, out_pad=17)
         assert outs == srcs
+
+
+def test_lengths_beyond_32_bits():
+    # runs of ~2^24 0xFF extension bytes: lengths just below and above 2^32;
+    # a literal that long fails the input-length check, a match that long
+    # the capacity check, with the exact 64-bit required size
+    streams, want = [], []
+    for nrun in ((1 << 24) + 10, (1 << 24) + (1 << 18)):
+        run = b"\xff" * nrun
+        streams += [bytes([0xF0]) + run + b"\x00" + b"tail", bytes([0x1F]) + b"a" + b"\x01\x00" + run + b"\x00"]
+        want.append(1 + 19 + 255 * nrun)
+    assert want[0] < 1 << 32 < want[1]
+    outs, st = check_against_oracle(streams, [1 << 20] * 4)
+    assert [r["code"] for r in st] == [O.UNEXPECTED_EOF, O.BUFFER_TOO_SMALL] * 2
+    assert [st[1]["required"], st[3]["required"]] == want
