@@ -90,12 +90,14 @@ class TurboReader:
     """Reads a turbo output file through a memory map."""
 
     def __init__(self, path_or_bytes):
+        self._map = None
         if isinstance(path_or_bytes, (bytes, bytearray, memoryview)):
             self._buf = memoryview(bytes(path_or_bytes))
             self._file = None
         else:
             self._file = open(path_or_bytes, "rb")
-            self._buf = memoryview(mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ))
+            self._map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ)
+            self._buf = memoryview(self._map)
         if len(self._buf) < 8:
             raise HaagentiError(CORRUPTED_DATA, "turbo file too short")
         hl = struct.unpack_from("<Q", self._buf)[0]
@@ -161,7 +163,19 @@ class TurboReader:
         return loader
 
     def close(self):
-        self._buf = None
+        """Releases the map (views returned by tensor_bytes() must be gone)."""
+        if self._buf is not None:
+            self._buf.release()
+            self._buf = None
+        if self._map is not None:
+            self._map.close()
+            self._map = None
         if self._file:
             self._file.close()
             self._file = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
