@@ -279,3 +279,22 @@ def test_model_loader_rounds_from_file(tmp_path):
     for name, _, frags in ts:
         assert rel_err(m.get(name).reconstruct(), O.spectral_reconstruct(frags)[0]) <= TOL
     r.close()
+
+
+@pytest.mark.gpu
+def test_turbo_decode_of_libzstd_level1_frames():
+    # the frames the reference writes (zstd level 1, turbo.rs:389-391),
+    # decoded by hh_turbo_tensor_decode
+    pa = pytest.importorskip("pyarrow")
+    import gpu_util as G
+    ts = list(tensors())
+    meta, data = {}, b""
+    for name, shape, frags in ts:
+        f = pa.Codec("zstd", compression_level=1).compress(H().hct3_container(frags), asbytes=True)
+        meta[name] = {"dtype": "hct_v3", "shape": shape, "data_offsets": [len(data), len(data) + len(f)]}
+        data += f
+    hdr = json.dumps(meta, separators=(",", ":")).encode()
+    r = T().TurboReader(struct.pack("<Q", len(hdr)) + hdr + data)
+    for name, shape, frags in ts:
+        got = r.decode_gpu(name, G.ctx()).cpu().numpy().ravel()
+        assert rel_err(got, O.spectral_reconstruct(frags)[0]) <= TOL
