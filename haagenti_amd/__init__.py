@@ -179,18 +179,33 @@ def lib():
     return _lib
 
 
+def _zstd_size_hint(b):
+    """Content size declared by the first frame header, or None."""
+    if len(b) < 6 or b[:4] != b"\x28\xb5\x2f\xfd":
+        return None
+    fhd = b[4]
+    fcs_flag, single, did = fhd >> 6, (fhd >> 5) & 1, fhd & 3
+    size = [1 if single else 0, 2, 4, 8][fcs_flag]
+    at = 5 + (0 if single else 1) + [0, 1, 2, 4][did]
+    if size == 0 or len(b) < at + size:
+        return None
+    v = int.from_bytes(b[at:at + size], "little")
+    return v + 256 if size == 2 else v
+
+
 def zstd_decompress(data):
     """zstd::decode_all (RFC 8878 frames) on the host (hh_zstd_decompress).
     Raises HaagentiError(CORRUPTED_DATA) on a malformed stream."""
     b = bytes(data)
     n = _sz(0)
-    rc = _lib.hh_zstd_decompress(b, len(b), None, 0, C.byref(n))
-    if rc == OK:
-        return b""
-    if rc != BUFFER_TOO_SMALL:
-        raise HaagentiError(rc, "zstd decode")
-    out = C.create_string_buffer(n.value)
-    _check(_lib.hh_zstd_decompress(b, len(b), out, n.value, C.byref(n)), "zstd decode")
+    hint = _zstd_size_hint(b)
+    cap = hint if hint is not None and hint <= 64 * len(b) + (1 << 20) else 8 * len(b) + (1 << 20)
+    out = C.create_string_buffer(max(cap, 1))
+    rc = _lib.hh_zstd_decompress(b, len(b), out, cap, C.byref(n))
+    if rc == BUFFER_TOO_SMALL:  # more than the hint (concatenated frames) or the estimate
+        out = C.create_string_buffer(n.value)
+        rc = _lib.hh_zstd_decompress(b, len(b), out, n.value, C.byref(n))
+    _check(rc, "zstd decode")
     return out.raw[:n.value]
 
 

@@ -14,6 +14,8 @@
 // Frames with a dictionary id are rejected (decode_all has no dictionary),
 // as are windows above 2^27 bytes (libzstd's default decoding limit).
 #include <cstdint>
+#include <cstddef>
+#include <climits>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -119,6 +121,10 @@ struct BackBits {
     }
     uint64_t get(int64_t start, int nb) const {  // bits [start, start + nb), nb <= 56
         if (nb == 0) return 0;
+        // the 8 bytes ending at the byte of the last bit hold all nb bits
+        const int64_t base = ((start + nb - 1) >> 3) - 7;
+        if (start >= 0 && base >= 0 && (size_t)base + 8 <= n)
+            return (ld64(p + base) >> (start - base * 8)) & ((1ull << nb) - 1);
         uint64_t v = 0;
         const int64_t first = start >> 3, last = (start + nb - 1) >> 3;
         for (int64_t b = last; b >= first; b--) v = (v << 8) | (b >= 0 && (size_t)b < n ? p[b] : 0u);
@@ -327,6 +333,44 @@ void huf_stream(const HufTable &H, const uint8_t *src, size_t len, uint8_t *out,
     if (br.pos != 0) throw Fail{};  // the stream is consumed exactly
 }
 
+// Up to four Huffman streams decoded in one loop, so that their symbol
+// chains (each read depends on the previous symbol's length) overlap; each
+// stream reads from a 64-bit window reloaded from memory while at least 7
+// bytes precede its read position, and through BackBits near its start.
+void huf_streams(const HufTable &H, int k, const uint8_t *const *src, const size_t *len, uint8_t *const *out,
+                 const size_t *n) {
+    BackBits br[4];
+    size_t nmin = SIZE_MAX;
+    for (int j = 0; j < k; j++) {
+        br[j].init(src[j], len[j]);
+        nmin = n[j] < nmin ? n[j] : nmin;
+    }
+    const int mb = H.maxbits;
+    const uint8_t *sym = H.sym.data(), *nbits = H.nbits.data();
+    size_t i = 0;
+    // all streams in step while each has >= 8 readable bytes below its position
+    for (; i < nmin; i++) {
+        bool fast = true;
+        for (int j = 0; j < k; j++) fast = fast && br[j].pos - mb >= 64;
+        if (!fast) break;
+        for (int j = 0; j < k; j++) {
+            const int64_t start = br[j].pos - mb;
+            const int64_t base = ((br[j].pos - 1) >> 3) - 7;
+            const uint32_t idx = (uint32_t)((ld64(br[j].p + base) >> (start - base * 8)) & ((1ull << mb) - 1));
+            out[j][i] = sym[idx];
+            br[j].pos -= nbits[idx];
+        }
+    }
+    for (int j = 0; j < k; j++) {
+        for (size_t q = i; q < n[j]; q++) {
+            const uint32_t idx = (uint32_t)br[j].peek(mb);
+            out[j][q] = sym[idx];
+            br[j].skip(nbits[idx]);
+        }
+        if (br[j].pos != 0) throw Fail{};
+    }
+}
+
 // ---------------------------------------------------------------- sequences
 const uint32_t kLLBase[36] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 18, 20, 22, 24, 28, 32, 40,
                               48, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768, 65536};
@@ -458,10 +502,11 @@ void decode_block(FrameState &F, const uint8_t *src, size_t len, std::vector<uin
             const size_t q = (regen + 3) / 4;
             if (3 * q > regen) throw Fail{};
             const uint8_t *d = c + 6;
-            huf_stream(F.huf, d, s1, lit.data(), q);
-            huf_stream(F.huf, d + s1, s2, lit.data() + q, q);
-            huf_stream(F.huf, d + s1 + s2, s3, lit.data() + 2 * q, q);
-            huf_stream(F.huf, d + s1 + s2 + s3, s4, lit.data() + 3 * q, regen - 3 * q);
+            const uint8_t *srcs[4] = {d, d + s1, d + s1 + s2, d + s1 + s2 + s3};
+            const size_t lens[4] = {s1, s2, s3, s4};
+            uint8_t *outs[4] = {lit.data(), lit.data() + q, lit.data() + 2 * q, lit.data() + 3 * q};
+            const size_t ns[4] = {q, q, q, regen - 3 * q};
+            huf_streams(F.huf, 4, srcs, lens, outs, ns);
         }
         p = hdr + comp;
     }
@@ -533,8 +578,13 @@ void decode_block(FrameState &F, const uint8_t *src, size_t len, std::vector<uin
         if (off > produced || off > F.window) throw Fail{};
         size_t from = out.size() - off;
         out.resize(out.size() + ml);
-        uint8_t *o = out.data();
-        for (uint64_t j = 0; j < ml; j++) o[out.size() - ml + j] = o[from + j];
+        uint8_t *o = out.data() + out.size() - ml;
+        const uint8_t *q = out.data() + from;
+        if (off >= ml) {
+            std::memcpy(o, q, ml);
+        } else {
+            for (uint64_t j = 0; j < ml; j++) o[j] = q[j];  // overlapping: byte order matters
+        }
         if (i + 1 < nseq) {
             sll = F.ll.t[sll].base + (uint32_t)br.read(F.ll.t[sll].nbits);
             sml = F.ml.t[sml].base + (uint32_t)br.read(F.ml.t[sml].nbits);
@@ -587,6 +637,11 @@ void decode_frames(const uint8_t *in, size_t len, std::vector<uint8_t> &out) {
         for (int i = 0; i < fcs_size; i++) fcs |= (uint64_t)in[p + i] << (8 * i);
         if (fcs_size == 2) fcs += 256;
         p += fcs_size;
+        // room for the declared content (bounded: the field is untrusted)
+        if (fcs_size) {
+            const uint64_t cap = 64ull * len + (1ull << 20);
+            out.reserve(out.size() + (size_t)(fcs < cap ? fcs : cap));
+        }
         if (single) window = fcs;
         if (!single && window > (1ull << 27)) throw Fail{};  // libzstd's default window limit
         F.window = window ? window : 1;
