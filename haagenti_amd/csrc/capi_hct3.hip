@@ -297,21 +297,25 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
     const uint64_t bm = (n + 7) / 8;
     if (24 + bm > l0) return corrupt(HH_CORRUPT_SIZE);  // "truncated bitmap"
     uint64_t cnt = 0;
-    for (uint64_t i = 0; i < bm; i++) {
-        uint32_t b = f0[24 + i];
-        if (i == bm - 1 && (n & 7)) b &= (1u << (n & 7)) - 1;  // bits past n are not scanned
-        cnt += (uint64_t)__builtin_popcount(b);
+    {
+        const uint8_t *bp = f0 + 24;
+        uint64_t i = 0;
+        for (; i + 8 <= bm; i += 8) {
+            uint64_t wv;
+            std::memcpy(&wv, bp + i, 8);
+            cnt += (uint64_t)__builtin_popcountll(wv);
+        }
+        for (; i < bm; i++) cnt += (uint64_t)__builtin_popcount((uint32_t)bp[i]);
+        if (n & 7) cnt -= (uint64_t)__builtin_popcount((uint32_t)bp[bm - 1] & ~((1u << (n & 7)) - 1) & 0xffu);
     }
     if (cnt != ntot) return corrupt(HH_CORRUPT_BITMAP_COUNT);  // compressive.rs:630-636
     // coefficients in index-map order; unset entries stay 0.0
     std::vector<uint8_t> coef((size_t)ntot * csz, 0);
-    size_t off = 24 + (size_t)bm;
-    for (uint32_t i = 0; i < ness; i++) {
-        if (off + csz > l0) return corrupt(HH_CORRUPT_SIZE);  // "truncated essential coefficients"
-        if (i >= ntot) return corrupt(HH_CORRUPT_SIZE);       // the reference indexes past its array
-        std::memcpy(&coef[(size_t)i * csz], f0 + off, csz);
-        off += csz;
-    }
+    const size_t off = 24 + (size_t)bm;
+    // "truncated essential coefficients", or more of them than retained
+    // positions (the reference indexes past its array): both a size error
+    if ((uint64_t)ness * csz > l0 - off || ness > ntot) return corrupt(HH_CORRUPT_SIZE);
+    if (ness) std::memcpy(coef.data(), f0 + off, (size_t)ness * csz);
     // add_detail (compressive.rs:653-700)
     for (uint32_t f = 1; f < nfrags; f++) {
         if (frag_index[f] == 0) continue;
@@ -322,12 +326,12 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
         const uint32_t count = rd32(d + 4);
         if (fi == 0) return corrupt(HH_CORRUPT_HEADER);  // start would underflow in the reference
         const uint64_t start = (uint64_t)ness + (uint64_t)(fi - 1) * dpf;
-        size_t o = 8;
-        for (uint32_t i = 0; i < count; i++) {
-            if (o + csz > l) break;
-            const uint64_t idx = start + i;
-            if (idx < ntot) std::memcpy(&coef[(size_t)idx * csz], d + o, csz);
-            o += csz;
+        // the values present (up to count), those at positions below ntot
+        uint64_t nv = (l - 8) / csz;
+        if (nv > count) nv = count;
+        if (start < ntot) {
+            const uint64_t m = nv < ntot - start ? nv : ntot - start;
+            if (m) std::memcpy(&coef[(size_t)start * csz], d + 8, (size_t)m * csz);
         }
     }
     if (n == 0) return HH_OK;
