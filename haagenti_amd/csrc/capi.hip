@@ -285,6 +285,19 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
                                            pick_stream(ctx, stream)));
 }
 
+int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
+                                 const uint32_t *d_in_len, uint8_t *d_scratch, const uint64_t *d_out_off,
+                                 const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
+                                 const hh_hctt_tensor *tensors, uint32_t ntensors, int32_t out_dtype,
+                                 void *stream) {
+    // both launches on the caller's stream: the tile decode reads the
+    // scratch after every block has been written
+    int32_t rc = hh_lz4_decompress_batch(ctx, d_in, in_total, d_in_off, d_in_len, d_scratch, d_out_off, d_out_cap,
+                                         nblocks, d_status, stream);
+    if (rc != HH_OK) return rc;
+    return hh_hctt_decode_batch(ctx, tensors, ntensors, out_dtype, stream);
+}
+
 int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len, uint32_t rows,
                        uint32_t cols, uint32_t k, int32_t out_dtype, void *d_out,
                        int32_t *d_tile_status, void *stream) {

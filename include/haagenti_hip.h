@@ -183,6 +183,22 @@ typedef struct hh_hctt_tensor {
 int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uint32_t n,
                              int32_t out_dtype, void *stream);
 
+/* LZ4-compressed HCT-T tiles of several tensors in one call: every block of
+ * d_in is decoded into d_scratch (hh_lz4_decompress_batch semantics, one
+ * status record per block in d_status), then the tensors, whose d_tiles point
+ * into d_scratch, are decoded (hh_hctt_decode_batch semantics); both launches
+ * are queued on `stream` with no host synchronization.  This is what
+ * HctReader::decompress_all (haagenti-hct/src/tensor.rs:417-515) followed by
+ * GpuDecompressor::decompress_batch_to_gpu (haagenti-cuda/src/decompress.rs:
+ * 282-293) does for one layer's tensors.  Tiles of a block that failed are
+ * decoded from undefined bytes: check d_status once the stream completes. */
+int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                 const uint64_t *d_in_off, const uint32_t *d_in_len,
+                                 uint8_t *d_scratch, const uint64_t *d_out_off,
+                                 const uint32_t *d_out_cap, uint32_t nblocks,
+                                 hh_block_status *d_status, const hh_hctt_tensor *tensors,
+                                 uint32_t ntensors, int32_t out_dtype, void *stream);
+
 /* Producer side on the host (threads = 0: all cores): per tile
  * dct_2d (dct.rs:282-308) -> top-k by |c| (compressive.rs:144-172) ->
  * quantize_int4 of the kept coefficients in ascending index order. */

@@ -1,0 +1,110 @@
+"""One decoder layer's LZ4-compressed HCT-T tensors in one call
+(hh_hctt_decode_lz4_batch: HctReader::decompress_all then
+GpuDecompressor::decompress_batch_to_gpu, crates/haagenti-hct/src/
+tensor.rs:417-515 and crates/haagenti-cuda/src/decompress.rs:282-293):
+bit-identical to the two batched calls it queues, within 1e-3 x RMS of the
+oracle's decode of the same tiles, LZ4 status records equal to the
+oracle's, and a corrupt block reported without disturbing the other
+tensors."""
+import numpy as np
+import pytest
+
+import gpu_util as G
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def H():
+    import haagenti_amd as h
+    return h
+
+
+def layer(seed=4):
+    """Three tensors with their own k, LZ4 blocks of 3 whole tiles."""
+    Hm = H()
+    rng = np.random.default_rng(seed)
+    blocks, tensors, spos = [], [], 0
+    for rows, cols, k in [(128, 192, 1228), (64, 256, 410), (192, 64, 2048)]:
+        w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+        tiles = Hm.hctt_encode(w, k)
+        tb = Hm.hctt_tile_bytes(k)
+        for s in range(0, tiles.size, 3 * tb):
+            chunk = tiles[s:s + 3 * tb].tobytes()
+            blocks.append((O.lz4_compress_block(chunk)[0], spos + s, len(chunk)))
+        tensors.append(dict(rows=rows, cols=cols, k=k, soff=spos, tiles=tiles))
+        spos += tiles.size
+    return blocks, tensors, spos
+
+
+def device_tables(blocks):
+    T = G.torch()
+    comp = b"".join(c for c, _, _ in blocks)
+    in_off = np.cumsum([0] + [len(c) for c, _, _ in blocks[:-1]]).astype(np.int64)
+    tabs = [G.dev(np.frombuffer(comp, np.uint8)), len(comp), T.from_numpy(in_off).cuda(),
+            T.from_numpy(np.array([len(c) for c, _, _ in blocks], np.int32)).cuda(),
+            T.from_numpy(np.array([o for _, o, _ in blocks], np.int64)).cuda(),
+            T.from_numpy(np.array([n for _, _, n in blocks], np.int32)).cuda()]
+    return comp, tabs
+
+
+def run(blocks, tensors, scratch_len, fused, dtype):
+    Hm = H()
+    T = G.torch()
+    comp, (d_in, in_total, d_off, d_len, d_oo, d_oc) = device_tables(blocks)
+    scratch = T.zeros(scratch_len, dtype=T.uint8, device="cuda")
+    status = T.zeros(len(blocks) * 32, dtype=T.uint8, device="cuda")
+    tdt = T.float32 if dtype == Hm.F32 else T.bfloat16
+    outs = [T.empty(t["rows"] * t["cols"], dtype=tdt, device="cuda") for t in tensors]
+    desc = [(scratch.data_ptr() + t["soff"], t["tiles"].size, t["rows"], t["cols"], t["k"], o)
+            for t, o in zip(tensors, outs)]
+    ctx = G.ctx()
+    if fused:
+        ctx.hctt_decode_lz4_batch(d_in, in_total, d_off, d_len, scratch, d_oo, d_oc, len(blocks), status, desc,
+                                  dtype=dtype, stream=G.stream())
+    else:
+        assert ctx.lz4_decompress_batch(d_in, in_total, d_off, d_len, scratch, d_oo, d_oc, len(blocks), status,
+                                        stream=G.stream()) == Hm.OK
+        ctx.hctt_decode_batch(desc, dtype=dtype, stream=G.stream())
+    G.sync()
+    codes = status.cpu().numpy().view(np.int32).reshape(-1, 8)
+    return [o.cpu() for o in outs], codes, scratch.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype_name", ["F32", "BF16"])
+def test_fused_layer_call_equals_two_calls_and_oracle(dtype_name):
+    Hm = H()
+    dtype = getattr(Hm, dtype_name)
+    blocks, tensors, slen = layer()
+    a, ca, sa = run(blocks, tensors, slen, True, dtype)
+    b, cb, sb = run(blocks, tensors, slen, False, dtype)
+    assert (ca[:, 0] == 0).all() and np.array_equal(ca, cb)
+    for t in tensors:
+        assert np.array_equal(sa[t["soff"]:t["soff"] + t["tiles"].size], t["tiles"])   # LZ4 bit-exact
+    for t, x, y in zip(tensors, a, b):
+        assert np.array_equal(x.view(G.torch().int16).numpy() if dtype == Hm.BF16 else x.numpy(),
+                              y.view(G.torch().int16).numpy() if dtype == Hm.BF16 else y.numpy())
+        rc, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+        assert rc == O.OK
+        got = x.float().numpy().reshape(t["rows"], t["cols"])
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        tol = TOL if dtype == Hm.F32 else 2 ** -7     # bf16: RNE of the f32 result
+        assert np.abs(got - ref).max() <= tol * (rms if dtype == Hm.F32 else np.abs(ref).max())
+
+
+def test_fused_layer_call_reports_a_corrupt_block():
+    Hm = H()
+    blocks, tensors, slen = layer(seed=9)
+    bad = 2                                   # the first block of the second tensor
+    c, o, n = blocks[bad]
+    blocks[bad] = (c[:len(c) // 2], o, n)     # truncated: the reference reports UnexpectedEof
+    outs, codes, _ = run(blocks, tensors, slen, True, Hm.F32)
+    for j, (cb, _, nb) in enumerate(blocks):
+        _, e = O.lz4_decompress_block(cb, nb)
+        assert codes[j, 0] == e.kind
+    assert codes[bad, 0] != Hm.OK and (np.delete(codes[:, 0], bad) == 0).all()
+    for t, x in zip([tensors[0], tensors[2]], [outs[0], outs[2]]):
+        _, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.abs(x.numpy().reshape(t["rows"], t["cols"]) - ref).max() <= TOL * rms
