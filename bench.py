@@ -742,13 +742,12 @@ def wl_stream(args, torch, H, O):
             copied[b].record(copy_stream)
             comp_stream.wait_event(copied[b])
             e = t_dec.start() if timed else None
-            rc = ctx.lz4_decompress_batch(d_in[b], nin, T["in_off"], T["in_len"], scratch,
-                                          T["out_off"], T["out_cap"], T["n"], status, stream=csp)
-            assert rc == H.OK
+            ctx.hctt_decode_lz4_batch(d_in[b], nin, T["in_off"], T["in_len"], scratch, T["out_off"],
+                                      T["out_cap"], T["n"], status,
+                                      [(scratch.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"], t["k"],
+                                        slot[b][i]) for i, t in enumerate(L["tensors"])],
+                                      dtype=H.BF16, stream=csp)
             consumed[b].record(comp_stream)
-            ctx.hctt_decode_batch([(scratch.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"],
-                                    t["k"], slot[b][i]) for i, t in enumerate(L["tensors"])],
-                                  dtype=H.BF16, stream=csp)
             if timed:
                 t_dec.stop(e)
 
