@@ -231,3 +231,37 @@ def test_encoder_gpu_dct_end_to_end():
     back = d.reconstruct_gpu()
     diff = back.cpu().numpy().astype(np.float64) - w.cpu().numpy().ravel()
     assert np.sqrt(np.mean(diff ** 2)) <= 1e-3 * 0.02
+
+
+def hct2_from_hct3(frags, rng):
+    """The same fragments in the f32 layout ("HCT2", compressive.rs:23,
+    470-500), values perturbed off the f16 grid so that the inverse DCT
+    takes the split path of arbitrary f32 input."""
+    f0 = frags[0][1]
+    magic, w, h, keep, ess, dpf = struct.unpack_from("<6I", f0)
+    bm = (w * h + 7) // 8
+    v0 = np.frombuffer(f0[24 + bm:24 + bm + 2 * ess], np.float16).astype(np.float32)
+    v0 = (v0 * (1 + rng.normal(0, 1e-3, v0.size))).astype(np.float32)
+    out = [(0, struct.pack("<6I", 0x48435432, w, h, keep, ess, dpf) + f0[24:24 + bm] + v0.tobytes())]
+    for idx, d in frags[1:]:
+        fi, tot, cnt = struct.unpack_from("<HHI", d)
+        v = np.frombuffer(d[8:8 + 2 * cnt], np.float16).astype(np.float32)
+        v = (v * (1 + rng.normal(0, 1e-3, v.size))).astype(np.float32)
+        out.append((idx, struct.pack("<HHI", fi, tot, cnt) + v.tobytes()))
+    return out
+
+
+def test_hct2_f32_fragments_vs_oracle():
+    Hm = H()
+    rng = np.random.default_rng(21)
+    x = sin_input(96 * 160, 0.003)
+    for w, h, nf, r in [(160, 96, 4, 0.3), (64, 64, 2, 1.0)]:
+        frags = hct2_from_hct3(encode(x[:w * h], w, h, nf, r), rng)
+        d = Hm.CompressiveSpectralDecoder(G.ctx())
+        d.add_essentials(frags[0])
+        for f in frags[1:]:
+            d.add_detail(f)
+        got = d.reconstruct()
+        ref, e, ww, hh = O.spectral_reconstruct(frags)
+        assert e.kind == O.OK and (ww, hh) == (w, h)
+        assert rel_err(got, ref) <= TOL
