@@ -217,3 +217,18 @@ def test_v2_block_checksum_detects_corruption_on_host():
     assert e.value.code == H.CORRUPTED_DATA
     e2, fb = O.hct_validate_v2(bytes(g))
     assert e2.sub == O.CORRUPT_BLOCK_CHECKSUM and fb == 0
+
+
+def test_import_without_the_hip_library_fails_loudly(tmp_path):
+    # the package has no CPU fallback: without libhaagenti_hip.so it refuses
+    # to import rather than decode on the host
+    import shutil
+    import subprocess
+    import sys
+    pkg = tmp_path / "haagenti_amd"
+    pkg.mkdir()
+    shutil.copy(H.__file__, pkg / "__init__.py")
+    r = subprocess.run([sys.executable, "-c", "import haagenti_amd"], cwd=tmp_path, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0
+    assert "ImportError" in r.stderr and "no CPU fallback" in r.stderr
