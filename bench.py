@@ -905,9 +905,9 @@ def main():
                          "(the reference HctWriter default is 16 KiB)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build "
-              "decodes on a single MI355X; see DESIGN.md for how the path would shard).",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the decode runs on "
+              "a single MI355X; across GPUs each would decode its own tensors or 64-aligned slabs, "
+              "with nothing exchanged).", file=sys.stderr)
         sys.exit(2)
     import torch
     import haagenti_amd as H
