@@ -741,6 +741,35 @@ class GpuDecompressor:
     def decompress_batch(self, tensors):
         return [self.decompress(c, s) for c, s in tensors]
 
+    def decompress_batch_pipelined(self, tensors):
+        """decompress_batch_pipelined (decompress.rs:228-279): every tensor's
+        coefficient matrix first (zstd unwrap, container parse and the
+        bitmap scatter: hh_hct3_coefficients), then every inverse DCT
+        (hh_idct_2d), with the reference's DecompressStats of the two
+        phases.  Returns ([flat float32 numpy arrays], stats dict)."""
+        import time
+        import torch
+        t0 = time.perf_counter()
+        stats = dict(num_tensors=len(tensors), total_input_bytes=0, total_output_bytes=0)
+        coefs = []
+        for compressed, shape in tensors:
+            w, h = _dims(shape)
+            stats["total_input_bytes"] += len(compressed)
+            stats["total_output_bytes"] += w * h * 4
+            coefs.append((self.reconstruct_coefficients_gpu(compressed, w * h), w, h))
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        outs = []
+        for c, w, h in coefs:
+            x = torch.empty(max(w * h, 1), dtype=torch.float32, device="cuda")
+            if w * h:
+                self.ctx.idct_2d(c, h, w, x)
+            outs.append(x[:w * h])
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        stats.update(parse_time_ms=(t1 - t0) * 1e3, idct_time_ms=(t2 - t1) * 1e3, total_time_ms=(t2 - t0) * 1e3)
+        return [o.cpu().numpy() for o in outs], stats
+
 
 class CompressiveSpectralDecoder:
     """CompressiveSpectralDecoder (compressive.rs:420-752): add_essentials()

@@ -265,3 +265,22 @@ def test_hct2_f32_fragments_vs_oracle():
         ref, e, ww, hh = O.spectral_reconstruct(frags)
         assert e.kind == O.OK and (ww, hh) == (w, h)
         assert rel_err(got, ref) <= TOL
+
+
+def test_decompress_batch_pipelined_matches_decompress():
+    # decompress.rs:228-279: same results as one tensor at a time, with the
+    # phase statistics the reference reports
+    rng = np.random.default_rng(23)
+    shapes = [(64, 96), (40, 40), (1, 500)]
+    items = []
+    for shp in shapes:
+        total = int(np.prod(shp))
+        items.append((container([random_fragment(rng, total, 0.3)]), shp))
+    d = dec()
+    outs, stats = d.decompress_batch_pipelined(items)
+    assert stats["num_tensors"] == 3 and stats["total_output_bytes"] == 4 * sum(int(np.prod(s)) for s in shapes)
+    assert stats["total_input_bytes"] == sum(len(c) for c, _ in items)
+    assert stats["total_time_ms"] >= stats["parse_time_ms"] >= 0 and stats["idct_time_ms"] >= 0
+    for (c, shp), o in zip(items, outs):
+        assert rel_err(o, dec().decompress(c, shp)) <= 1e-5
+        assert rel_err(o, O.hct3_decode(c, shp)[1]) <= TOL
