@@ -627,7 +627,7 @@ def wl_hct3(args, torch, H, O):
     roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
             "kernel": ("rocBLAS f16 gemm_ex x5, split f16 operands, f32 accumulation (+ bitmap scatter, "
-                       "split, scale and bf16 passes)") if split else
+                       "split and scale-to-bf16 passes)") if split else
                       "rocBLAS sgemm x2 (+ bitmap scatter, bf16 conversion)",
             "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
             "mfma_type": "f16" if split else "fp32",

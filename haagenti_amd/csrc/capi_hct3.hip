@@ -154,9 +154,11 @@ int32_t inverse_to(hh_context *ctx, float *d_dense, float *d_tmp, uint32_t rows,
                    int32_t dtype, void *d_out, hipStream_t s, bool f16_exact) {
     const uint64_t total = (uint64_t)rows * cols;
     float *x = dtype == HH_F32 ? reinterpret_cast<float *>(d_out) : d_dense;
-    int32_t rc = hh::dct2d_full(ctx, true, d_dense, d_tmp, x, rows, cols, s, f16_exact);
+    bool converted = false;
+    int32_t rc = hh::dct2d_full(ctx, true, d_dense, d_tmp, x, rows, cols, s, f16_exact, dtype,
+                                dtype == HH_F32 ? nullptr : d_out, &converted);
     if (rc != HH_OK) return rc;
-    if (dtype != HH_F32) return from_hip(hh::launch_f32_convert(x, total, dtype, d_out, s));
+    if (dtype != HH_F32 && !converted) return from_hip(hh::launch_f32_convert(x, total, dtype, d_out, s));
     return HH_OK;
 }
 

@@ -268,6 +268,17 @@ __global__ __launch_bounds__(256) void scale_kernel(float *__restrict__ x, uint6
     if (i < n) x[i] *= scale[0];
 }
 
+// out = 16-bit RNE of x * *scale (the scale is a power of two: exact)
+__global__ __launch_bounds__(256) void scale_convert_kernel(const float *__restrict__ x, uint64_t n,
+                                                            const float *__restrict__ scale, int dtype,
+                                                            void *__restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i] * scale[0];
+    uint16_t *o = reinterpret_cast<uint16_t *>(out);
+    o[i] = (uint16_t)(dtype == HH_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+}
+
 }  // namespace
 
 hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t *d_block_sums,
@@ -384,7 +395,7 @@ static int32_t blas_status(rocblas_status st) {
 // X = B_h^T C B_w on the f16 MFMA (see the header): d_tmp holds T in f32.
 static int32_t idct_split(hh_context *ctx, rocblas_handle h, const float *d_in, float *d_tmp, float *d_out,
                           uint32_t rows, uint32_t cols, const float *bw, const float *bh, hipStream_t s,
-                          bool f16_exact) {
+                          bool f16_exact, int32_t cvt_dtype, void *cvt_out) {
     const uint64_t total = (uint64_t)rows * cols;
     const _Float16 *bw_hi, *bw_lo, *bh_hi, *bh_lo;
     int32_t rc = basis_split_for(ctx, cols, bw, s, &bw_hi, &bw_lo);
@@ -446,13 +457,19 @@ static int32_t idct_split(hh_context *ctx, rocblas_handle h, const float *d_in, 
     if (st == rocblas_status_success) st = gemm(N, T, n, k1, ohi, m, bh_lo, n, k1, d_out);
     if (st == rocblas_status_success) st = gemm(N, T, n, k1, olo, m, bh_hi, n, k1, d_out);
     if (st != rocblas_status_success) return blas_status(st);
-    hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
-                       (const float *)(consts + 3));
+    if (cvt_out)
+        hipLaunchKernelGGL(scale_convert_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
+                           (const float *)(consts + 3), (int)cvt_dtype, cvt_out);
+    else
+        hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
+                           (const float *)(consts + 3));
     return from_hip(hipGetLastError());
 }
 
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
-                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact) {
+                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact, int32_t cvt_dtype,
+                   void *cvt_out, bool *converted) {
+    if (converted) *converted = false;
     if (rows == 0 || cols == 0) return HH_OK;
     const float *bw = nullptr, *bh = nullptr;
     int32_t rc = basis_for(ctx, cols, s, &bw);
@@ -472,7 +489,10 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
     //             C^T = T^T B_h^T     (m = w, n = h, k = h)
     const int m = (int)cols, n = (int)rows;
     const char *f32env = std::getenv("HH_DCT_F32");
-    if (inverse && !(f32env && f32env[0] == '1')) return idct_split(ctx, h, d_in, d_tmp, d_out, rows, cols, bw, bh, s, f16_exact);
+    if (inverse && !(f32env && f32env[0] == '1')) {
+        if (converted) *converted = cvt_out != nullptr;
+        return idct_split(ctx, h, d_in, d_tmp, d_out, rows, cols, bw, bh, s, f16_exact, cvt_dtype, cvt_out);
+    }
     rocblas_status st = rocblas_sgemm(h, inverse ? rocblas_operation_none : rocblas_operation_transpose,
                                       rocblas_operation_none, m, n, m, &one, bw, m, d_in, m, &zero,
                                       d_tmp, m);

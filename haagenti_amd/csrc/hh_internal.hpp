@@ -121,8 +121,11 @@ hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_o
 // rows x cols f32 matrix: two GEMMs through d_tmp (rows*cols f32); d_out may
 // not alias d_in or d_tmp.  f16_exact: every input value is an f16 value
 // (the inverse then skips the GEMM pass of the input's low f16 half).
+// cvt_out: a 16-bit output (cvt_dtype) the inverse may write directly from
+// its last pass, reported in *converted (d_out then holds an intermediate).
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
-                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact = false);
+                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact = false,
+                   int32_t cvt_dtype = HH_F32, void *cvt_out = nullptr, bool *converted = nullptr);
 void release_dct_resources(hh_context *ctx);
 // zstd::decode_all on the host (host_zstd.cpp): false on a malformed stream.
 bool zstd_decode_all(const uint8_t *in, size_t len, std::vector<uint8_t> &out);
