@@ -127,7 +127,8 @@ int32_t hh_context_create(int32_t device, hh_context **out) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
         return HH_ERR_DEVICE_NOT_FOUND;
-    hipError_t e = hipSetDevice(device);
+    hh::DeviceGuard guard(device);
+    hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     hh_context *ctx = new hh_context();
     ctx->device = device;
@@ -157,7 +158,7 @@ int32_t hh_context_create(int32_t device, hh_context **out) {
 
 void hh_context_destroy(hh_context *ctx) {
     if (!ctx) return;
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     if (ctx->d_basis) hipFree(ctx->d_basis);
     if (ctx->d_scratch) hipFree(ctx->d_scratch);
@@ -183,7 +184,8 @@ int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_
     if (nblocks == 0) return HH_OK;
     if (!d_in || !d_in_off || !d_in_len || !d_out || !d_out_off || !d_out_cap || !d_status)
         return HH_ERR_INVALID_ARGUMENT;
-    hipError_t e = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     return from_hip(hh::launch_lz4_batch(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
                                          d_out_cap, nblocks, d_status, pick_stream(ctx, stream)));
@@ -193,7 +195,8 @@ int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, 
                              size_t out_cap, size_t *written, hh_block_status *status) {
     if (!ctx || (!in && in_len) || (!out && out_cap)) return HH_ERR_INVALID_ARGUMENT;
     if (in_len > 0xffffffffu || out_cap > 0xffffffffu) return HH_ERR_UNSUPPORTED;
-    hipError_t e = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     // scratch layout: [status 32][in_off 8][in_len 4 pad 4][out_off 8][out_cap 4 pad 4][in][out]
     const size_t hdr = 64;
@@ -247,7 +250,8 @@ int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_
     if (produced) *produced = m;
     if (m == 0) return HH_OK;
     if (!d_q || !d_out || ((uintptr_t)d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
-    hipError_t e = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     return from_hip(hh::launch_dequant_int4(d_q, m, groups, out_dtype, d_out, ctx->num_cus,
                                             pick_stream(ctx, stream)));
@@ -279,7 +283,8 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
     }
     if (total == 0) return HH_OK;
     if (total > 0xffffffffu) return HH_ERR_UNSUPPORTED;
-    hipError_t e = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     return from_hip(hh::launch_hctt_decode(tensors, n, out_dtype, ctx->d_basis, ctx->num_cus,
                                            pick_stream(ctx, stream)));
@@ -409,7 +414,8 @@ int32_t hct_blocks(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file
     // blocks that are decoded: the readable ones, less a last block of
     // inconsistent size
     const uint32_t md = decode ? (size_fail && m == n ? n - 1 : m) : 0;
-    hipError_t he = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t he = guard.status();
     if (he != hipSuccess) return from_hip(he);
     hipStream_t s = pick_stream(ctx, stream);
     const bool direct = nominal <= out_cap;
@@ -541,7 +547,8 @@ int32_t hh_xxh3_64_batch(hh_context *ctx, const uint8_t *d_data, size_t data_len
     if (!ctx) return HH_ERR_INVALID_ARGUMENT;
     if (n == 0) return HH_OK;
     if (!d_data || !d_off || !d_len || !d_out) return HH_ERR_INVALID_ARGUMENT;
-    hipError_t e = hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    hipError_t e = guard.status();
     if (e == hipSuccess) e = hh::launch_xxh3_batch(d_data, data_len, d_off, d_len, n, d_out, pick_stream(ctx, stream));
     return from_hip(e);
 }

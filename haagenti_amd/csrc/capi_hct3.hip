@@ -199,7 +199,8 @@ int32_t hh_hct3_coefficients(hh_context *ctx, const uint8_t *data, size_t len, u
     if (rc != HH_OK || total == 0) return rc;
     uint32_t mc = 0;
     for (const Layer &L : layers) mc = std::max(mc, L.ncoef);
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     rc = ensure_scratch(ctx, stage_bytes(total, mc, 0));
     if (rc != HH_OK) return rc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -223,7 +224,8 @@ int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, con
     if (!d_out) return HH_ERR_INVALID_ARGUMENT;
     uint32_t mc = 0;
     for (const Layer &L : layers) mc = std::max(mc, L.ncoef);
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     const size_t mat = align16((size_t)total * sizeof(float));
     rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, mc, 0));
     if (rc != HH_OK) return rc;
@@ -253,7 +255,8 @@ int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const 
     rc = parse_container(h_data, len, total, layers);
     if (rc != HH_OK || total == 0) return rc;
     if (!d_out) return HH_ERR_INVALID_ARGUMENT;
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     const size_t mat = align16((size_t)total * sizeof(float));
     rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, 0, 0));
     if (rc != HH_OK) return rc;
@@ -346,7 +349,8 @@ int32_t hh_spectral_reconstruct(hh_context *ctx, const uint8_t *const *frags, co
         return HH_ERR_BUFFER_TOO_SMALL;
     }
     // reconstruct (compressive.rs:728-752): one scatter with fragment 0's bitmap
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     const size_t mat = align16((size_t)n * sizeof(float));
     int32_t rc = ensure_scratch(ctx, 2 * mat + stage_bytes(n, ntot, f32c));
     if (rc != HH_OK) return rc;
@@ -430,7 +434,8 @@ int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t c
     const uint64_t total = (uint64_t)rows * cols;
     if (total == 0) return HH_OK;
     if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     const size_t mat = align16((size_t)total * sizeof(float));
     int32_t rc = ensure_scratch(ctx, out_dtype == HH_F32 ? mat : 2 * mat);
     if (rc != HH_OK) return rc;
@@ -449,7 +454,8 @@ int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t co
     const uint64_t total = (uint64_t)rows * cols;
     if (total == 0) return HH_OK;
     if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
-    hipSetDevice(ctx->device);
+    hh::DeviceGuard guard(ctx->device);
+    if (guard.status() != hipSuccess) return from_hip(guard.status());
     int32_t rc = ensure_scratch(ctx, align16((size_t)total * sizeof(float)));
     if (rc != HH_OK) return rc;
     return hh::dct2d_full(ctx, false, d_in, reinterpret_cast<float *>(ctx->d_scratch), d_out, rows, cols,

@@ -514,12 +514,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 
 hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dtype,
                               const void *d_basis, int num_cus, hipStream_t s) {
-    for (uint32_t first = 0; first < n; first += kMaxTensors) {
+    // each launch takes the next (up to) kMaxTensors non-empty tensors
+    for (uint32_t i = 0; i < n;) {
         TileBatch B;
         std::memset(&B, 0, sizeof(B));
         uint32_t max_k = 0, total = 0;
         bool all_dw = true;
-        for (uint32_t i = first; i < n && B.n < (uint32_t)kMaxTensors; i++) {
+        for (; i < n && B.n < (uint32_t)kMaxTensors; i++) {
             const hh_hctt_tensor &T = tensors[i];
             const uint32_t nt = (T.rows / 64) * (T.cols / 64);
             if (nt == 0) continue;

@@ -42,6 +42,33 @@ namespace hh {
 int32_t from_hip(hipError_t e);
 int32_t ensure_scratch(hh_context *ctx, size_t bytes);
 
+// Makes a device current for the lifetime of the guard and restores the
+// calling thread's previous current device afterwards, so an entry point
+// leaves the caller's device selection as it found it.  `status` is the
+// result of the switch (hipSuccess when nothing needed to change).
+class DeviceGuard {
+  public:
+    explicit DeviceGuard(int device) {
+        int cur = -1;
+        status_ = hipGetDevice(&cur);
+        if (status_ != hipSuccess) return;
+        if (cur != device) {
+            status_ = hipSetDevice(device);
+            if (status_ == hipSuccess) prev_ = cur;
+        }
+    }
+    ~DeviceGuard() {
+        if (prev_ >= 0) (void)hipSetDevice(prev_);
+    }
+    DeviceGuard(const DeviceGuard &) = delete;
+    DeviceGuard &operator=(const DeviceGuard &) = delete;
+    hipError_t status() const { return status_; }
+
+  private:
+    hipError_t status_ = hipSuccess;
+    int prev_ = -1;
+};
+
 // ---- device helpers -------------------------------------------------------
 
 // f16 bit pattern -> f32, exact for every code, NaN payload kept
@@ -64,6 +91,24 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
         bits = sign | ((113u - lz) << 23) | (f << 13);
     }
     return __uint_as_float(bits);
+}
+
+// Zero-fills out[0, cap) from one wavefront (every lane calls it with its
+// lane index): the output range of an LZ4 block whose decode failed, so no
+// byte of an earlier use of the buffer survives there (a tile whose bitmap
+// reads as zeros then fails its popcount check instead of decoding stale
+// bytes).  Stores of the same wave to the same address land in order, so
+// this overrides whatever the decoder wrote before the failure.
+__device__ __forceinline__ void wave_zero_fill(uint8_t *out, uint32_t cap, int lane) {
+    typedef uint32_t u32x4z __attribute__((ext_vector_type(4)));
+    uint32_t head = (uint32_t)((16u - ((uintptr_t)out & 15u)) & 15u);
+    if (head > cap) head = cap;
+    if ((uint32_t)lane < head) out[lane] = 0;
+    uint8_t *body = out + head;
+    const uint32_t nch = (cap - head) >> 4, tail = (cap - head) & 15u;
+    for (uint32_t c = (uint32_t)lane; c < nch; c += 64)
+        reinterpret_cast<u32x4z *>(body)[c] = u32x4z{0u, 0u, 0u, 0u};
+    if ((uint32_t)lane < tail) body[16u * nch + (uint32_t)lane] = 0;
 }
 
 // f32 -> bf16 round-to-nearest-even; NaN stays a (quiet) NaN.

@@ -8,10 +8,14 @@
 //            top-k by |c| with a stable order (compressive.rs:144-172),
 //            quantize_int4 of the kept values in ascending index order.
 //
-// The tile DCT is evaluated as f64 basis products rounded to f32 (the
-// reference evaluates an f32 FFT); coefficients agree to ~1e-7 relative,
-// so near-ties in the top-k selection can resolve differently.  Decoding is
-// defined on the bytes, which both sides then share.
+// The tile DCT is the reference's f32 computation: dct_1d's Makhoul form
+// (dct.rs:79-129; an n-point complex FFT of the even/odd-reordered input,
+// then a quarter-wave twiddle) over the rows, then over the columns
+// (dct_2d, dct.rs:282-308).  The 64-point FFT is an iterative radix-2
+// decimation in time whose twiddles are cos/sin of the f64 angle rounded to
+// f32 (rustfft's twiddle tables are made the same way); host code built
+// without FMA contraction, so the coefficient bits, and with them the top-k
+// selection, are fixed by this order of operations.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -163,43 +167,83 @@ size_t quantize(const float *w, size_t n, uint8_t *out) {
 
 // ------------------------------------------------------------------ HCT-T
 
-struct TileBasis {
-    double m[64][64];  // m[k][i] = a_k cos(pi k (2i+1) / 128)
-    TileBasis() {
-        const double pi = 3.14159265358979323846;
-        for (int k = 0; k < 64; k++)
-            for (int i = 0; i < 64; i++)
-                m[k][i] = (k == 0 ? std::sqrt(1.0 / 64) : std::sqrt(2.0 / 64)) *
-                          std::cos(pi * k * (2 * i + 1) / 128.0);
+// 64-point forward DCT-II (orthonormal) in f32, Makhoul's method.
+class TileDct {
+  public:
+    TileDct() {
+        for (int i = 0, j = 0; i < 64; i++) {  // bit-reversal permutation
+            rev_[i] = (uint8_t)j;
+            int bit = 32;
+            for (; j & bit; bit >>= 1) j ^= bit;
+            j ^= bit;
+        }
+        for (int k = 0; k <= 32; k++) {
+            const double a = -2.0 * 3.14159265358979323846 * (double)k / 64.0;
+            wr_[k] = (float)std::cos(a);
+            wi_[k] = (float)std::sin(a);
+        }
+        const float pi = 3.14159265358979323846f;
+        for (int k = 0; k < 64; k++) {
+            const float angle = -pi * (float)k / (2.0f * 64.0f);
+            cr_[k] = std::cos(angle);
+            ci_[k] = std::sin(angle);
+        }
+        scale_ = std::sqrt(2.0f / 64.0f);
     }
+
+    // out[k] = a_k sum_i in[i * stride] cos(pi k (2i + 1) / 128)
+    void operator()(const float *in, size_t stride, float *out) const {
+        float re[64], im[64], xr[64];
+        // v = [x0, x2, ..., x62, x63, x61, ..., x1]
+        for (int k = 0; k < 32; k++) {
+            xr[k] = in[(size_t)(2 * k) * stride];
+            xr[63 - k] = in[(size_t)(2 * k + 1) * stride];
+        }
+        for (int i = 0; i < 64; i++) {
+            re[rev_[i]] = xr[i];
+            im[rev_[i]] = 0.0f;
+        }
+        for (int len = 2, step = 32; len <= 64; len <<= 1, step >>= 1) {
+            const int half = len >> 1;
+            for (int i = 0; i < 64; i += len)
+                for (int k = 0; k < half; k++) {
+                    const float w_r = wr_[k * step], w_i = wi_[k * step];
+                    const int a = i + k, b = i + k + half;
+                    const float br = re[b] * w_r - im[b] * w_i;
+                    const float bi = re[b] * w_i + im[b] * w_r;
+                    const float ar = re[a], ai = im[a];
+                    re[a] = ar + br;
+                    im[a] = ai + bi;
+                    re[b] = ar - br;
+                    im[b] = ai - bi;
+                }
+        }
+        for (int k = 0; k < 64; k++) out[k] = (re[k] * cr_[k] - im[k] * ci_[k]) * scale_;
+        out[0] /= 1.41421356237309504880f;
+    }
+
+  private:
+    uint8_t rev_[64];
+    float wr_[33], wi_[33], cr_[64], ci_[64];
+    float scale_;
 };
 
-const TileBasis &basis() {
-    static const TileBasis b;
-    return b;
+const TileDct &tile_dct() {
+    static const TileDct d;
+    return d;
 }
 
 void encode_tile(const float *w, size_t ld, uint32_t k, uint8_t *out) {
-    const TileBasis &B = basis();
-    double t[64][64], c64[64][64];
-    // rows: t[i][v] = sum_j x[i][j] m[v][j]
-    for (int i = 0; i < 64; i++)
-        for (int v = 0; v < 64; v++) {
-            double acc = 0;
-            for (int j = 0; j < 64; j++) acc += (double)w[i * ld + j] * B.m[v][j];
-            t[i][v] = acc;
-        }
-    // columns: c[u][v] = sum_i m[u][i] t[i][v]
-    for (int u = 0; u < 64; u++)
-        for (int v = 0; v < 64; v++) {
-            double acc = 0;
-            for (int i = 0; i < 64; i++) acc += B.m[u][i] * t[i][v];
-            c64[u][v] = acc;
-        }
-    float c[4096];
+    const TileDct &dct = tile_dct();
+    float t[4096], c[4096];
+    for (int i = 0; i < 64; i++) dct(w + (size_t)i * ld, 1, t + 64 * i);  // rows
+    float col[64];
+    for (int v = 0; v < 64; v++) {  // then columns
+        dct(t + v, 64, col);
+        for (int u = 0; u < 64; u++) c[64 * u + v] = col[u];
+    }
     float mag[4096];
     for (int i = 0; i < 4096; i++) {
-        c[i] = (float)c64[i >> 6][i & 63];
         const float a = std::fabs(c[i]);
         mag[i] = a != a ? -1.0f : a;  // NaN ranks last
     }

@@ -333,6 +333,11 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
             op += (uint32_t)ml;
         }
     }
+    // a failed block's output reads as zeros (the reference returns no output)
+    if (code != HH_OK) {
+        wave_fence();
+        wave_zero_fill(out, cap, lane);
+    }
     if (lane == 0) {
         hh_block_status st;
         st.code = code;

@@ -519,6 +519,11 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
         }
         if (code == HH_OK) d.flush(true);
     }
+    // a failed block's output reads as zeros (the reference returns no output)
+    if (code != HH_OK) {
+        d.mem_sync();
+        wave_zero_fill(out, d.cap, lane);
+    }
     if (lane == 0) {
         hh_block_status st;
         st.code = code;

@@ -15,7 +15,9 @@
  * GpuDctContext / GpuContext (crates/haagenti-cuda/src/lib.rs:99-108).
  * Device entry points are asynchronous on the given stream; results are
  * valid after that stream is synchronised.  Host-pointer entry points are
- * synchronous.
+ * synchronous.  Every entry point makes the context's device current while
+ * it runs and restores the calling thread's current device before it
+ * returns.
  *
  * Errors: every entry returns an hh_status.  Kernels additionally write
  * per-block / per-tile status records (first error wins inside a block).
@@ -101,7 +103,9 @@ int32_t hh_context_synchronize(hh_context *ctx);
  * output_size of decompress_block (haagenti-lz4/src/block.rs:261-366).
  * in_total bounds every input read (size of the d_in allocation).
  * d_status[i] receives the block's result; a stream that ends early is
- * success with written < cap, as in the reference.
+ * success with written < cap, as in the reference.  A block that fails
+ * leaves its whole output range [d_out_off[i], +d_out_cap[i]) zeroed (the
+ * reference returns an error and no output).
  * Replaces NativeKernels::decompress_lz4_native
  * (crates/haagenti-cuda/src/native_kernels.rs:623-657) and
  * GpuContext::decompress_lz4 (lib.rs:173-197). */
@@ -190,8 +194,10 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
  * are queued on `stream` with no host synchronization.  This is what
  * HctReader::decompress_all (haagenti-hct/src/tensor.rs:417-515) followed by
  * GpuDecompressor::decompress_batch_to_gpu (haagenti-cuda/src/decompress.rs:
- * 282-293) does for one layer's tensors.  Tiles of a block that failed are
- * decoded from undefined bytes: check d_status once the stream completes. */
+ * 282-293) does for one layer's tensors.  A block that fails leaves its
+ * range of d_scratch zeroed, so every tile it covers fails the bitmap count
+ * (tile status HH_ERR_CORRUPTED_DATA, output zeros) whatever the scratch held
+ * before; d_status names the block once the stream completes. */
 int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
                                  const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  uint8_t *d_scratch, const uint64_t *d_out_off,

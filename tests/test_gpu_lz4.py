@@ -241,3 +241,74 @@ def test_lengths_beyond_32_bits():
     outs, st = check_against_oracle(streams, [1 << 20] * 4)
     assert [r["code"] for r in st] == [O.UNEXPECTED_EOF, O.BUFFER_TOO_SMALL] * 2
     assert [st[1]["required"], st[3]["required"]] == want
+
+
+def _reference_decompress(data):
+    """Lz4Decompressor::decompress (crates/haagenti-lz4/src/decompress.rs:33-57)
+    on the oracle: 4x the input first, max(required, 2x) on BufferTooSmall,
+    a 256 MiB limit.  Returns (bytes or None, error kind, attempts).  Note
+    that decompress_block only stops early when the output reaches the size
+    it is given, so a stream that ends with literals and decodes to less
+    than that size runs on into a missing match offset (UnexpectedEof): the
+    size-unknown call succeeds only for streams ending with a match."""
+    size, tries = len(data) * 4, 0
+    while True:
+        tries += 1
+        out, e = O.lz4_decompress_block(data, size)
+        if e.kind == O.OK:
+            return out, O.OK, tries
+        if e.kind != O.BUFFER_TOO_SMALL:
+            return None, e.kind, tries
+        size = max(int(e.required), size * 2)
+        if size > 256 * 1024 * 1024:
+            return None, O.CORRUPTED, tries
+
+
+def _gpu_decompress(d, c):
+    import haagenti_amd as H
+    try:
+        return d.decompress(c), O.OK
+    except H.HaagentiError as e:
+        return None, e.code
+
+
+def test_decompressor_size_unknown_grows_like_the_reference():
+    import haagenti_amd as H
+    d = H.Lz4Decompressor(G.ctx())
+    rng = np.random.default_rng(8)
+    # streams ending with a match: one literal then an offset-1 match
+    ends_with_match = [bytes([0x1F]) + b"a" + b"\x01\x00" + b"\xff" * n + b"\x07" for n in (0, 3, 400)]
+    # two sequences, the second ending with a periodic match of period 3
+    ends_with_match.append(bytes([0x3F]) + b"xyz" + b"\x03\x00" + b"\xff" * 50 + b"\x00")
+    cases = [(s, True) for s in ends_with_match]
+    for src in [b"", rng.integers(0, 4, 5000, dtype=np.uint8).tobytes(), bytes(200000)]:
+        cases.append((O.lz4_compress_block(src)[0], False))
+    cases.append((b"", True))                    # no input: an empty output
+    for c, ok in cases:
+        ref, kind, tries = _reference_decompress(c)
+        assert (kind == O.OK) == ok, (c[:8], kind)
+        got, gkind = _gpu_decompress(d, c)
+        assert gkind == kind and got == ref
+        if ok and len(c) > 10:
+            assert tries >= 2        # the 4x estimate was short
+        # decompress_with_size at the true size succeeds for every stream
+        if ref is not None:
+            assert d.decompress_with_size(c, len(ref)) == ref
+    src = bytes(200000)
+    c = O.lz4_compress_block(src)[0]
+    assert d.decompress_with_size(c, len(src)) == src
+    assert _reference_decompress(c)[2] == 3      # grew twice, then ran past the last literals
+
+
+def test_decompressor_size_unknown_limit():
+    # one literal, then an offset-1 match longer than 256 MiB: the first
+    # attempt (4x the input) reports the required size, which exceeds the
+    # limit -> CorruptedData("decompressed size exceeds limit")
+    import haagenti_amd as H
+    nrun = (1 << 28) // 255 + 1
+    c = bytes([0x1F]) + b"a" + b"\x01\x00" + b"\xff" * nrun + b"\x00"
+    ref, kind, tries = _reference_decompress(c)
+    assert ref is None and kind == O.CORRUPTED and tries == 1
+    with pytest.raises(H.HaagentiError) as ei:
+        H.Lz4Decompressor(G.ctx()).decompress(c)
+    assert ei.value.code == H.CORRUPTED_DATA
