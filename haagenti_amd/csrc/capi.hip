@@ -187,8 +187,10 @@ int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_
     hh::DeviceGuard guard(ctx->device);
     hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
-    return from_hip(hh::launch_lz4_batch(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
-                                         d_out_cap, nblocks, d_status, pick_stream(ctx, stream)));
+    // the caller's output buffer has no stated size: its block table is trusted
+    const hh::Lz4Batch B = {d_in,      in_total,  d_in_off, d_in_len, d_out, ~0ull,
+                            d_out_off, d_out_cap, nblocks,  d_status};
+    return from_hip(hh::launch_lz4_batch(B, pick_stream(ctx, stream)));
 }
 
 int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, uint8_t *out,
@@ -215,11 +217,17 @@ int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, 
     if (e == hipSuccess && in_len)
         e = hipMemcpyAsync(base + in_at, in, in_len, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return from_hip(e);
-    e = hh::launch_lz4_batch(base + in_at, in_len, reinterpret_cast<uint64_t *>(base + 32),
-                             reinterpret_cast<uint32_t *>(base + 40), base + out_at,
-                             reinterpret_cast<uint64_t *>(base + 48),
-                             reinterpret_cast<uint32_t *>(base + 56), 1,
-                             reinterpret_cast<hh_block_status *>(base), s);
+    const hh::Lz4Batch B = {base + in_at,
+                            in_len,
+                            reinterpret_cast<uint64_t *>(base + 32),
+                            reinterpret_cast<uint32_t *>(base + 40),
+                            base + out_at,
+                            out_cap,
+                            reinterpret_cast<uint64_t *>(base + 48),
+                            reinterpret_cast<uint32_t *>(base + 56),
+                            1,
+                            reinterpret_cast<hh_block_status *>(base)};
+    e = hh::launch_lz4_batch(B, s);
     if (e != hipSuccess) return from_hip(e);
     hh_block_status st;
     e = hipMemcpyAsync(&st, base, sizeof(st), hipMemcpyDeviceToHost, s);
@@ -448,9 +456,9 @@ int32_t hct_blocks(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file
                 he = hipMemcpyAsync(d_out_off, out_off.data(), 8 * (size_t)md, hipMemcpyHostToDevice, s);
             if (he == hipSuccess)
                 he = hipMemcpyAsync(d_cap, expect.data(), 4 * (size_t)md, hipMemcpyHostToDevice, s);
-            if (he == hipSuccess)
-                he = hh::launch_lz4_batch(d_file, file_len, d_in_off, d_in_len, dst, d_out_off, d_cap, md,
-                                          d_st, s);
+            const hh::Lz4Batch B = {d_file,    file_len, d_in_off, d_in_len, dst, direct ? out_cap : nominal,
+                                    d_out_off, d_cap,    md,       d_st};
+            if (he == hipSuccess) he = hh::launch_lz4_batch(B, s);
             if (he == hipSuccess)
                 he = hipMemcpyAsync(st.data(), d_st, 32 * (size_t)md, hipMemcpyDeviceToHost, s);
         }

@@ -129,18 +129,29 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 hipError_t launch_dequant_int4(const uint8_t *d_q, size_t n, size_t nscale_groups,
                                int dtype, void *d_out, int num_cus, hipStream_t s);
 
+// One batched LZ4 decode: block i reads in[in_off[i], +in_len[i]) (ranges
+// outside [0, in_total) are reported as HH_ERR_INVALID_ARGUMENT) and writes
+// at most out_cap[i] bytes at out + out_off[i]; a block whose output range
+// leaves [0, out_total) is reported the same way and writes nothing.
+struct Lz4Batch {
+    const uint8_t *in;
+    uint64_t in_total;
+    const uint64_t *in_off;
+    const uint32_t *in_len;
+    uint8_t *out;
+    uint64_t out_total;
+    const uint64_t *out_off;
+    const uint32_t *out_cap;
+    uint32_t nblocks;
+    hh_block_status *status;
+};
+
 // Batched LZ4: dispatches to the LDS-ring decoder (lz4_ring.hip) or, when
 // the environment sets HH_LZ4_KERNEL=window, to the register-window decoder
 // (lz4_decode.hip).  The ring is 4 KiB with a 4 KiB input stage;
 // HH_LZ4_KERNEL=ring8 / ring16 / ring32 select an 8 / 16 / 32 KiB ring.
-hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                            const uint32_t *d_in_len, uint8_t *d_out,
-                            const uint64_t *d_out_off, const uint32_t *d_out_cap,
-                            uint32_t nblocks, hh_block_status *d_status, hipStream_t s);
-hipError_t launch_lz4_ring(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                           const uint32_t *d_in_len, uint8_t *d_out, const uint64_t *d_out_off,
-                           const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
-                           uint32_t ring_kib, hipStream_t s);
+hipError_t launch_lz4_batch(const Lz4Batch &B, hipStream_t s);
+hipError_t launch_lz4_ring(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s);
 
 hipError_t launch_xxh3_batch(const uint8_t *d_data, size_t data_len, const uint64_t *d_off,
                              const uint32_t *d_len, uint32_t n, uint64_t *d_out, hipStream_t s);

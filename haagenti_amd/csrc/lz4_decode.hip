@@ -239,25 +239,25 @@ struct Window {
     }
 };
 
-__global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
-    const uint8_t *__restrict__ d_in, uint64_t in_total, const uint64_t *__restrict__ in_off,
-    const uint32_t *__restrict__ in_len, uint8_t *__restrict__ d_out,
-    const uint64_t *__restrict__ out_off, const uint32_t *__restrict__ out_cap, uint32_t nblocks,
-    hh_block_status *__restrict__ status) {
+__global__ __launch_bounds__(kThreads) void lz4_batch_kernel(Lz4Batch B) {
     const int lane = threadIdx.x & 63;
     const uint32_t b = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (b >= nblocks) return;
+    if (b >= B.nblocks) return;
+    const uint8_t *__restrict__ d_in = B.in;
+    const uint64_t in_total = B.in_total;
 
     int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
     uint64_t pos = 0, req = 0;
     uint32_t op = 0;
 
-    const uint64_t ioff = in_off[b];
-    const uint32_t ilen = in_len[b];
-    uint8_t *out = d_out + out_off[b];
-    const uint32_t cap = out_cap[b];
+    const uint64_t ioff = B.in_off[b];
+    const uint32_t ilen = B.in_len[b];
+    const uint64_t oofs = B.out_off[b];
+    const uint32_t cap = B.out_cap[b];
+    const bool out_ok = oofs <= B.out_total && (uint64_t)cap <= B.out_total - oofs;
+    uint8_t *out = B.out + oofs;
 
-    if (ioff > in_total || (uint64_t)ilen > in_total - ioff) {
+    if (ioff > in_total || (uint64_t)ilen > in_total - ioff || !out_ok) {
         code = HH_ERR_INVALID_ARGUMENT;
     } else {
         const uint8_t *__restrict__ glo = d_in;
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
         }
     }
     // a failed block's output reads as zeros (the reference returns no output)
-    if (code != HH_OK) {
+    if (code != HH_OK && out_ok) {
         wave_fence();
         wave_zero_fill(out, cap, lane);
     }
@@ -345,30 +345,24 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(
         st.position = pos;
         st.required = req;
         st.written = code == HH_OK ? op : 0;
-        status[b] = st;
+        B.status[b] = st;
     }
 }
 
 }  // namespace
 
-hipError_t launch_lz4_batch(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                            const uint32_t *d_in_len, uint8_t *d_out, const uint64_t *d_out_off,
-                            const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
-                            hipStream_t s) {
-    if (nblocks == 0) return hipSuccess;
+hipError_t launch_lz4_batch(const Lz4Batch &B, hipStream_t s) {
+    if (B.nblocks == 0) return hipSuccess;
     const char *k = std::getenv("HH_LZ4_KERNEL");
     if (k == nullptr || std::strcmp(k, "window") != 0) {
         uint32_t kib = 4u;
         if (k != nullptr && std::strcmp(k, "ring8") == 0) kib = 8u;
         if (k != nullptr && std::strcmp(k, "ring16") == 0) kib = 16u;
         if (k != nullptr && std::strcmp(k, "ring32") == 0) kib = 32u;
-        return launch_lz4_ring(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,
-                               d_status, kib, s);
+        return launch_lz4_ring(B, kib, s);
     }
-    const uint32_t grid = (nblocks + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL(lz4_batch_kernel, dim3(grid), dim3(kThreads), 0, s, d_in,
-                       (uint64_t)in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,
-                       d_status);
+    const uint32_t grid = (B.nblocks + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL(lz4_batch_kernel, dim3(grid), dim3(kThreads), 0, s, B);
     return hipGetLastError();
 }
 

@@ -329,31 +329,31 @@ struct RingDec {
 };
 
 template <uint32_t R, uint32_t S>
-__global__ __launch_bounds__(64) void lz4_ring_kernel(
-    const uint8_t *__restrict__ d_in, uint64_t in_total, const uint64_t *__restrict__ in_off,
-    const uint32_t *__restrict__ in_len, uint8_t *d_out, const uint64_t *__restrict__ out_off,
-    const uint32_t *__restrict__ out_cap, uint32_t nblocks, hh_block_status *__restrict__ status) {
+__global__ __launch_bounds__(64) void lz4_ring_kernel(Lz4Batch B) {
     using D = RingDec<R, S>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x;
     const uint32_t b = blockIdx.x;
-    if (b >= nblocks) return;
+    if (b >= B.nblocks) return;
 
     int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
     uint64_t pos = 0, req = 0;
 
-    const uint64_t ioff = in_off[b];
-    const uint32_t ilen = in_len[b];
-    uint8_t *out = d_out + out_off[b];
+    const uint64_t ioff = B.in_off[b];
+    const uint32_t ilen = B.in_len[b];
+    const uint64_t oofs = B.out_off[b];
+    const uint32_t ocap = B.out_cap[b];
+    const bool out_ok = oofs <= B.out_total && (uint64_t)ocap <= B.out_total - oofs;
+    uint8_t *out = B.out + oofs;
     D d;
     d.ring = smem;
     d.stage = smem + R + D::kSFront;
-    d.gbuf = d_in;
-    d.gsz = in_total;
+    d.gbuf = B.in;
+    d.gsz = B.in_total;
     d.ioff = ioff;
     d.a0 = (uint32_t)((uintptr_t)out & 15u);
     d.obase = out - d.a0;
-    d.cap = out_cap[b];
+    d.cap = ocap;
     d.sb = 0;
     d.at_end = false;
     d.wso = kNoWin;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
     d.fl = 0;
     d.lane = lane;
 
-    if (ioff > in_total || (uint64_t)ilen > in_total - ioff) {
+    if (ioff > B.in_total || (uint64_t)ilen > B.in_total - ioff || !out_ok) {
         code = HH_ERR_INVALID_ARGUMENT;
     } else {
         const uint32_t end = ilen;
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
         if (code == HH_OK) d.flush(true);
     }
     // a failed block's output reads as zeros (the reference returns no output)
-    if (code != HH_OK) {
+    if (code != HH_OK && out_ok) {
         d.mem_sync();
         wave_zero_fill(out, d.cap, lane);
     }
@@ -531,41 +531,29 @@ __global__ __launch_bounds__(64) void lz4_ring_kernel(
         st.position = pos;
         st.required = req;
         st.written = code == HH_OK ? d.op : 0;
-        status[b] = st;
+        B.status[b] = st;
     }
 }
 
 template <uint32_t R, uint32_t S>
-hipError_t launch_ring(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                       const uint32_t *d_in_len, uint8_t *d_out, const uint64_t *d_out_off,
-                       const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
-                       hipStream_t s) {
+hipError_t launch_ring(const Lz4Batch &B, hipStream_t s) {
     constexpr uint32_t lds = RingDec<R, S>::kLds;
     hipError_t e = hipFuncSetAttribute((const void *)lz4_ring_kernel<R, S>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((lz4_ring_kernel<R, S>), dim3(nblocks), dim3(64), lds, s, d_in,
-                       (uint64_t)in_total, d_in_off, d_in_len, d_out, d_out_off, d_out_cap, nblocks,
-                       d_status);
+    hipLaunchKernelGGL((lz4_ring_kernel<R, S>), dim3(B.nblocks), dim3(64), lds, s, B);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_lz4_ring(const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                           const uint32_t *d_in_len, uint8_t *d_out, const uint64_t *d_out_off,
-                           const uint32_t *d_out_cap, uint32_t nblocks, hh_block_status *d_status,
-                           uint32_t ring_kib, hipStream_t s) {
-    if (nblocks == 0) return hipSuccess;
+hipError_t launch_lz4_ring(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s) {
+    if (B.nblocks == 0) return hipSuccess;
     switch (ring_kib) {
-        case 8: return launch_ring<8192, 2048>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
-                                               d_out_cap, nblocks, d_status, s);
-        case 16: return launch_ring<16384, 3072>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
-                                                 d_out_cap, nblocks, d_status, s);
-        case 32: return launch_ring<32768, 4096>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
-                                                 d_out_cap, nblocks, d_status, s);
-        default: return launch_ring<4096, 4096>(d_in, in_total, d_in_off, d_in_len, d_out, d_out_off,
-                                                d_out_cap, nblocks, d_status, s);
+        case 8: return launch_ring<8192, 2048>(B, s);
+        case 16: return launch_ring<16384, 3072>(B, s);
+        case 32: return launch_ring<32768, 4096>(B, s);
+        default: return launch_ring<4096, 4096>(B, s);
     }
 }
 
