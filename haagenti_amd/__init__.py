@@ -105,6 +105,9 @@ class HcttTensor(C.Structure):
 _sig("hh_hctt_decode_batch", _i32, [_vp, C.POINTER(HcttTensor), _u32, _i32, _vp])
 _sig("hh_hctt_decode_lz4_batch", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _u32, _vp, C.POINTER(HcttTensor), _u32,
                                         _i32, _vp])
+_sig("hh_hctt_decode_lz4_batch_noalloc", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _u32, _vp, C.POINTER(HcttTensor),
+                                                _u32, _i32, _vp])
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class HctInfo(C.Structure):
@@ -158,7 +161,8 @@ EXPORTS = [
     "hh_lz4_decompress_batch", "hh_lz4_decompress_to", "hh_lz4_compress_block",
     "hh_lz4_max_compressed_size", "hh_dequant_int4", "hh_quantize_int4",
     "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
-    "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_decode_lz4_batch", "hh_hctt_encode",
+    "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_decode_lz4_batch", "hh_hctt_decode_lz4_batch_noalloc",
+    "hh_hctt_encode",
     "hh_hct_read_header", "hh_hct_decompress_all",
     "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
     "hh_hct_validate_checksums", "hh_hct3_coefficients", "hh_hct3_decompress", "hh_hct3_decompress_device",
@@ -340,6 +344,20 @@ class HipContext:
             self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), _addr(d_scratch),
             _addr(d_out_off), _addr(d_out_cap), int(nblocks), _addr(d_status), arr, len(tensors), int(dtype),
             stream), "hh_hctt_decode_lz4_batch")
+
+    def hctt_decode_lz4_batch_noalloc(self, d_in, in_total, d_in_off, d_in_len, d_out_off, d_out_cap,
+                                      nblocks, d_status, tensors, dtype=F32, stream=None):
+        """hh_hctt_decode_lz4_batch_noalloc: as hctt_decode_lz4_batch with the
+        tile bytes in the library's own device array; tensors are (tiles_len,
+        rows, cols, k, d_out[, d_status]), packed in order in that array, and
+        d_out_off are offsets into it.  Returns the status code."""
+        arr = (HcttTensor * max(len(tensors), 1))()
+        for i, t in enumerate(tensors):
+            st = t[5] if len(t) > 5 else None
+            arr[i] = HcttTensor(None, int(t[0]), int(t[1]), int(t[2]), int(t[3]), _addr(t[4]), _addr(st))
+        return _lib.hh_hctt_decode_lz4_batch_noalloc(
+            self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), _addr(d_out_off),
+            _addr(d_out_cap), int(nblocks), _addr(d_status), arr, len(tensors), int(dtype), stream)
 
     # ---------------------------------------------------------- host API
     def lz4_decompress_to(self, data, out_cap):

@@ -139,6 +139,9 @@ int32_t hh_context_create(int32_t device, hh_context **out) {
         return from_hip(e);
     }
     ctx->num_cus = prop.multiProcessorCount;
+    // set-up of hh_hctt_decode_lz4_batch_noalloc (its failure is reported
+    // by that entry point, not here)
+    ctx->noalloc_status = hh::noalloc_scratch(device, &ctx->noalloc_scratch);
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete ctx;

@@ -33,6 +33,11 @@ struct hh_context {
     // f16 split operands of the whole-matrix inverse DCT (grown on demand)
     void *d_split = nullptr;
     size_t split_bytes = 0;
+    // Device address of the library-owned tile-byte array of
+    // hh_hctt_decode_lz4_batch_noalloc on this context's device, looked up
+    // at context creation (capi_noalloc.hip), and the lookup's result.
+    uint8_t *noalloc_scratch = nullptr;
+    hipError_t noalloc_status = hipErrorNotInitialized;
 };
 
 namespace hh {
@@ -41,6 +46,9 @@ namespace hh {
 // (capi.hip).
 int32_t from_hip(hipError_t e);
 int32_t ensure_scratch(hh_context *ctx, size_t bytes);
+// Device address of the no-allocation entry point's array on `device`
+// (which must be current), looked up once per device (capi_noalloc.hip).
+hipError_t noalloc_scratch(int device, uint8_t **out);
 
 // Makes a device current for the lifetime of the guard and restores the
 // calling thread's previous current device afterwards, so an entry point

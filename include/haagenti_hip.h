@@ -205,6 +205,31 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
                                  hh_block_status *d_status, const hh_hctt_tensor *tensors,
                                  uint32_t ntensors, int32_t out_dtype, void *stream);
 
+/* Size of the tile-byte array hh_hctt_decode_lz4_batch_noalloc uses: 64 MiB
+ * (a Llama-3-8B layer's tiles at 30 % retention take 64,110,592 bytes). */
+#define HH_NOALLOC_SCRATCH_BYTES (64ull << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  hh_hctt_decode_lz4_batch with the LZ4 output held in a
+ * device array the library owns (HH_NOALLOC_SCRATCH_BYTES per GPU, held
+ * until the process ends) instead of a caller's d_scratch; it allocates
+ * nothing.  Every tensors[i].d_tiles must be NULL: the tensors' tiles are
+ * packed in order from the array's start (tensor i's at byte offset
+ * sum_{j<i} tiles_len_j), and d_out_off are offsets into the array.  More
+ * than HH_NOALLOC_SCRATCH_BYTES of tiles_len in total is
+ * HH_ERR_BUFFER_TOO_SMALL (nothing is launched); a block whose output range
+ * leaves the packed tiles gets HH_ERR_INVALID_ARGUMENT in d_status and
+ * writes nothing.  All calls on one GPU share its array and it keeps the
+ * last call's bytes: calls that overlap on one GPU race, and tile bytes no
+ * block covers hold an earlier call's data. */
+int32_t hh_hctt_decode_lz4_batch_noalloc(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                         const uint64_t *d_in_off, const uint32_t *d_in_len,
+                                         const uint64_t *d_out_off, const uint32_t *d_out_cap,
+                                         uint32_t nblocks, hh_block_status *d_status,
+                                         const hh_hctt_tensor *tensors, uint32_t ntensors,
+                                         int32_t out_dtype, void *stream);
+
 /* Producer side on the host (threads = 0: all cores): per tile
  * dct_2d (dct.rs:282-308) -> top-k by |c| (compressive.rs:144-172) ->
  * quantize_int4 of the kept coefficients in ascending index order. */
