@@ -659,6 +659,10 @@ def write_layer_files(H, L, shapes, d):
 
 
 def wl_stream(args, torch, H, O):
+    """Config 5 through the product pipeline (hh_pipeline_*: pinned staging,
+    copy stream + compute stream ordered by events, double-buffered output
+    slot), one seeded 70B layer encoding streamed --stream-layers times."""
+    import haagenti_amd.pipeline as P
     rng = np.random.default_rng(70)
     rhos = rng.uniform(0.10, 0.50, len(L70B))
     ks = [H.hctt_retain_count(float(r)) for r in rhos]
@@ -669,16 +673,23 @@ def wl_stream(args, torch, H, O):
     log(f"encoded one 70B layer in {time.time() - t0:.1f}s: {L['blob'].size / 1e6:.1f} MB "
         f"compressed, {L['scratch_bytes'] / 1e6:.1f} MB tile bytes; k = {ks}")
     ctx = H.HipContext(0)
-    comp_stream = torch.cuda.current_stream()
-    copy_stream = torch.cuda.Stream()
-    csp, ysp = comp_stream.cuda_stream, copy_stream.cuda_stream
-    host = torch.from_numpy(L["blob"].copy()).pin_memory()
-    nin = host.numel()
-    files, maps, pool, host_b = None, [], None, None
+    nin = int(L["blob"].size)
+    nb = int(L["in_off"].size)
+    cfg = P.default_config()
+    cfg.num_staging_buffers = 2
+    cfg.max_blocks = nb
+    cfg.staging_buffer_size = nin + 24 * nb + 256
+    cfg.tile_scratch_size = L["scratch_bytes"]
+    pool = P.MemoryPool(ctx, 2 * cfg.staging_buffer_size + cfg.tile_scratch_size + (16 << 20))
+    pipe = P.DecompressionPipeline(ctx, pool, cfg)
+    # compressed layer in pinned host memory (copied to the device from there)
+    host = P.PinnedBuffer(nin)
+    host.copy_from_host(L["blob"])
+    files, maps, rpool = None, [], None
     if args.from_file:
         # the layer as HCT v2 files, memory-mapped; each layer's payloads are
-        # copied from the maps into one of two pinned staging buffers (by
-        # host threads) while the other buffer's H2D copy and decode run
+        # read by host threads straight into the pipeline's next staging
+        # buffer while the previous layers copy and decode
         import concurrent.futures as cf
         import mmap
         import tempfile
@@ -692,100 +703,93 @@ def wl_stream(args, torch, H, O):
             start = r.data_offset()
             assert mm[start:start + nbytes] == L["blob"][first:first + nbytes].tobytes()
             maps.append((f, mm, start, first, nbytes))
-        host_b = [torch.empty(nin, dtype=torch.uint8).pin_memory() for _ in range(2)]
-        pool = cf.ThreadPoolExecutor(max_workers=8)
+        rpool = cf.ThreadPoolExecutor(max_workers=8)
         log(f"wrote {len(files)} HCT v2 files ({sum(x[2] for x in files) / 1e6:.1f} MB of blocks) to {d}")
 
-    def read_layer(b):
-        dst = host_b[b].numpy()
+    def read_layer(dst):
         jobs = []
         for _, mm, start, first, nbytes in maps:
             step = 8 << 20
             for o in range(0, nbytes, step):
                 n = min(step, nbytes - o)
-                jobs.append(pool.submit(np.copyto, dst[first + o:first + o + n],
-                                        np.frombuffer(mm, np.uint8, n, start + o)))
+                jobs.append(rpool.submit(np.copyto, dst[first + o:first + o + n],
+                                         np.frombuffer(mm, np.uint8, n, start + o)))
         for j in jobs:
             j.result()
-    d_in = [torch.empty(nin, dtype=torch.uint8, device="cuda") for _ in range(2)]
-    scratch = torch.empty(L["scratch_bytes"], dtype=torch.uint8, device="cuda")
-    slot = [[torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L70B]
-            for _ in range(2)]
-    T = dict(in_off=devtab(torch, L["in_off"]), in_len=devtab(torch, L["in_len"]),
-             out_off=devtab(torch, L["out_off"]), out_cap=devtab(torch, L["out_cap"]),
-             n=L["in_off"].size)
-    status = torch.zeros(T["n"] * 32, dtype=torch.uint8, device="cuda")
-    copied = [torch.cuda.Event() for _ in range(2)]
-    consumed = [torch.cuda.Event() for _ in range(2)]
-    t_dec, t_h2d = (Timed(torch, comp_stream, args.stream_layers),
-                    Timed(torch, copy_stream, args.stream_layers))
-    torch.cuda.synchronize()
 
+    slot = [[torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L70B] for _ in range(2)]
+    tabs = (L["in_off"], L["in_len"], L["out_off"], L["out_cap"])
     read_s = [0.0]
 
     def run(nlayers, timed):
+        tickets = []
         for l in range(nlayers):
-            b = l % 2
-            src = host
+            src = host.as_slice()
             if args.from_file:
-                copied[b].synchronize()              # layer l - 2's H2D has read host_b[b]
                 r0 = time.perf_counter()
-                read_layer(b)
+                st = pipe.next_staging()
+                read_layer(st)
                 read_s[0] += time.perf_counter() - r0 if timed else 0.0
-                src = host_b[b]
-            copy_stream.wait_event(consumed[b])      # layer l - 2 has finished reading d_in[b]
-            e = t_h2d.start() if timed else None
-            with torch.cuda.stream(copy_stream):
-                d_in[b].copy_(src, non_blocking=True)
-            if timed:
-                t_h2d.stop(e)
-            copied[b].record(copy_stream)
-            comp_stream.wait_event(copied[b])
-            e = t_dec.start() if timed else None
-            ctx.hctt_decode_lz4_batch(d_in[b], nin, T["in_off"], T["in_len"], scratch, T["out_off"],
-                                      T["out_cap"], T["n"], status,
-                                      [(scratch.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"], t["k"],
-                                        slot[b][i]) for i, t in enumerate(L["tensors"])],
-                                      dtype=H.BF16, stream=csp)
-            consumed[b].record(comp_stream)
-            if timed:
-                t_dec.stop(e)
+                src = st[:nin]
+            desc = [(t["tlen"], t["rows"], t["cols"], t["k"], slot[l % 2][i]) for i, t in enumerate(L["tensors"])]
+            tickets.append(pipe.submit(src, *tabs, tensors=desc, dtype=H.BF16))
+        return tickets
 
-    run(2, False)                            # correctness pass (checked below)
+    tk = run(2, False)                        # correctness pass (checked below)
+    for t in tk:
+        pipe.wait(t)                          # raises on any failed block
+    check = None
+    if O is not None:
+        T0 = L["tensors"][1]                  # k (1024 x 8192), first rows
+        sub = 256
+        tb = H.hctt_tile_bytes(T0["k"])
+        comp, kinds, _ = O.lz4_decompress_batch(L["blob"], L["in_off"], L["in_len"], L["out_off"], L["out_cap"],
+                                                L["scratch_bytes"], nthreads=cpu_threads())
+        rc, ref = O.hctt_decode_tensor(comp[T0["soff"]:T0["soff"] + (sub // 64) * (T0["cols"] // 64) * tb], sub,
+                                       T0["cols"], T0["k"])
+        got = slot[1][1].view(T0["rows"], T0["cols"])[:sub].float().cpu().numpy()
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        check = float(np.abs(got - ref).max() / rms)
+        assert (kinds == 0).all()
+        del comp
+        log(f"spot check layer 1 / k rows 0..{sub}: max|bf16 - oracle f32| = {check:.2e} x RMS")
+    for _ in range(max(1, args.warmup // 10)):
+        for t in run(2, False):
+            pipe.wait(t)
+    pipe.finish()
+    pipe.reset_stats()
     torch.cuda.synchronize()
-    codes = status.cpu().numpy().view(np.int32)[0::8]
-    assert (codes == 0).all()
-    warm(lambda: run(2, False), args)
-    ta, tz = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ta.record(comp_stream)
-    copy_stream.wait_event(ta)
     w0 = time.perf_counter()
-    run(args.stream_layers, True)
-    tz.record(comp_stream)
-    torch.cuda.synchronize()
+    tk = run(args.stream_layers, True)
+    times = [pipe.times(t) for t in tk]
+    pipe.finish()
     wall = time.perf_counter() - w0
-    e2e_s = ta.elapsed_time(tz) / 1e3
-    dec_s, h2d_s = t_dec.mean_s(), t_h2d.mean_s()
+    st = pipe.stats()
+    e2e_ms = times[-1].decode_end_ms - times[0].h2d_start_ms
+    dec_s = st.decompress_time_ns / st.units / 1e9
+    h2d_s = st.transfer_time_ns / st.units / 1e9
     value = out_layer / dec_s / 1e9
-    e2e = out_layer * args.stream_layers / e2e_s / 1e9
+    e2e = out_layer * args.stream_layers / (e2e_ms / 1e3) / 1e9
     h2d_gbs = nin / h2d_s / 1e9
-    # fraction of the shorter stage hidden under the longer one
-    per_layer = e2e_s / args.stream_layers
-    overlap = max(0.0, min(1.0, (dec_s + h2d_s - per_layer) / min(dec_s, h2d_s)))
+    # copy of layer l + 1 under the decode of layer l, from the event times
+    hidden = [max(0.0, min(times[l + 1].h2d_end_ms, times[l].decode_end_ms) -
+                  max(times[l + 1].h2d_start_ms, times[l].decode_start_ms)) /
+              (times[l].decode_end_ms - times[l].decode_start_ms) for l in range(len(times) - 1)]
+    overlap = float(np.mean(hidden))
     file_info = None
     if args.from_file:
         file_info = {"files": len(files), "host_read_gbs": round(nin * args.stream_layers / read_s[0] / 1e9, 2),
-                     "source": "HCT v2 files (mmap, page cache) -> pinned staging -> H2D"}
+                     "source": "HCT v2 files (mmap, page cache) -> pinned staging (in place) -> H2D"}
         log(f"from files: host reads {file_info['host_read_gbs']} GB/s")
         for f, mm, *_ in maps:
             mm.close()
             f.close()
-        pool.shutdown()
+        rpool.shutdown()
         import shutil
         shutil.rmtree(os.path.dirname(files[0][0]), ignore_errors=True)
     log(f"per layer: decode {dec_s * 1e3:.2f} ms ({value:.0f} GB/s out), H2D {h2d_s * 1e3:.2f} ms "
-        f"({h2d_gbs:.1f} GB/s), end to end {e2e_s / args.stream_layers * 1e3:.2f} ms/layer "
-        f"({e2e:.0f} GB/s out); wall {wall:.2f}s")
+        f"({h2d_gbs:.1f} GB/s), end to end {e2e_ms / args.stream_layers:.2f} ms/layer "
+        f"({e2e:.0f} GB/s out); decode hidden under the next copy: {overlap:.3f}; wall {wall:.2f}s")
     cpu = None
     if not args.no_cpu and O is not None:
         reps, secs, ne = cpu_layer_decode(O, L, args.cpu_budget, max_reps=3, tensor_subset=[1, 2])
@@ -793,21 +797,27 @@ def wl_stream(args, torch, H, O):
                "kind": "port",
                "sample": f"{reps} x LZ4 of the whole 70B layer + tile decode of its k and v tensors "
                          f"({ne} elements), {cpu_threads()} threads, {secs:.1f} s"}
-    return line("llama70b-stream", value, e2e_s / args.stream_layers * 1e3, args,
-                "f16-split-mfma/f32",
-                "synthetic (one seeded 70B layer encoding streamed %d times)" % args.stream_layers,
-                {"layers": args.stream_layers, "elements_per_layer": n_elem,
-                 "rho": [round(float(r), 4) for r in rhos], "k": ks,
-                 "compressed_bytes_per_layer": int(nin), "out_dtype": "bf16",
-                 "source": file_info["source"] if file_info else "pinned host memory",
-                 "value_is": "decode-only (inputs in HBM)"},
-                roofline("llama70b-stream", "lz4_ring_kernel + hctt_decode_kernel<bf16>",
-                         L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
-                cpu,
-                {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
-                 "decode_ms_per_layer": round(dec_s * 1e3, 3),
-                 "h2d_ms_per_layer": round(h2d_s * 1e3, 3),
-                 "overlap_fraction": round(overlap, 3), "from_file": file_info})
+    res = line("llama70b-stream", value, e2e_ms / args.stream_layers, args,
+               "f16-split-mfma/f32",
+               "synthetic (one seeded 70B layer encoding streamed %d times)" % args.stream_layers,
+               {"layers": args.stream_layers, "elements_per_layer": n_elem,
+                "rho": [round(float(r), 4) for r in rhos], "k": ks,
+                "compressed_bytes_per_layer": nin, "out_dtype": "bf16",
+                "source": file_info["source"] if file_info else "pinned host memory (hh_pinned_alloc)",
+                "value_is": "decode-only (events around LZ4 + tile decode on the pipeline's compute stream)",
+                "runtime": "hh_pipeline_* (copy stream + compute stream, 2 staging slots)"},
+               roofline("llama70b-stream", "lz4_ring_kernel + hctt_decode_kernel<bf16>",
+                        L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
+               cpu,
+               {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
+                "decode_ms_per_layer": round(dec_s * 1e3, 3),
+                "h2d_ms_per_layer": round(h2d_s * 1e3, 3),
+                "overlap_fraction": round(overlap, 3), "from_file": file_info,
+                "spot_check_max_err_over_rms": check})
+    pipe.close()
+    pool.close()
+    host.close()
+    return res
 
 
 def wl_copy(args, torch, H, O):

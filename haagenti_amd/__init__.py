@@ -110,6 +110,53 @@ _sig("hh_hctt_decode_lz4_batch_noalloc", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _v
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
+class PoolStats(C.Structure):
+    """hh_pool_stats: PoolStats (crates/haagenti-cuda/src/memory.rs:341-347)."""
+    _fields_ = [("total_size", C.c_uint64), ("allocated", C.c_uint64), ("available", C.c_uint64),
+                ("free_buffers", C.c_uint64), ("free_buffer_bytes", C.c_uint64), ("largest_free", C.c_uint64)]
+
+
+class PipelineConfig(C.Structure):
+    """hh_pipeline_config: PipelineConfig (crates/haagenti-cuda/src/pipeline.rs:35-60)."""
+    _fields_ = [("num_staging_buffers", _u32), ("max_blocks", _u32), ("staging_buffer_size", C.c_uint64),
+                ("tile_scratch_size", C.c_uint64), ("use_pinned_memory", _u32), ("copy_threads", _u32)]
+
+
+class PipelineStats(C.Structure):
+    """hh_pipeline_stats: PipelineStats (pipeline.rs:121-128)."""
+    _fields_ = [("blocks_processed", C.c_uint64), ("bytes_read", C.c_uint64), ("bytes_decompressed", C.c_uint64),
+                ("transfer_time_ns", C.c_uint64), ("decompress_time_ns", C.c_uint64), ("units", C.c_uint64),
+                ("bytes_output", C.c_uint64)]
+
+
+class PipelineTimes(C.Structure):
+    """hh_pipeline_times: a unit's copy and decode intervals (ms since creation)."""
+    _fields_ = [("h2d_start_ms", C.c_double), ("h2d_end_ms", C.c_double), ("decode_start_ms", C.c_double),
+                ("decode_end_ms", C.c_double)]
+
+
+_sig("hh_pinned_alloc", _i32, [_sz, C.POINTER(_vp)])
+_sig("hh_pinned_free", _i32, [_vp])
+_sig("hh_pool_create", _i32, [_vp, _sz, C.POINTER(_vp)])
+_sig("hh_pool_destroy", None, [_vp])
+_sig("hh_pool_allocate", _i32, [_vp, _sz, _i32, C.POINTER(_vp)])
+_sig("hh_pool_recycle", _i32, [_vp, _vp])
+_sig("hh_pool_get_stats", _i32, [_vp, C.POINTER(PoolStats)])
+_sig("hh_pipeline_default_config", None, [C.POINTER(PipelineConfig)])
+_sig("hh_pipeline_create", _i32, [_vp, _vp, C.POINTER(PipelineConfig), C.POINTER(_vp)])
+_sig("hh_pipeline_destroy", None, [_vp])
+_sig("hh_pipeline_streams", _i32, [_vp, C.POINTER(_vp), C.POINTER(_vp)])
+_sig("hh_pipeline_next_staging", _i32, [_vp, C.POINTER(_vp), C.POINTER(_sz)])
+_sig("hh_pipeline_submit", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _u32, _vp, C.c_uint64,
+                                  C.POINTER(HcttTensor), _u32, _i32, _vp, C.POINTER(C.c_uint64)])
+_sig("hh_pipeline_wait", _i32, [_vp, C.c_uint64, _vp, C.POINTER(C.c_int64)])
+_sig("hh_pipeline_stream_wait", _i32, [_vp, C.c_uint64, _vp])
+_sig("hh_pipeline_get_times", _i32, [_vp, C.c_uint64, C.POINTER(PipelineTimes)])
+_sig("hh_pipeline_finish", _i32, [_vp, _vp, C.POINTER(C.c_int64), C.POINTER(C.c_uint64)])
+_sig("hh_pipeline_get_stats", _i32, [_vp, C.POINTER(PipelineStats)])
+_sig("hh_pipeline_reset_stats", None, [_vp])
+
+
 class HctInfo(C.Structure):
     """hh_hct_info: HCT v1 header fields (crates/haagenti-hct/src/tensor.rs:275-375)."""
     _fields_ = [("version", C.c_uint32), ("algorithm", C.c_uint8), ("dtype", C.c_uint8),
@@ -169,6 +216,11 @@ EXPORTS = [
     "hh_spectral_reconstruct", "hh_idct_2d", "hh_dct_2d", "hh_spectral_encoded_size",
     "hh_zstd_decompress", "hh_xxh64", "hh_turbo_tensor_decode",
     "hh_spectral_encode_from_dct",
+    "hh_pinned_alloc", "hh_pinned_free", "hh_pool_create", "hh_pool_destroy", "hh_pool_allocate",
+    "hh_pool_recycle", "hh_pool_get_stats", "hh_pipeline_default_config", "hh_pipeline_create",
+    "hh_pipeline_destroy", "hh_pipeline_streams", "hh_pipeline_next_staging", "hh_pipeline_submit",
+    "hh_pipeline_wait", "hh_pipeline_stream_wait", "hh_pipeline_get_times", "hh_pipeline_finish",
+    "hh_pipeline_get_stats", "hh_pipeline_reset_stats",
 ]
 
 CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8

@@ -162,11 +162,11 @@ int32_t hh_context_create(int32_t device, hh_context **out) {
 void hh_context_destroy(hh_context *ctx) {
     if (!ctx) return;
     hh::DeviceGuard guard(ctx->device);
-    if (ctx->stream) hipStreamSynchronize(ctx->stream);
-    if (ctx->d_basis) hipFree(ctx->d_basis);
-    if (ctx->d_scratch) hipFree(ctx->d_scratch);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->d_basis) (void)hipFree(ctx->d_basis);
+    if (ctx->d_scratch) (void)hipFree(ctx->d_scratch);
     hh::release_dct_resources(ctx);
-    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
 

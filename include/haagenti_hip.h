@@ -236,6 +236,111 @@ int32_t hh_hctt_decode_lz4_batch_noalloc(hh_context *ctx, const uint8_t *d_in, s
 int32_t hh_hctt_encode(const float *w, uint32_t rows, uint32_t cols, uint32_t k,
                        uint8_t *out, int32_t threads);
 
+/* ---------------------------------------------------------------- streaming */
+
+/* PinnedBuffer::new (crates/haagenti-cuda/src/memory.rs:156-196), as page-
+ * locked host memory (hipHostMalloc; the reference's is a Vec placeholder,
+ * memory.rs:161-168).  bytes = 0 gives *out = NULL. */
+int32_t hh_pinned_alloc(size_t bytes, void **out);
+int32_t hh_pinned_free(void *ptr);
+
+/* MemoryPool (memory.rs:200-340): one device arena of total_size bytes
+ * (allocated once at creation), handed out in 256-byte-aligned pieces,
+ * first fit, freed pieces coalesced.  Not thread-safe across pools; one
+ * pool may be used from several threads. */
+typedef struct hh_pool hh_pool;
+typedef struct hh_pool_stats { /* PoolStats (memory.rs:341-347) */
+    uint64_t total_size;
+    uint64_t allocated;
+    uint64_t available;          /* MemoryPool::available (memory.rs:251-254) */
+    uint64_t free_buffers;       /* free extents */
+    uint64_t free_buffer_bytes;
+    uint64_t largest_free;       /* the largest piece allocate() can return */
+} hh_pool_stats;
+int32_t hh_pool_create(hh_context *ctx, size_t total_size, hh_pool **out);
+void hh_pool_destroy(hh_pool *pool);
+/* MemoryPool::allocate (memory.rs:256-301): HH_ERR_OUT_OF_MEMORY when no
+ * free extent holds size bytes; zero != 0 clears the piece (the reference
+ * hands out zeroed buffers) with a synchronous memset. */
+int32_t hh_pool_allocate(hh_pool *pool, size_t size, int32_t zero, void **d_out);
+/* MemoryPool::recycle (memory.rs:312-317): the piece returns to the pool. */
+int32_t hh_pool_recycle(hh_pool *pool, void *d_ptr);
+int32_t hh_pool_get_stats(hh_pool *pool, hh_pool_stats *out);
+
+/* DecompressionPipeline (crates/haagenti-cuda/src/pipeline.rs:87-289):
+ * units of compressed LZ4 blocks (a decoder layer's tensors) staged in
+ * page-locked host buffers, copied to the device on a copy stream and
+ * decoded on a compute stream, ordered by events only, so the copy of unit
+ * l + 1 runs under the decode of unit l.  The reference synchronises the
+ * device between stages (pipeline.rs:212-232). */
+typedef struct hh_pipeline hh_pipeline;
+typedef struct hh_pipeline_config { /* PipelineConfig (pipeline.rs:35-60) */
+    uint32_t num_staging_buffers; /* 2 = double buffering (1..16) */
+    uint32_t max_blocks;          /* LZ4 blocks per unit */
+    uint64_t staging_buffer_size; /* bytes of one unit: data + 24 bytes per block of tables */
+    uint64_t tile_scratch_size;   /* device bytes for a unit's LZ4 output (tile bytes) */
+    uint32_t use_pinned_memory;   /* 1: hipHostMalloc staging */
+    uint32_t copy_threads;        /* host threads that copy a unit into staging */
+} hh_pipeline_config;
+typedef struct hh_pipeline_stats { /* PipelineStats (pipeline.rs:121-128) */
+    uint64_t blocks_processed;
+    uint64_t bytes_read;          /* compressed bytes copied to the device */
+    uint64_t bytes_decompressed;  /* LZ4 output bytes */
+    uint64_t transfer_time_ns;    /* host -> device copies (copy-stream events) */
+    uint64_t decompress_time_ns;  /* LZ4 + tile decode (compute-stream events) */
+    uint64_t units;               /* units completed */
+    uint64_t bytes_output;        /* decoded tensor bytes */
+} hh_pipeline_stats;
+/* Event times of one unit, in milliseconds since the pipeline's creation. */
+typedef struct hh_pipeline_times {
+    double h2d_start_ms, h2d_end_ms, decode_start_ms, decode_end_ms;
+} hh_pipeline_times;
+
+/* PipelineConfig::default: 2 staging buffers of 4 MiB, 65536 blocks, no
+ * tile scratch, pinned memory, 8 copy threads. */
+void hh_pipeline_default_config(hh_pipeline_config *cfg);
+/* DecompressionPipeline::new (pipeline.rs:134-170): the staging buffers,
+ * their device copies, per-slot status records and events, and the tile
+ * scratch; device memory comes from `pool` when given, else hipMalloc. */
+int32_t hh_pipeline_create(hh_context *ctx, hh_pool *pool, const hh_pipeline_config *cfg, hh_pipeline **out);
+void hh_pipeline_destroy(hh_pipeline *p);
+/* The pipeline's copy and compute streams (hipStream_t as void*). */
+int32_t hh_pipeline_streams(hh_pipeline *p, void **copy_stream, void **compute_stream);
+/* The staging buffer the next hh_pipeline_submit uses (after the unit that
+ * last used it has completed), for callers that read their data straight
+ * into it (PinnedBuffer::as_mut_slice); submitting from there copies
+ * nothing on the host. */
+int32_t hh_pipeline_next_staging(hh_pipeline *p, uint8_t **h_ptr, size_t *cap);
+/* DecompressionPipeline::submit_block + process (pipeline.rs:178-259) for
+ * one unit: h_data[0, len) holds nblocks LZ4 blocks (block i at h_in_off[i],
+ * h_in_len[i] bytes), decoded to d_lz4_out (lz4_out_cap bytes; NULL: the
+ * pipeline's tile scratch) at h_out_off[i], at most h_out_cap[i] bytes
+ * (hh_lz4_decompress_batch semantics).  Then the tensors (their d_tiles
+ * NULL: their tiles are packed in order in the LZ4 output) are decoded as
+ * hh_hctt_decode_batch does.  after_event (a hipEvent_t, or NULL) delays
+ * the decode until it completes (e.g. the consumer of the tensors' output
+ * slot is done with it).  The host blocks only while the staging slot's
+ * previous unit completes.  *ticket names the unit. */
+int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, const uint64_t *h_in_off,
+                           const uint32_t *h_in_len, const uint64_t *h_out_off, const uint32_t *h_out_cap,
+                           uint32_t nblocks, uint8_t *d_lz4_out, uint64_t lz4_out_cap,
+                           const hh_hctt_tensor *tensors, uint32_t ntensors, int32_t out_dtype,
+                           void *after_event, uint64_t *ticket);
+/* Blocks until the unit is decoded; returns its first failing block's code
+ * (HH_OK when every block decoded), with that block's record and index.
+ * Each ticket can be waited for once. */
+int32_t hh_pipeline_wait(hh_pipeline *p, uint64_t ticket, hh_block_status *status, int64_t *failed_block);
+/* Makes `stream` wait (on the device) for the unit's decode. */
+int32_t hh_pipeline_stream_wait(hh_pipeline *p, uint64_t ticket, void *stream);
+/* The unit's copy and decode intervals (waits for it). */
+int32_t hh_pipeline_get_times(hh_pipeline *p, uint64_t ticket, hh_pipeline_times *out);
+/* DecompressionPipeline::finish (pipeline.rs:262-269): waits for every
+ * unit; returns the first failure among the units not waited for. */
+int32_t hh_pipeline_finish(hh_pipeline *p, hh_block_status *status, int64_t *failed_block, uint64_t *failed_ticket);
+/* DecompressionPipeline::stats / reset_stats (pipeline.rs:281-289). */
+int32_t hh_pipeline_get_stats(hh_pipeline *p, hh_pipeline_stats *out);
+void hh_pipeline_reset_stats(hh_pipeline *p);
+
 /* ---------------------------------------------------------------- HCT container */
 
 /* Header and block-index geometry of an HCT v1 file (64-byte header,

@@ -65,3 +65,37 @@ def same_f32(a, b):
     b = np.ascontiguousarray(b, dtype=np.float32)
     na, nb = np.isnan(a), np.isnan(b)
     return bool((na == nb).all() and (a.view(np.uint32)[~na] == b.view(np.uint32)[~nb]).all())
+
+
+_hip = None
+
+
+def _hiprt():
+    """The HIP runtime torch loaded (for raw-pointer copies in tests)."""
+    global _hip
+    if _hip is None:
+        import ctypes
+        torch()
+        path = None
+        with open("/proc/self/maps") as f:
+            for ln in f:
+                if "libamdhip64" in ln:
+                    path = ln.split()[-1]
+                    break
+        _hip = ctypes.CDLL(path or "libamdhip64.so")
+        _hip.hipMemcpy.restype = ctypes.c_int
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return _hip
+
+
+def d2h(ptr, n):
+    """n bytes at a raw device address, copied to the host (hipMemcpy)."""
+    out = np.empty(int(n), np.uint8)
+    assert _hiprt().hipMemcpy(out.ctypes.data, int(ptr), int(n), 2) == 0
+    return out
+
+
+def h2d(ptr, a):
+    """Host bytes copied to a raw device address (hipMemcpy)."""
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    assert _hiprt().hipMemcpy(int(ptr), a.ctypes.data, a.size, 1) == 0

@@ -1,0 +1,213 @@
+"""Streaming decode runtime on the GPU: MemoryPool and PinnedBuffer
+(crates/haagenti-cuda/src/memory.rs:156-340) and DecompressionPipeline
+(crates/haagenti-cuda/src/pipeline.rs:87-320) streaming Llama-70B-shaped
+layers from pinned host memory into a double-buffered output slot, each
+layer checked against the oracle, the copy of layer l + 1 observed under
+the decode of layer l."""
+import numpy as np
+import pytest
+
+import gpu_util as G
+import layer_util as LU
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def H():
+    import haagenti_amd as h
+    return h
+
+
+def P():
+    import haagenti_amd.pipeline as p
+    return p
+
+
+def test_memory_pool_first_fit_and_coalescing():
+    Hm, Pm = H(), P()
+    pool = Pm.MemoryPool(G.ctx(), 1 << 20)
+    assert pool.total_size() == 1 << 20 and pool.allocated() == 0
+    a = pool.allocate(1000)                      # 256-byte pieces
+    b = pool.allocate(4096)
+    c = pool.allocate(300)
+    assert (b.ptr - a.ptr, c.ptr - b.ptr) == (1024, 4096)
+    assert pool.allocated() == 1024 + 4096 + 512
+    pool.recycle(b)
+    s = pool.stats()
+    assert s.free_buffers == 2 and s.largest_free == (1 << 20) - 1024 - 4096 - 512
+    assert s.available == (1 << 20) - 1024 - 512
+    d = pool.allocate(2048)                      # first fit: b's hole
+    assert d.ptr == b.ptr
+    pool.recycle(a)
+    pool.recycle(d)
+    pool.recycle(c)                              # everything coalesces back
+    s = pool.stats()
+    assert s.allocated == 0 and s.free_buffers == 1 and s.free_buffer_bytes == 1 << 20
+    big = pool.allocate(1 << 20)
+    with pytest.raises(Hm.HaagentiError) as ei:
+        pool.allocate(1)                         # OutOfMemory
+    assert ei.value.code == Hm.OUT_OF_MEMORY
+    with pytest.raises(Hm.HaagentiError):
+        pool.recycle(Pm.GpuBuffer(big.ptr + 256, 1, pool))   # not a piece start
+    pool.recycle(big)
+    pool.close()
+
+
+def test_pool_pieces_are_zeroed_on_request():
+    Pm = P()
+    pool = Pm.MemoryPool(G.ctx(), 1 << 16)
+    a = pool.allocate(5000, zero=False)
+    G.h2d(a.ptr, np.full(5000, 0xAB, np.uint8))
+    assert (G.d2h(a.ptr, 5000) == 0xAB).all()
+    pool.recycle(a)
+    b = pool.allocate(5000, zero=True)           # the same piece, cleared
+    assert b.ptr == a.ptr and (G.d2h(b.ptr, 5000) == 0).all()
+    pool.recycle(b)
+    pool.close()
+
+
+def test_pinned_buffer():
+    Hm, Pm = H(), P()
+    b = Pm.PinnedBuffer(1024)
+    b.copy_from_host(bytes([1, 2, 3, 4]))
+    assert b.size() == 4 and bytes(b.as_slice()) == bytes([1, 2, 3, 4])
+    with pytest.raises(Hm.HaagentiError):
+        b.copy_from_host(bytes(2048))            # SizeMismatch
+    b.close()
+
+
+def _layer_tables(L):
+    return L["in_off"], L["in_len"], L["out_off"], L["out_cap"]
+
+
+def test_pipeline_streams_70b_layers_with_overlap():
+    Hm, Pm = H(), P()
+    T = G.torch()
+    rng = np.random.default_rng(75)
+    ks_a = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, 7)]
+    ks_b = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, 7)]
+    LA = LU.encode_layer(Hm, LU.L70B, ks_a, seed=76)
+    LB = LU.encode_layer(Hm, LU.L70B, ks_b, seed=77)
+    layers = [LA, LB, LA]
+    # compressed layers in pinned host memory
+    pins = []
+    for L in (LA, LB):
+        pb = Pm.PinnedBuffer(L["blob"].size)
+        pb.copy_from_host(L["blob"])
+        pins.append(pb)
+    cfg = Pm.default_config()
+    cfg.num_staging_buffers = 2
+    cfg.max_blocks = max(L["in_off"].size for L in (LA, LB))
+    cfg.staging_buffer_size = max(L["blob"].size for L in (LA, LB)) + 24 * cfg.max_blocks + 256
+    cfg.tile_scratch_size = max(L["scratch_bytes"] for L in (LA, LB))
+    pool = Pm.MemoryPool(G.ctx(), 2 * cfg.staging_buffer_size + cfg.tile_scratch_size + (16 << 20))
+    pipe = Pm.DecompressionPipeline(G.ctx(), pool, cfg)
+    # the double-buffered output slot: two sets of the layer's tensors (f32)
+    slots = [[T.empty(r * c, dtype=T.float32, device="cuda") for _, r, c in LU.L70B] for _ in range(2)]
+    tst = [[T.full(((r // 64) * (c // 64),), -1, dtype=T.int32, device="cuda") for _, r, c in LU.L70B]
+           for _ in range(2)]
+
+    def submit(i):
+        L = layers[i]
+        src = pins[0 if L is LA else 1].as_slice()
+        desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o, s)
+                for t, o, s in zip(L["tensors"], slots[i % 2], tst[i % 2])]
+        print(f"[pipeline] submit layer {i}: {src.size} bytes, {L['in_off'].size} blocks", flush=True)
+        return pipe.submit(src, *_layer_tables(L), tensors=desc, dtype=Hm.F32)
+
+    def check(i):
+        L = layers[i]
+        for t, o, s in zip(L["tensors"], slots[i % 2], tst[i % 2]):
+            assert (s.cpu().numpy() == 0).all()
+            rc, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+            assert rc == O.OK
+            got = o.cpu().numpy().reshape(t["rows"], t["cols"])
+            rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+            err = float(np.abs(got - ref).max())
+            print(f"[pipeline] layer {i} {t['name']}: {err / rms:.2e} x RMS", flush=True)
+            assert err <= TOL * rms
+
+    t0 = submit(0)
+    t1 = submit(1)                                # copy of layer 1 under the decode of layer 0
+    pipe.wait(t0)
+    check(0)
+    t2 = submit(2)                                # back into slot 0, after layer 0 was read
+    pipe.wait(t1)
+    check(1)
+    pipe.wait(t2)
+    check(2)
+    tm = [pipe.times(t) for t in (t0, t1, t2)]
+    for i, t in enumerate(tm):
+        print(f"[pipeline] layer {i}: h2d {t.h2d_start_ms:.3f}-{t.h2d_end_ms:.3f} ms, "
+              f"decode {t.decode_start_ms:.3f}-{t.decode_end_ms:.3f} ms", flush=True)
+        assert t.h2d_start_ms <= t.h2d_end_ms <= t.decode_start_ms <= t.decode_end_ms
+    # overlap: layer 1's copy runs while layer 0 decodes
+    assert tm[1].h2d_start_ms < tm[0].decode_end_ms and tm[1].h2d_end_ms > tm[0].decode_start_ms
+    st = pipe.stats()
+    assert st.units == 3 and st.blocks_processed == sum(L["in_off"].size for L in layers)
+    assert st.bytes_read == sum(L["blob"].size for L in layers)
+    assert st.bytes_output == 3 * 4 * sum(r * c for _, r, c in LU.L70B)
+    pipe.finish()
+    pipe.close()
+    pool.close()
+
+
+def test_pipeline_pageable_and_in_place_staging_and_errors():
+    # a small layer through both host paths (pageable source copied into
+    # staging; data written straight into next_staging()), a corrupt block
+    # reported by wait() with its index, and finish() after that
+    Hm, Pm = H(), P()
+    T = G.torch()
+    shapes = [("a", 128, 192), ("b", 64, 256), ("c", 192, 64)]
+    L = LU.encode_layer(Hm, shapes, [1228, 410, 2048], seed=78, block_bytes=4096)
+    cfg = Pm.default_config()
+    cfg.staging_buffer_size = 1 << 20
+    cfg.tile_scratch_size = 1 << 20
+    cfg.max_blocks = 64
+    pipe = Pm.DecompressionPipeline(G.ctx(), None, cfg)
+    refs = []
+    for t in L["tensors"]:
+        _, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+        refs.append(ref)
+
+    def run(src, blob_tables=None):
+        outs = [T.empty(r * c, dtype=T.float32, device="cuda") for _, r, c in shapes]
+        desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o) for t, o in zip(L["tensors"], outs)]
+        tk = pipe.submit(src, *(blob_tables or _layer_tables(L)), tensors=desc, dtype=Hm.F32)
+        return tk, outs
+
+    tk, outs = run(L["blob"].copy())                         # pageable
+    pipe.wait(tk)
+    st = pipe.next_staging()                                 # in place
+    st[:L["blob"].size] = L["blob"]
+    tk2, outs2 = run(st[:L["blob"].size])
+    pipe.wait(tk2)
+    for o, o2, t, ref in zip(outs, outs2, L["tensors"], refs):
+        a = o.cpu().numpy().reshape(t["rows"], t["cols"])
+        assert np.array_equal(a, o2.cpu().numpy().reshape(t["rows"], t["cols"]))
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.abs(a - ref).max() <= TOL * rms
+    # a truncated block: wait() names it
+    bad = 3
+    il = L["in_len"].copy()
+    il[bad] //= 2
+    tk3, _ = run(L["blob"].copy(), (L["in_off"], il, L["out_off"], L["out_cap"]))
+    with pytest.raises(Hm.HaagentiError) as ei:
+        pipe.wait(tk3)
+    a = int(L["in_off"][bad])
+    _, e = O.lz4_decompress_block(L["blob"][a:a + int(il[bad])].tobytes(), int(L["out_cap"][bad]))
+    assert ei.value.code == e.kind and ei.value.block == bad
+    # raw LZ4 into a caller buffer, no tensors, failure reported by finish()
+    dst = T.zeros(L["scratch_bytes"], dtype=T.uint8, device="cuda")
+    tk4 = pipe.submit(L["blob"].copy(), *_layer_tables(L), lz4_out=dst, lz4_out_cap=dst.numel())
+    pipe.wait(tk4)
+    assert np.array_equal(dst.cpu().numpy(), np.concatenate([t["tiles"] for t in L["tensors"]]))
+    pipe.submit(L["blob"].copy(), L["in_off"], il, L["out_off"], L["out_cap"], lz4_out=dst,
+                lz4_out_cap=dst.numel())
+    with pytest.raises(Hm.HaagentiError) as ei:
+        pipe.finish()
+    assert ei.value.block == bad
+    pipe.finish()                                            # nothing pending any more
+    pipe.close()
