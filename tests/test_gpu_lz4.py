@@ -228,6 +228,59 @@ def test_ring_boundaries_far_long_and_periodic_copies():
         assert outs == srcs
 
 
+def _lz4_len(n):
+    """Extension bytes of a length field whose nibble is 15 (block.rs:277-289)."""
+    out = bytearray()
+    n -= 15
+    while n >= 255:
+        out.append(255)
+        n -= 255
+    out.append(n)
+    return bytes(out)
+
+
+def _seq(lit, off=None, ml=None):
+    """One LZ4 sequence; a literal-only last sequence when off is None."""
+    mn = 0 if off is None else min(ml - 4, 15)
+    s = bytearray([(min(len(lit), 15) << 4) | mn])
+    if len(lit) >= 15:
+        s += _lz4_len(len(lit))
+    s += lit
+    if off is not None:
+        s += bytes([off & 0xFF, off >> 8])
+        if ml - 4 >= 15:
+            s += _lz4_len(ml - 4)
+    return bytes(s)
+
+
+def test_long_literals_then_matches_into_them():
+    # Literals of 2 KiB and more (the ring decoder copies those straight
+    # from the input to the output and keeps only their tail in the ring),
+    # each followed by matches whose sources lie in the literal, just inside
+    # and just outside the ring's reach (offset R - 32 = 4064 for 4 KiB),
+    # before the literal, and periodic; blocks that end with a long literal;
+    # and capacities that end inside a long literal or right after it.
+    rng = np.random.default_rng(7)
+    streams, caps = [], []
+    for L in [2048, 2049, 3000, 4064, 4065, 4100, 9000, 20000]:
+        for off_kind in range(6):
+            head = rng.integers(0, 256, 37, dtype=np.uint8).tobytes()
+            lit = rng.integers(0, 256, L, dtype=np.uint8).tobytes()
+            off = {0: 1, 1: 17, 2: min(L, 4064), 3: min(L + 30, 4065), 4: L + 30, 5: L // 2}[off_kind]
+            ml = [4, 19, 300, 5000][off_kind % 4]
+            tail = rng.integers(0, 256, 2500 + 13 * off_kind, dtype=np.uint8).tobytes()
+            streams.append(_seq(head, 3, 40) + _seq(lit, off, ml) + _seq(b"xy", 2100, 64) + _seq(tail))
+            caps.append(37 + 40 + L + ml + 2 + 64 + len(tail))
+    # exact sizes (the block ends with its literal), a cap inside the long
+    # literal, and one right after it (early stop: block.rs:309-311)
+    lit = rng.integers(0, 256, 6000, dtype=np.uint8).tobytes()
+    s = _seq(b"ab", 1, 100) + _seq(lit, 50, 20) + _seq(lit[:3000])
+    streams += [s, s, s]
+    caps += [102 + 6000 + 20 + 3000, 102 + 3000, 102 + 6000]
+    for out_align in (0, 1, 7, 15):
+        check_against_oracle(streams, caps, out_align=out_align, in_align=out_align % 3, out_pad=5)
+
+
 def test_lengths_beyond_32_bits():
     # runs of ~2^24 0xFF extension bytes: lengths just below and above 2^32;
     # a literal that long fails the input-length check, a match that long
