@@ -39,9 +39,9 @@ Other workloads (one JSON line each, same contract):
   hct3-4096        one 4096x4096 N(0, 0.02) tensor as an HCT V3 fragment
                    container (whole-tensor DCT, turbo defaults: top 20 %,
                    f16 coefficients); GPU bitmap scatter + whole-matrix
-                   inverse DCT as five f16 GEMMs on split hi/lo operands
-                   (f32 accumulation), bf16 out; roofline against the dense
-                   f16 MFMA peak (HH_DCT_F32=1: two fp32 GEMMs, fp32 peak)
+                   inverse DCT as two hand-written split-f16 MFMA products
+                   (five f16 passes, f32 accumulation), bf16 out; roofline
+                   against the dense f16 MFMA peak
   hbm-copy         a plain 1 GiB device copy: the HBM reference rate and the
                    calibration for the FETCH_SIZE / WRITE_SIZE counters
 
@@ -622,17 +622,14 @@ def wl_hct3(args, torch, H, O):
     per = ms_step / 1e3
     flop = 4.0 * n ** 3          # two n x n x n GEMMs
     achieved = flop / per / 1e12
-    split = os.environ.get("HH_DCT_F32", "0") != "1"
-    peak = 2500.0 if split else 157.3
+    peak = 2500.0
     roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
-            "kernel": ("rocBLAS f16 gemm_ex x5, split f16 operands, f32 accumulation (+ bitmap scatter, "
-                       "split and scale-to-bf16 passes)") if split else
-                      "rocBLAS sgemm x2 (+ bitmap scatter, bf16 conversion)",
+            "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA, 2 + 3 passes, f32 accumulation; "
+                       "+ bitmap scatter and the amax / scale passes)"),
             "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
-            "mfma_type": "f16" if split else "fp32",
-            "mfma_flop_per_launch": 5 * 2 * n ** 3 if split else flop}
-    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, "f16-split-mfma/f32" if split else "f32",
+            "mfma_type": "f16", "mfma_flop_per_launch": 5 * 2 * n ** 3}
+    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, "f16-split-mfma/f32",
                 "synthetic (4096x4096 N(0,0.02), torch seed 17, turbo defaults)",
                 {"rows": n, "cols": n, "retention": 0.20, "coefficients": int(keep),
                  "container_bytes": len(data), "out_dtype": "bf16"}, roof, cpu,

@@ -19,25 +19,14 @@
 //
 // Transform.  With B_n[k][i] = s_k cos(pi k (2i + 1) / 2n) (s_0 = sqrt(1/n),
 // s_k = sqrt(2/n)), the inverse DCT of the h x w coefficient matrix C is
-// X = B_h^T C B_w, computed as two fp32 GEMMs (rocBLAS): T = C B_w, then
-// X = B_h^T T.  The forward DCT-II (dct_2d, dct.rs:282-308) is the
-// transpose: C = B_h X B_w^T.  The basis matrices are generated on the GPU
-// from an exact integer reduction of the cosine argument and cached per
-// context.  fp32 GEMMs with K = n accumulate to ~1e-6 x RMS, against the
+// X = B_h^T C B_w and the forward DCT-II (dct_2d, dct.rs:282-308) is
+// C = B_h X B_w^T; each is two split-f16 MFMA products (dct_gemm.hip)
+// against basis planes generated on the GPU from an exact integer reduction
+// of the cosine argument and cached per context.  The input is first scaled
+// by a power of two 2^e chosen from max |input| (the amax and scale kernels
+// below) so that every f16 operand stays far from overflow; the last
+// product multiplies by 2^-e (exact).  Error ~1e-6 x RMS, against the
 // 1e-3 x RMS bar of the tolerance-based IDCT parity.
-//
-// The inverse runs on the f16 MFMA instead (16x the fp32 MFMA rate): every
-// operand is split into f16 hi + lo (x = hi + lo to ~2^-22 relative) and each
-// product of two split operands is three f16 GEMMs with f32 accumulation
-// (hi*hi + hi*lo + lo*hi; the dropped lo*lo is ~2^-22 relative).  C is first
-// scaled by a power of two 2^e chosen from max|C| so that |C 2^e| and the
-// intermediate T = B_w^T C 2^e stay below 2^14 (|T| <= max|C| sqrt(w)), far
-// from f16 overflow; a last elementwise pass multiplies by 2^-e (exact).
-// HH_DCT_F32=1 selects the fp32 GEMMs.
-#include <cstdlib>
-
-#include <rocblas/rocblas.h>
-
 #include "hh_internal.hpp"
 
 namespace hh {
@@ -168,17 +157,6 @@ __global__ __launch_bounds__(256) void hct3_scatter_kernel(const uint64_t *__res
     }
 }
 
-// B[k][i] = s_k cos(pi k (2i + 1) / 2n): the argument is reduced exactly in
-// integers (k (2i + 1) mod 4n) before the double-precision cosine.
-__global__ __launch_bounds__(256) void dct3_basis_kernel(float *__restrict__ B, uint32_t n) {
-    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (uint64_t)n * n) return;
-    const uint32_t k = (uint32_t)(idx / n), i = (uint32_t)(idx % n);
-    const uint64_t m = ((uint64_t)k * (2ull * i + 1ull)) % (4ull * n);
-    const double sk = k == 0 ? sqrt(1.0 / (double)n) : sqrt(2.0 / (double)n);
-    B[idx] = (float)(sk * cospi((double)m / (2.0 * (double)n)));
-}
-
 // 64-bit words of a bitmap held at any byte address (nbytes bytes; the last
 // word is zero-padded).
 __global__ __launch_bounds__(256) void pack_bits_kernel(const uint8_t *__restrict__ src, uint64_t nbytes,
@@ -249,36 +227,6 @@ __global__ __launch_bounds__(256) void split_scale_kernel(const float *__restric
     }
 }
 
-// hi = f16(x s), lo = f16(x s - hi) (round to nearest even; x s - hi is
-// exact in f32); s = *scale, or 1 without one.
-__global__ __launch_bounds__(256) void split_f16_kernel(const float *__restrict__ x, uint64_t n,
-                                                        const float *__restrict__ scale,
-                                                        _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
-    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float v = scale ? x[i] * scale[0] : x[i];
-    const _Float16 h = (_Float16)v;
-    hi[i] = h;
-    lo[i] = (_Float16)(v - (float)h);
-}
-
-// x *= *scale, in place
-__global__ __launch_bounds__(256) void scale_kernel(float *__restrict__ x, uint64_t n, const float *__restrict__ scale) {
-    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) x[i] *= scale[0];
-}
-
-// out = 16-bit RNE of x * *scale (the scale is a power of two: exact)
-__global__ __launch_bounds__(256) void scale_convert_kernel(const float *__restrict__ x, uint64_t n,
-                                                            const float *__restrict__ scale, int dtype,
-                                                            void *__restrict__ out) {
-    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float v = x[i] * scale[0];
-    uint16_t *o = reinterpret_cast<uint16_t *>(out);
-    o[i] = (uint16_t)(dtype == HH_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
-}
-
 }  // namespace
 
 hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t *d_block_sums,
@@ -312,102 +260,77 @@ hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_o
     return hipGetLastError();
 }
 
-// The context's cached basis B_n (two sizes are kept; the older is replaced).
-static int32_t basis_for(hh_context *ctx, uint32_t n, hipStream_t s, const float **out) {
-    for (int i = 0; i < 2; i++)
-        if (ctx->dct_basis[i].d && ctx->dct_basis[i].n == n) {
-            ctx->dct_basis[i].stamp = ++ctx->dct_stamp;
-            *out = ctx->dct_basis[i].d;
+// The context's cached basis planes of B_n (or B_n^T); two are kept, the
+// older is replaced.
+static int32_t planes_for(hh_context *ctx, uint32_t n, bool transposed, hipStream_t s, const uint16_t **hi,
+                          const uint16_t **lo) {
+    const uint64_t plane = (uint64_t)dct_planes_rows(n) * dct_planes_cols(n);
+    for (int i = 0; i < 2; i++) {
+        hh_context::Basis &b = ctx->dct_basis[i];
+        if (b.hl && b.n == n && b.transposed == transposed) {
+            b.stamp = ++ctx->dct_stamp;
+            *hi = b.hl;
+            *lo = b.hl + plane;
             return HH_OK;
         }
-    const int v = !ctx->dct_basis[0].d ? 0 : !ctx->dct_basis[1].d ? 1
+    }
+    const int v = !ctx->dct_basis[0].hl ? 0 : !ctx->dct_basis[1].hl ? 1
                   : ctx->dct_basis[0].stamp <= ctx->dct_basis[1].stamp ? 0 : 1;
     hh_context::Basis &b = ctx->dct_basis[v];
-    if (b.d) {
-        hipError_t e = hipFree(b.d);
-        if (b.hl && e == hipSuccess) e = hipFree(b.hl);
-        b.d = nullptr;
+    if (b.hl) {
+        // the stream may still read the old planes: wait before freeing
+        hipError_t e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = hipFree(b.hl);
         b.hl = nullptr;
         b.n = 0;
         if (e != hipSuccess) return from_hip(e);
     }
-    hipError_t e = hipMalloc(&b.d, (size_t)n * n * sizeof(float));
+    hipError_t e = hipMalloc(&b.hl, 2 * plane * sizeof(uint16_t));
     if (e != hipSuccess) {
-        b.d = nullptr;
+        b.hl = nullptr;
         return from_hip(e);
     }
     b.n = n;
+    b.transposed = transposed;
     b.stamp = ++ctx->dct_stamp;
-    hipLaunchKernelGGL(dct3_basis_kernel, dim3(blocks_for((uint64_t)n * n, 256)), dim3(256), 0, s, b.d, n);
-    e = hipGetLastError();
+    e = launch_dct_basis_planes(b.hl, b.hl + plane, n, transposed, s);
     if (e != hipSuccess) return from_hip(e);
-    *out = b.d;
+    *hi = b.hl;
+    *lo = b.hl + plane;
     return HH_OK;
 }
 
-// The f16 hi / lo halves of the cached basis B_n (made on first use).
-static int32_t basis_split_for(hh_context *ctx, uint32_t n, const float *bd, hipStream_t s, const _Float16 **hi,
-                               const _Float16 **lo) {
-    for (int i = 0; i < 2; i++) {
-        hh_context::Basis &b = ctx->dct_basis[i];
-        if (b.d != bd) continue;
-        const uint64_t nn = (uint64_t)n * n;
-        if (!b.hl) {
-            hipError_t e = hipMalloc(&b.hl, 2 * nn * sizeof(uint16_t));
-            if (e != hipSuccess) {
-                b.hl = nullptr;
-                return from_hip(e);
-            }
-            _Float16 *h = reinterpret_cast<_Float16 *>(b.hl);
-            hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(nn, 256)), dim3(256), 0, s, b.d, nn,
-                               (const float *)nullptr, h, h + nn);
-            e = hipGetLastError();
-            if (e != hipSuccess) return from_hip(e);
-        }
-        *hi = reinterpret_cast<const _Float16 *>(b.hl);
-        *lo = *hi + nn;
-        return HH_OK;
-    }
-    return HH_ERR_INVALID_ARGUMENT;
-}
-
-static int32_t blas_for(hh_context *ctx, hipStream_t s, rocblas_handle *h) {
-    if (!ctx->blas) {
-        rocblas_handle nh = nullptr;
-        if (rocblas_create_handle(&nh) != rocblas_status_success) return HH_ERR_DEVICE;
-        ctx->blas = nh;
-    }
-    *h = reinterpret_cast<rocblas_handle>(ctx->blas);
-    return rocblas_set_stream(*h, s) == rocblas_status_success ? HH_OK : HH_ERR_DEVICE;
-}
-
-static int32_t blas_status(rocblas_status st) {
-    switch (st) {
-        case rocblas_status_success: return HH_OK;
-        case rocblas_status_memory_error: return HH_ERR_OUT_OF_MEMORY;
-        case rocblas_status_invalid_size:
-        case rocblas_status_invalid_pointer:
-        case rocblas_status_invalid_value: return HH_ERR_INVALID_ARGUMENT;
-        default: return HH_ERR_KERNEL_LAUNCH;
-    }
-}
-
-// X = B_h^T C B_w on the f16 MFMA (see the header): d_tmp holds T in f32.
-static int32_t idct_split(hh_context *ctx, rocblas_handle h, const float *d_in, float *d_tmp, float *d_out,
-                          uint32_t rows, uint32_t cols, const float *bw, const float *bh, hipStream_t s,
-                          bool f16_exact, int32_t cvt_dtype, void *cvt_out) {
-    const uint64_t total = (uint64_t)rows * cols;
-    const _Float16 *bw_hi, *bw_lo, *bh_hi, *bh_lo;
-    int32_t rc = basis_split_for(ctx, cols, bw, s, &bw_hi, &bw_lo);
+int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
+                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact, int32_t cvt_dtype,
+                   void *cvt_out, bool *converted) {
+    if (converted) *converted = false;
+    if (rows == 0 || cols == 0) return HH_OK;
+    const uint32_t h = rows, w = cols;
+    const uint64_t total = (uint64_t)h * w;
+    // the inverse needs B^T planes, the forward B planes; a square matrix
+    // uses one set for both products
+    const uint16_t *wh, *wl, *hh_, *hl;
+    int32_t rc = planes_for(ctx, w, inverse, s, &wh, &wl);
     if (rc != HH_OK) return rc;
-    rc = basis_split_for(ctx, rows, bh, s, &bh_hi, &bh_lo);
+    rc = planes_for(ctx, h, inverse, s, &hh_, &hl);
     if (rc != HH_OK) return rc;
-    // split scratch: hi and lo operand halves, block maxima, constants
+    if (h == w) {  // the second lookup may have replaced the first's slot
+        wh = hh_;
+        wl = hl;
+    }
+    // scratch: block maxima, the constants {0, 1, 2^e, 2^-e}, the input's
+    // planes and the intermediate's planes
     const uint32_t np = 1024;
-    const size_t need = 2 * total * sizeof(uint16_t) + (np + 4) * sizeof(float) + 256;
+    const uint64_t in_plane = (uint64_t)dct_planes_rows(h) * dct_planes_cols(w);
+    const uint64_t mid_plane = (uint64_t)dct_planes_rows(w) * dct_planes_cols(h);
+    const bool need_lo = !(inverse && f16_exact);
+    const size_t off_in = ((np + 4) * sizeof(float) + 255) & ~(size_t)255;  // after the maxima and constants
+    const size_t off_mid = off_in + ((in_plane * (need_lo ? 4 : 2) + 255) & ~(uint64_t)255);
+    const size_t need = off_mid + mid_plane * 4;
     if (ctx->split_bytes < need) {
         if (ctx->d_split) {
-            hipError_t e = hipFree(ctx->d_split);
+            hipError_t e = hipStreamSynchronize(s);
+            if (e == hipSuccess) e = hipFree(ctx->d_split);
             ctx->d_split = nullptr;
             ctx->split_bytes = 0;
             if (e != hipSuccess) return from_hip(e);
@@ -419,102 +342,68 @@ static int32_t idct_split(hh_context *ctx, rocblas_handle h, const float *d_in, 
         }
         ctx->split_bytes = need;
     }
-    _Float16 *ohi = reinterpret_cast<_Float16 *>(ctx->d_split);
-    _Float16 *olo = ohi + total;
-    float *partial = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->d_split) +
-                                               ((2 * total * sizeof(uint16_t) + 255) & ~(size_t)255));
+    uint8_t *sp = reinterpret_cast<uint8_t *>(ctx->d_split);
+    float *partial = reinterpret_cast<float *>(sp);
     float *consts = partial + np;
+    uint16_t *in_hi = reinterpret_cast<uint16_t *>(sp + off_in);
+    uint16_t *in_lo = need_lo ? in_hi + in_plane : nullptr;
+    uint16_t *mid_hi = reinterpret_cast<uint16_t *>(sp + off_mid);
+    uint16_t *mid_lo = mid_hi + mid_plane;
+    (void)d_tmp;
     hipLaunchKernelGGL(amax_kernel, dim3(np), dim3(256), 0, s, d_in, total, partial);
-    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, partial, np, cols, consts);
-    hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_in, total,
-                       (const float *)(consts + 2), ohi, olo);
+    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, partial, np, w, consts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return from_hip(e);
-    const int m = (int)cols, n = (int)rows;
-    // host scalars (rocBLAS reads device scalars back to the host per call);
-    // 2^-e is applied by a last elementwise pass
-    const float c0 = 0.0f, c1 = 1.0f;
-    const float *k0 = &c0, *k1 = &c1;
-    const rocblas_datatype f16 = rocblas_datatype_f16_r, f32 = rocblas_datatype_f32_r;
-    auto gemm = [&](rocblas_operation ta, rocblas_operation tb, int k, const float *alpha, const void *a, int lda,
-                    const void *b, int ldb, const float *beta, float *c) {
-        return rocblas_gemm_ex(h, ta, tb, m, n, k, alpha, a, f16, lda, b, f16, ldb, beta, c, f32, m, c, f32, m, f32,
-                               rocblas_gemm_algo_standard, 0, 0);
-    };
-    const rocblas_operation N = rocblas_operation_none, T = rocblas_operation_transpose;
-    // T^T = B_w^T (C 2^e)^T, three passes (column-major views as below)
-    rocblas_status st = gemm(N, N, m, k1, bw_hi, m, ohi, m, k0, d_tmp);
-    if (st == rocblas_status_success) st = gemm(N, N, m, k1, bw_lo, m, ohi, m, k1, d_tmp);
-    // (an input of f16 values scaled by 2^e has no low half)
-    if (st == rocblas_status_success && !f16_exact) st = gemm(N, N, m, k1, bw_hi, m, olo, m, k1, d_tmp);
-    if (st == rocblas_status_success) {
-        hipLaunchKernelGGL(split_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_tmp, total,
-                           (const float *)nullptr, ohi, olo);
-        if (hipGetLastError() != hipSuccess) st = rocblas_status_internal_error;
-    }
-    // X^T 2^e = T^T B_h, three passes; then X = 2^-e (X 2^e)
-    if (st == rocblas_status_success) st = gemm(N, T, n, k1, ohi, m, bh_hi, n, k0, d_out);
-    if (st == rocblas_status_success) st = gemm(N, T, n, k1, ohi, m, bh_lo, n, k1, d_out);
-    if (st == rocblas_status_success) st = gemm(N, T, n, k1, olo, m, bh_hi, n, k1, d_out);
-    if (st != rocblas_status_success) return blas_status(st);
-    if (cvt_out)
-        hipLaunchKernelGGL(scale_convert_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
-                           (const float *)(consts + 3), (int)cvt_dtype, cvt_out);
-    else
-        hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, d_out, total,
-                           (const float *)(consts + 3));
-    return from_hip(hipGetLastError());
-}
-
-int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
-                   uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact, int32_t cvt_dtype,
-                   void *cvt_out, bool *converted) {
-    if (converted) *converted = false;
-    if (rows == 0 || cols == 0) return HH_OK;
-    const float *bw = nullptr, *bh = nullptr;
-    int32_t rc = basis_for(ctx, cols, s, &bw);
-    if (rc != HH_OK) return rc;
-    rc = basis_for(ctx, rows, s, &bh);
-    if (rc != HH_OK) return rc;
-    if (rows == cols) bw = bh;  // one cache slot serves both
-    rocblas_handle h;
-    rc = blas_for(ctx, s, &h);
-    if (rc != HH_OK) return rc;
-    const float one = 1.0f, zero = 0.0f;
-    // Column-major views: a row-major h x w matrix M is the w x h matrix
-    // M^T with leading dimension w; a row-major basis B_n is B_n^T.
-    //   inverse:  T^T = B_w^T C^T     (m = w, n = h, k = w)
-    //             X^T = T^T B_h       (m = w, n = h, k = h)
-    //   forward:  T^T = B_w X^T       (m = w, n = h, k = w)
-    //             C^T = T^T B_h^T     (m = w, n = h, k = h)
-    const int m = (int)cols, n = (int)rows;
-    const char *f32env = std::getenv("HH_DCT_F32");
-    if (inverse && !(f32env && f32env[0] == '1')) {
-        if (converted) *converted = cvt_out != nullptr;
-        return idct_split(ctx, h, d_in, d_tmp, d_out, rows, cols, bw, bh, s, f16_exact, cvt_dtype, cvt_out);
-    }
-    rocblas_status st = rocblas_sgemm(h, inverse ? rocblas_operation_none : rocblas_operation_transpose,
-                                      rocblas_operation_none, m, n, m, &one, bw, m, d_in, m, &zero,
-                                      d_tmp, m);
-    if (st != rocblas_status_success) return blas_status(st);
-    st = rocblas_sgemm(h, rocblas_operation_none, inverse ? rocblas_operation_transpose : rocblas_operation_none,
-                       m, n, n, &one, d_tmp, m, bh, n, &zero, d_out, m);
-    return blas_status(st);
+    e = launch_operand_planes(d_in, h, w, w, consts + 2, in_hi, in_lo, s);
+    if (e != hipSuccess) return from_hip(e);
+    // first product: the w x h matrix P = B_w^T (C 2^e)^T (inverse) or
+    // B_w (X 2^e)^T (forward), as the second product's planes
+    DctGemm g1;
+    g1.a_hi = wh;
+    g1.a_lo = wl;
+    g1.b_hi = in_hi;
+    g1.b_lo = in_lo;
+    g1.out_scale = nullptr;
+    g1.d = mid_hi;
+    g1.ldd = 0;
+    g1.d_dtype = HH_F32;
+    g1.d_planes = true;
+    g1.M = w;
+    g1.N = h;
+    g1.K = w;
+    e = launch_dct_gemm(g1, s);
+    if (e != hipSuccess) return from_hip(e);
+    // second product: the h x w result 2^-e B_h^T P^T (inverse) or
+    // 2^-e B_h P^T (forward), converted on the way out when asked
+    const bool cvt = inverse && cvt_out != nullptr;
+    DctGemm g2;
+    g2.a_hi = hh_;
+    g2.a_lo = hl;
+    g2.b_hi = mid_hi;
+    g2.b_lo = mid_lo;
+    g2.out_scale = consts + 3;
+    g2.d = cvt ? cvt_out : d_out;
+    g2.ldd = w;
+    g2.d_dtype = cvt ? cvt_dtype : HH_F32;
+    g2.d_planes = false;
+    g2.M = h;
+    g2.N = w;
+    g2.K = h;
+    e = launch_dct_gemm(g2, s);
+    if (e != hipSuccess) return from_hip(e);
+    if (converted) *converted = cvt;
+    return HH_OK;
 }
 
 void release_dct_resources(hh_context *ctx) {
     for (int i = 0; i < 2; i++) {
-        if (ctx->dct_basis[i].d) hipFree(ctx->dct_basis[i].d);
-        if (ctx->dct_basis[i].hl) hipFree(ctx->dct_basis[i].hl);
-        ctx->dct_basis[i].d = nullptr;
+        if (ctx->dct_basis[i].hl) (void)hipFree(ctx->dct_basis[i].hl);
         ctx->dct_basis[i].hl = nullptr;
         ctx->dct_basis[i].n = 0;
     }
-    if (ctx->d_split) hipFree(ctx->d_split);
+    if (ctx->d_split) (void)hipFree(ctx->d_split);
     ctx->d_split = nullptr;
     ctx->split_bytes = 0;
-    if (ctx->blas) rocblas_destroy_handle(reinterpret_cast<rocblas_handle>(ctx->blas));
-    ctx->blas = nullptr;
 }
 
 }  // namespace hh

@@ -19,18 +19,18 @@ struct hh_context {
     // (grown on demand, kept until the context is destroyed).
     void *d_scratch = nullptr;
     size_t scratch_bytes = 0;
-    // Whole-matrix DCT bases B_n (hct3_decode.hip), two sizes cached, and the
-    // rocBLAS handle of the whole-matrix transforms, created on first use.
+    // Whole-matrix DCT bases B_n (or B_n^T) as f16 hi / lo planes
+    // (dct_gemm.hip), two cached.
     struct Basis {
         uint32_t n = 0;
-        float *d = nullptr;
-        uint16_t *hl = nullptr;  // the same as f16 hi (n x n) then lo (n x n)
+        bool transposed = false;
+        uint16_t *hl = nullptr;  // hi plane then lo plane, dct_planes_rows(n) x dct_planes_cols(n) each
         uint64_t stamp = 0;
     };
     Basis dct_basis[2];
     uint64_t dct_stamp = 0;
-    void *blas = nullptr;
-    // f16 split operands of the whole-matrix inverse DCT (grown on demand)
+    // scratch of the whole-matrix transforms: block maxima, scale constants
+    // and the f16 planes of the input and of the intermediate product
     void *d_split = nullptr;
     size_t split_bytes = 0;
     // Device address of the library-owned tile-byte array of
@@ -181,12 +181,39 @@ size_t hct3_block_sums_bytes(uint64_t nbits);
 // Bitmap bytes at any device address -> zero-padded 64-bit words.
 hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_words, hipStream_t s);
 hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_out, hipStream_t s);
+// One split-f16 MFMA product D = s_out * A Bt^T (dct_gemm.hip).  A (M x K)
+// and Bt (N x K) are f16 hi / lo planes, row-major with k contiguous,
+// dct_planes_rows(rows) x dct_planes_cols(K) with zeros past the matrix;
+// b_lo null: Bt has no low half.  D: M x N (row stride ldd) in d_dtype, or
+// with d_planes the hi / lo planes of the next product's Bt (its padded
+// extent, zeros included; lo follows hi at dct_planes_rows(M) x
+// dct_planes_cols(N) elements).
+struct DctGemm {
+    const uint16_t *a_hi, *a_lo, *b_hi, *b_lo;
+    const float *out_scale;  // device scalar, or null for 1
+    void *d;
+    uint32_t ldd;
+    int32_t d_dtype;
+    bool d_planes;
+    uint32_t M, N, K;
+};
+hipError_t launch_dct_gemm(const DctGemm &p, hipStream_t s);
+uint32_t dct_planes_rows(uint32_t n);
+uint32_t dct_planes_cols(uint32_t n);
+// hi / lo planes of B_n (P[m][k] = B_n[m][k]) or of B_n^T.
+hipError_t launch_dct_basis_planes(uint16_t *hi, uint16_t *lo, uint32_t n, bool transposed, hipStream_t s);
+// hi (and lo, unless null) planes of an f32 rows x cols matrix (row stride
+// ld) times *scale.
+hipError_t launch_operand_planes(const float *x, uint32_t rows, uint32_t cols, uint32_t ld, const float *scale,
+                                 uint16_t *hi, uint16_t *lo, hipStream_t s);
+
 // Orthonormal 2-D DCT-III (inverse) or DCT-II (forward) of a row-major
-// rows x cols f32 matrix: two GEMMs through d_tmp (rows*cols f32); d_out may
-// not alias d_in or d_tmp.  f16_exact: every input value is an f16 value
-// (the inverse then skips the GEMM pass of the input's low f16 half).
-// cvt_out: a 16-bit output (cvt_dtype) the inverse may write directly from
-// its last pass, reported in *converted (d_out then holds an intermediate).
+// rows x cols f32 matrix: two split-f16 MFMA products through d_tmp
+// (rows*cols f32); d_out may not alias d_in or d_tmp.  f16_exact: every
+// input value is an f16 value (the first product then skips the pass of the
+// input's low f16 half).  cvt_out: a 16-bit output (cvt_dtype) the inverse
+// may write directly from its last pass, reported in *converted (d_out then
+// is not written).
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,
                    uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact = false,
                    int32_t cvt_dtype = HH_F32, void *cvt_out = nullptr, bool *converted = nullptr);
