@@ -599,6 +599,52 @@ class HctReaderV2(HctReader):
         self._gpu(ctx, False, d_file, None, 0, stream)
 
 
+class HctWriter:
+    """HctWriter (crates/haagenti-hct/src/tensor.rs:519-617), host producer of
+    version-1 files: the 64-byte header (HctHeader::to_bytes, :299-328;
+    version 1, flags 0, shape dims at 37 + 8 i), one 8-byte index entry per
+    block (offset from the data start, compressed size; :391-396), then the
+    blocks in order.  Shapes of rank 4 and more do not fit the header (the
+    reference's header serialization indexes past its 64 bytes); they raise
+    ValueError."""
+
+    def __init__(self, dtype, shape, block_size=16 * 1024, algorithm=0):
+        if len(shape) > 3:
+            raise ValueError("an HCT v1 header holds at most 3 dimensions")
+        self.dtype, self.shape, self.block_size, self.algorithm = dtype, list(shape), block_size, algorithm
+        self.blocks = []
+        self.original_size = 0
+
+    def with_block_size(self, block_size):
+        self.block_size = block_size
+        return self
+
+    def add_block(self, compressed, original_len):
+        self.blocks.append(bytes(compressed))
+        self.original_size += original_len
+
+    def compress_data(self, data, compressor):
+        data = bytes(data)
+        for s in range(0, len(data), self.block_size):
+            chunk = data[s:s + self.block_size]
+            self.add_block(compressor.compress(chunk), len(chunk))
+
+    def finish(self):
+        import struct
+        index, off = b"", 0
+        for c in self.blocks:
+            index += struct.pack("<II", off, len(c))
+            off += len(c)
+        h = bytearray(64)
+        h[0:4] = b"HCTN"
+        struct.pack_into("<IBBHQQII", h, 4, 1, self.algorithm, self.dtype, 0,
+                         self.original_size, off, self.block_size, len(self.blocks))
+        h[36] = len(self.shape)
+        for i, d in enumerate(self.shape):
+            struct.pack_into("<Q", h, 37 + 8 * i, d)
+        return bytes(h) + index + b"".join(self.blocks)
+
+
 class HctWriterV2:
     """HctWriterV2 (tensor.rs:679-829), host producer: header (version 2,
     flags), optional quantization metadata, 16-byte index entries with the

@@ -157,6 +157,23 @@ def test_hct_header_errors_match_oracle():
         assert ei.value.code == e.kind, (c[:12], ei.value.code, e.kind)
 
 
+def test_v1_writer_byte_identical_to_oracle():
+    # HctWriter (tensor.rs:519-617) against the oracle's restatement, for
+    # whole and ragged last blocks and ranks 0..3
+    import haagenti_amd as H
+    rng = np.random.default_rng(23)
+    for n, bs, dtype, shape in [(70001, 16384, 3, [70001]), (4096, 1024, 4, [64, 32]),
+                                (1000, 256, 0, [10, 10, 10]), (1, 16384, 2, []), (0, 16384, 1, [0])]:
+        data = rng.integers(0, 6, n, dtype=np.uint8).tobytes()
+        w = H.HctWriter(dtype, shape, bs)
+        w.compress_data(data, H.Lz4Compressor())
+        assert w.finish() == O.hct_write_lz4(data, bs, dtype, shape), (n, bs, shape)
+        r = H.HctReader(w.finish())
+        assert r.header()["shape"] == shape and r.header()["num_blocks"] == (n + bs - 1) // bs
+    with pytest.raises(ValueError):
+        H.HctWriter(0, [2, 2, 2, 2])
+
+
 # ---------------------------------------------------------------- HCT v2 (host side)
 def test_xxh3_host_matches_xxhash_library():
     xxhash = pytest.importorskip("xxhash")

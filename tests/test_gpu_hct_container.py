@@ -67,6 +67,18 @@ def test_block_boundaries(n, bs):
     assert code == 0 and got == data
 
 
+def test_product_writer_file():
+    # a file from the product's HctWriter (tensor.rs:519-617), read back on
+    # the GPU and by the oracle
+    import haagenti_amd as H
+    rng = np.random.default_rng(12)
+    data = rng.integers(0, 7, 100003, dtype=np.uint8).tobytes()
+    w = H.HctWriter(4, [100003], 16384)
+    w.compress_data(data, H.Lz4Compressor())
+    got, code, _ = check(w.finish())
+    assert code == 0 and got == data
+
+
 def test_int4_payload_in_default_blocks():
     # the example's on-disk layout: [f16 scales][nibbles], DType::I4, 16 KiB blocks
     rng = np.random.default_rng(11)
