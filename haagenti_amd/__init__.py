@@ -201,6 +201,8 @@ _sig("hh_spectral_encoded_size", _sz, [_u32, _u32, C.c_uint16, C.c_float, C.c_fl
 _sig("hh_spectral_encode_from_dct", _i32, [_vp, _u32, _u32, C.c_uint16, C.c_float, C.c_float, _vp,
                                            _sz, _vp, C.POINTER(_sz)])
 
+_sig("hh_hbm_copy", _i32, [_vp, _vp, _vp, C.c_uint64, _vp])
+
 # Every symbol include/haagenti_hip.h declares (checked by the tests).
 EXPORTS = [
     "hh_status_category", "hh_status_is_recoverable", "hh_version", "hh_device_count",
@@ -220,7 +222,7 @@ EXPORTS = [
     "hh_pool_recycle", "hh_pool_get_stats", "hh_pipeline_default_config", "hh_pipeline_create",
     "hh_pipeline_destroy", "hh_pipeline_streams", "hh_pipeline_next_staging", "hh_pipeline_submit",
     "hh_pipeline_wait", "hh_pipeline_stream_wait", "hh_pipeline_get_times", "hh_pipeline_finish",
-    "hh_pipeline_get_stats", "hh_pipeline_reset_stats",
+    "hh_pipeline_get_stats", "hh_pipeline_reset_stats", "hh_hbm_copy",
 ]
 
 CORRUPT_HEADER_CHECKSUM, CORRUPT_BLOCK_CHECKSUM, CORRUPT_QUANT_SCHEME = 6, 7, 8
@@ -1051,6 +1053,15 @@ def _hip_dct(self, d_in, rows, cols, d_out, stream=None):
     """Orthonormal 2-D DCT-II of a row-major rows x cols f32 device matrix
     (hh_dct_2d; GpuDctContext::dct_2d)."""
     _check(_lib.hh_dct_2d(self.handle, _addr(d_in), int(rows), int(cols), _addr(d_out), stream), "hh_dct_2d")
+
+
+def _hip_hbm_copy(self, d_dst, d_src, nbytes, stream=None):
+    """Streaming device copy of nbytes (hh_hbm_copy): the bandwidth
+    calibration kernel of the measurements."""
+    _check(_lib.hh_hbm_copy(self.handle, _addr(d_dst), _addr(d_src), int(nbytes), stream), "hh_hbm_copy")
+
+
+HipContext.hbm_copy = _hip_hbm_copy
 
 
 def _hip_idct(self, d_in, rows, cols, d_out, dtype=F32, stream=None):

@@ -95,6 +95,13 @@ void hh_context_destroy(hh_context *ctx);
 void *hh_context_stream(hh_context *ctx);
 int32_t hh_context_synchronize(hh_context *ctx);
 
+/* Streaming device-to-device copy of `bytes` bytes (non-overlapping ranges):
+ * no counterpart in the reference; it is the bandwidth calibration of this
+ * library's measurements (the rate a kernel that reads and writes every byte
+ * once can reach on the device, and the scale of the FETCH_SIZE /
+ * WRITE_SIZE counters).  Asynchronous on the stream. */
+int32_t hh_hbm_copy(hh_context *ctx, void *d_dst, const void *d_src, uint64_t bytes, void *stream);
+
 /* ---------------------------------------------------------------- LZ4 */
 
 /* Batched raw-LZ4 block decode, one wavefront per block.  Block i reads
