@@ -284,9 +284,22 @@ def wl_llama3_8b_layer(args, torch, H, O):
     t_lz4, t_tile = (Timed(torch, stream, args.steps * len(sampled)),
                      Timed(torch, stream, args.steps * len(sampled)))
 
+    fused = args.path == "fused"
+
     def run_layer(l, timed):
         L = layers_host[l % args.distinct]
         T = tabs[l % args.distinct]
+        if fused:
+            # the layer in one launch: LZ4 blocks -> tile bytes in LDS -> bf16
+            fdesc = [(t["rows"], t["cols"], k, outs[l][i]) for i, t in enumerate(L["tensors"])]
+            if timed and l % args.kernel_sample == 0:
+                e = t_tile.start()
+            rc = ctx.hctt_decode_lz4_fused(d_comp[l], d_comp[l].numel(), T["in_off"], T["in_len"], T["n"], status,
+                                           fdesc, tiles_per_block, dtype=H.BF16, stream=sp)
+            assert rc == H.OK
+            if timed and l % args.kernel_sample == 0:
+                t_tile.stop(e)
+            return
         s = scratch[l % 2]
         desc = [(s.data_ptr() + t["soff"], t["tlen"], t["rows"], t["cols"], k, outs[l][i])
                 for i, t in enumerate(L["tensors"])]
@@ -335,10 +348,15 @@ def wl_llama3_8b_layer(args, torch, H, O):
     value = out_bytes_layer * args.layers / (ms_step / 1e3) / 1e9
     in_tile = layers_host[0]["scratch_bytes"]
     comp_bytes = layers_host[0]["blob"].size
-    tile_s, lz4_s = t_tile.mean_s(), t_lz4.mean_s()
-    log(f"per layer: lz4 {lz4_s * 1e6:.1f} us ({(comp_bytes + in_tile) / lz4_s / 1e9:.0f} GB/s "
-        f"in+out), tiles {tile_s * 1e6:.1f} us ({(in_tile + out_bytes_layer) / tile_s / 1e9:.0f} "
-        f"GB/s in+out)")
+    tile_s = t_tile.mean_s()
+    lz4_s = t_lz4.mean_s() if not fused else None
+    if fused:
+        log(f"per layer: fused LZ4 + tiles {tile_s * 1e6:.1f} us ({(comp_bytes + out_bytes_layer) / tile_s / 1e9:.0f} "
+            f"GB/s compressed in + bf16 out; the {in_tile / 1e6:.1f} MB of tile bytes stay in LDS)")
+    else:
+        log(f"per layer: lz4 {lz4_s * 1e6:.1f} us ({(comp_bytes + in_tile) / lz4_s / 1e9:.0f} GB/s "
+            f"in+out), tiles {tile_s * 1e6:.1f} us ({(in_tile + out_bytes_layer) / tile_s / 1e9:.0f} "
+            f"GB/s in+out)")
     log("tile launch us min/median/max %.1f / %.1f / %.1f; sampled tile time per step (ms): %s" % (
         *t_tile.spread(), " ".join("%.2f" % (sum(a.elapsed_time(b) for a, b in
                                                   t_tile.pairs[i * len(sampled):(i + 1) * len(sampled)]))
@@ -358,14 +376,18 @@ def wl_llama3_8b_layer(args, torch, H, O):
                  "tile": 64, "tile_bytes": tb, "lz4_block_tiles": tiles_per_block,
                  "out_dtype": "bf16", "hct_bytes_per_layer": in_tile,
                  "lz4_bytes_per_layer": comp_bytes},
-                roofline("llama3-8b-layer", "hctt_decode_kernel<bf16>", in_tile + out_bytes_layer,
-                         tile_s),
+                (roofline("llama3-8b-layer:fused", "hctt_lz4_fused_kernel<bf16>", comp_bytes + out_bytes_layer,
+                          tile_s) if fused else
+                 roofline("llama3-8b-layer", "hctt_decode_kernel<bf16>", in_tile + out_bytes_layer, tile_s)),
                 cpu,
-                {"kernels_us": {"lz4_ring_kernel": round(lz4_s * 1e6, 2),
-                                "hctt_decode_kernel": round(tile_s * 1e6, 2)},
-                 "lz4_roofline": {"achieved": round((comp_bytes + in_tile) / lz4_s / 1e9, 1),
-                                  "frac": round((comp_bytes + in_tile) / lz4_s / 1e9 / HBM_PEAK_GBS, 4)},
-                 "spot_check_max_err_over_rms": check})
+                ({"path": "fused", "kernels_us": {"hctt_lz4_fused_kernel": round(tile_s * 1e6, 2)},
+                  "spot_check_max_err_over_rms": check} if fused else
+                 {"path": "two-launch",
+                  "kernels_us": {"lz4_ring_kernel": round(lz4_s * 1e6, 2),
+                                 "hctt_decode_kernel": round(tile_s * 1e6, 2)},
+                  "lz4_roofline": {"achieved": round((comp_bytes + in_tile) / lz4_s / 1e9, 1),
+                                   "frac": round((comp_bytes + in_tile) / lz4_s / 1e9 / HBM_PEAK_GBS, 4)},
+                  "spot_check_max_err_over_rms": check}))
 
 
 def wl_int4(args, torch, H, O):
@@ -921,6 +943,9 @@ def main():
                     help="llama70b-stream: read each layer from HCT v2 files (mmap) into pinned staging")
     ap.add_argument("--kernel-sample", type=int, default=8,
                     help="llama3-8b-layer: per-kernel events on every n-th layer of the timed steps")
+    ap.add_argument("--path", choices=["fused", "two-launch"], default="fused",
+                    help="llama3-8b-layer: one fused LZ4 + tile launch per layer (hh_hctt_decode_lz4_fused) "
+                         "or the LZ4 and tile launches through a scratch buffer (hh_hctt_decode_lz4_batch)")
     ap.add_argument("--lz4-block", type=int, default=16384,
                     help="LZ4 block size in bytes before rounding down to whole tiles "
                          "(the reference HctWriter default is 16 KiB)")

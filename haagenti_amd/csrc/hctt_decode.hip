@@ -44,8 +44,10 @@
 //   5. the output block is parked in LDS (reusing V's space) and written as
 //      coalesced 16-byte row segments.
 #include <cstring>
+#include <type_traits>
 
 #include "hh_internal.hpp"
+#include "lz4_ring.hpp"
 
 namespace hh {
 namespace {
@@ -132,6 +134,9 @@ typedef u32x2 __attribute__((address_space(3))) lds_u32x2;
 // fall into distinct banks.
 template <int DT>
 constexpr uint32_t kParkPitch = DT == HH_F32 ? 64u * 4u + 16u : 64u * 2u + 8u;
+// The same for one 32-column block of the tile.
+template <int DT>
+constexpr uint32_t kHalfPitch = DT == HH_F32 ? 32u * 4u + 16u : 32u * 2u + 8u;
 
 // Two outputs rounded to the 16-bit output type, packed low | high.
 template <int DT>
@@ -226,6 +231,266 @@ __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, i
     }
 }
 
+// One tile from its bytes in LDS (`pay`): steps 1-8 of the data flow above,
+// with this wave's V table / output park at LDS byte offset wbase (V is the
+// same area as a pointer).  `consumed` runs once the tile's bytes are no
+// longer read: right after the V table is built (HALF), or just before the
+// output stores (whole-tile park).
+template <int DT, bool HALF, typename Hook>
+__device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint32_t t, const uint8_t *pay,
+                                          uint32_t *V, uint32_t wbase, const u32x4 *mtab, int lane, float one,
+                                          int32_t n4, Hook &&consumed) {
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    const uint32_t k = B.k[ti], cols = B.cols[ti];
+    const uint32_t nsc = (k + 31) >> 5;
+    const uint32_t nib_off = 512 + 2 * nsc;
+
+    // 1. bitmap row `lane`: set-bit count and exclusive prefix over rows
+    const uint64_t bits = reinterpret_cast<const uint64_t *>(pay)[lane];
+    const uint32_t cnt = (uint32_t)__popcll(bits);
+    const uint32_t incl = wave_incl_sum(cnt);
+    const bool ok = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) == k;
+    const uint32_t pre = incl - cnt;
+
+    // 2. per-tile power-of-two prescale from the largest scale exponent
+    const uint16_t *sc16 = reinterpret_cast<const uint16_t *>(pay + 512);
+    uint32_t emax = 0;
+    for (uint32_t g = lane; g < nsc; g += 64) {
+        const uint32_t ex = ((uint32_t)sc16[g] >> 10) & 31u;
+        emax = ex > emax ? ex : emax;
+    }
+    emax = wave_max_u5(emax);
+    // coefficients are scaled by 2^E (|C 2^E| < 4); the basis carries 2^8
+    const int E = 13 - (int)emax;
+    const float pe = pow2f(E);
+
+    // 3. dense table of the retained coefficients, 8 per lane per pass:
+    //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E
+    //    exactly.  The scaled scale s = scale * 2^E (11 significant bits)
+    //    is split into s_hi (its top 8 bits) + s_lo (the other 3); with
+    //    |q - 8| <= 8 (at most 3 significant bits) both (q - 8) s_hi and
+    //    (q - 8) s_lo are exact f16 products, formed two at a time by
+    //    packed f16 multiplies.
+    if (ok) {
+        const uint16_t *nib16 = reinterpret_cast<const uint16_t *>(pay + nib_off);
+        for (uint32_t c8 = lane; 8 * c8 < k; c8 += 64) {
+            const uint32_t r0 = 8 * c8;
+            // nibbles r0 .. r0+7, low first (bytes past the tile's end
+            // are staged slack; their entries lie past V[k - 1])
+            const uint32_t n32 = (uint32_t)nib16[2 * c8] | ((uint32_t)nib16[2 * c8 + 1] << 16);
+            const float sf = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
+            const float shi = __uint_as_float(__float_as_uint(sf) & 0xffff0000u);
+            const half2v sc = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(shi, sf - shi));
+            uint32_t v[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // f16 (1024 + q) for nibbles e and e + 4, minus 1032
+                const uint32_t y = ((n32 >> (4 * e)) & 0x000f000fu) | 0x64006400u;
+                const half2v q = __builtin_bit_cast(half2v, y) - half2v{(_Float16)1032.0f, (_Float16)1032.0f};
+                v[e] = __builtin_bit_cast(uint32_t, half2v{q.x, q.x} * sc);
+                v[e + 4] = __builtin_bit_cast(uint32_t, half2v{q.y, q.y} * sc);
+            }
+            u32x4 *dst = reinterpret_cast<u32x4 *>(V + r0);
+            dst[0] = u32x4{v[0], v[1], v[2], v[3]};
+            dst[1] = u32x4{v[4], v[5], v[6], v[7]};
+        }
+    }
+    wave_sync();
+    // the tile's bytes have all been read (their values feed the V stores)
+    if constexpr (HALF) consumed();
+
+    // 4. GEMM1 A fragments.  A[upar][vpar][s] holds, for row
+    //    u = 2 l32 + upar, the columns v = 2 pi(16 s + 8 h + e) + vpar,
+    //    e = 0..7.  For fixed (upar, s) these are two runs of 8
+    //    consecutive columns, v0 = 32 s + 16 run + 8 h: even offsets feed
+    //    vpar 0, odd offsets vpar 1.
+    const uint64_t bits_r[2] = {__shfl(bits, 2 * l32), __shfl(bits, 2 * l32 + 1)};
+    const uint32_t pre_r[2] = {__shfl(pre, 2 * l32), __shfl(pre, 2 * l32 + 1)};
+    // 5. GEMM1 (even/odd halves of the column frequencies), one row
+    //    parity at a time so that only its A fragments are live:
+    //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
+    //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int up = 0; up < 2; up++) {
+        u32x4 ahi[2][2], alo[2][2];  // [vpar][s]
+        const uint64_t b64 = ok ? bits_r[up] : 0ull;
+        // the row shifted so that column 8 h is bit 0: every column this
+        // lane needs sits at a compile-time bit position
+        const uint64_t bh = b64 >> (8 * h);
+        const uint32_t wd[2] = {(uint32_t)bh, (uint32_t)(bh >> 32)};
+        const uint32_t rank_h = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << (8 * h)) - 1ull));
+        // LDS byte address of V[rank]; a column that is not retained
+        // masks it to 0, the zero word
+        uint32_t diff = wbase + 4 * rank_h;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int run = 0; run < 2; run++) {
+                const uint32_t word = wd[s];
+                uint32_t a[8];  // LDS address of each column's table entry, or 0
+#pragma unroll
+                for (int o = 0; o < 8; o++) {
+                    // all-ones when column 16 run + o of the word is retained
+                    const int32_t m = (int32_t)(word << (31 - (16 * run + o))) >> 31;
+                    a[o] = (uint32_t)m & diff;
+                    diff = (uint32_t)((int32_t)diff + m * n4);  // v_mad_i32_i24
+                }
+                // columns 16 run + 8 .. 16 run + 15 of this word belong to the
+                // other lane half
+                diff += (uint32_t)__popc((word >> (16 * run + 8)) & 0xffu) << 2;
+                // dword p of a fragment packs elements e = 2p, 2p + 1 (this run
+                // supplies e = 4 run .. 4 run + 3, at offsets 2 (e - 4 run) + vpar);
+                // a table entry is f16 hi | f16 lo << 16
+                uint32_t w[8];
+#pragma unroll
+                for (int o = 0; o < 8; o++) w[o] = lds_load(a[o]);
+#pragma unroll
+                for (int vp = 0; vp < 2; vp++) {
+                    ahi[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
+                    alo[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
+                    ahi[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
+                    alo[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
+                }
+            }
+        }
+#pragma unroll
+        for (int vp = 0; vp < 2; vp++) {
+            acc[up][vp] = floatx16{};
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
+                const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
+                acc[up][vp] = mfma(ahi[vp][s], mh, acc[up][vp]);
+                acc[up][vp] = mfma(ahi[vp][s], ml, acc[up][vp]);
+                acc[up][vp] = mfma(alo[vp][s], mh, acc[up][vp]);
+                acc[up][vp] = mfma(alo[vp][s], ml, acc[up][vp]);
+            }
+        }
+    }
+    wave_sync();
+
+    // 6. butterfly in place: acc[upar][0] = E + O = S[u][n],
+    //    acc[upar][1] = E - O = S[u][63 - n]
+#pragma unroll
+    for (int up = 0; up < 2; up++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float e = acc[up][0][r], o = acc[up][1][r];
+            acc[up][0][r] = e + o;
+            acc[up][1][r] = e - o;
+        }
+    }
+
+    // 7. GEMM2 transposed, per S column block jb (jb = 0: j = n;
+    //    jb = 1: j = 63 - n): X^T[j][i] = sum_u S[u][j] M[u][i], with S
+    //    (GEMM1's accumulators) as the A operand and the M fragments as B,
+    //    split by u parity into E2 (upar 0) and O2 (upar 1).  Lane l32 then
+    //    holds output rows i = l32 and 63 - i (X[63 - i][j] = E2 - O2) and
+    //    register r the column j = (r & 3) + 8 (r >> 2) + 4 h (or 63 minus
+    //    it): four consecutive columns per register quad, parked in LDS as
+    //    one 8-byte (16-bit outputs) or 16-byte (f32) write per row.  The
+    //    park holds the whole tile (HALF false: stored once, 16 bytes per
+    //    lane over whole rows) or one column block (HALF: stored after each
+    //    block, half the LDS).
+    const float os = pow2f(-(E + 16));
+    constexpr uint32_t pitch = HALF ? kHalfPitch<DT> : kParkPitch<DT>;
+    const uint32_t i_lo = wbase + (uint32_t)l32 * pitch;
+    const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * pitch;
+    constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
+    const uint32_t tpr = B.tiles_per_row[ti];
+    const uint32_t tr = t / tpr, tc = t % tpr;
+    const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
+    // row stores of columns [c0, c0 + ncols) from the park (16 bytes per lane)
+    auto store = [&](uint32_t c0, auto ncolc) {
+        constexpr uint32_t ncols = decltype(ncolc)::value;
+        constexpr uint32_t per_row = ncols * esz / 16;  // lanes per row
+        constexpr uint32_t rows_per = 64 / per_row;     // rows per instruction
+        const uint32_t rsub = (uint32_t)lane / per_row, csub = (uint32_t)lane % per_row;
+#pragma unroll
+        for (uint32_t it = 0; it < 64 / rows_per; it++) {
+            const uint32_t row = rows_per * it + rsub;
+            const uint32_t a0 = wbase + row * pitch + 16 * csub;
+            u32x4 v;
+            if constexpr (DT == HH_F32) {
+                v = *(lds_u32x4 *)(size_t)a0;
+            } else {
+                // rows are 8-byte aligned in the park: two 8-byte reads
+                const u32x2 lo = *(lds_u32x2 *)(size_t)a0, hi = *(lds_u32x2 *)(size_t)(a0 + 8);
+                v = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
+            uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[ti] + esz * (base + (size_t)row * cols + c0);
+            *(u32x4 HH_GLOBAL *)(o + 16 * csub) = v;
+        }
+    };
+#pragma unroll
+    for (int jb = 0; jb < 2; jb++) {
+        floatx16 x2[2];
+        x2[0] = floatx16{};
+        x2[1] = floatx16{};
+#pragma unroll
+        for (int up = 0; up < 2; up++) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                u32x4 shi, slo;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int r0 = 8 * s + 2 * p;
+                    uint32_t hp, lp;
+                    split2(acc[up][jb][r0], acc[up][jb][r0 + 1], one, hp, lp);
+                    shi[p] = hp;
+                    slo[p] = lp;
+                }
+                const u32x4 mh = mtab[((0 * 2 + up) * 2 + s) * 64 + lane];
+                const u32x4 ml = mtab[((1 * 2 + up) * 2 + s) * 64 + lane];
+                x2[up] = mfma(shi, mh, x2[up]);
+                x2[up] = mfma(shi, ml, x2[up]);
+                x2[up] = mfma(slo, mh, x2[up]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float va[4], vc[4];  // rows i and 63 - i, columns ascending
+#pragma unroll
+            for (int t4 = 0; t4 < 4; t4++) {
+                const int r = 4 * q + (jb == 0 ? t4 : 3 - t4);
+                const float o2 = x2[1][r] * os;
+                va[t4] = __builtin_fmaf(x2[0][r], os, o2);
+                vc[t4] = __builtin_fmaf(x2[0][r], os, -o2);
+            }
+            // first of the four columns (relative to 32 jb in a half park)
+            const uint32_t jabs = jb == 0 ? 8 * q + 4 * h : 60 - 8 * q - 4 * h;
+            const uint32_t j0 = HALF ? jabs - 32u * jb : jabs;
+            if constexpr (DT == HH_F32) {
+                *(lds_u32x4 *)(size_t)(i_lo + esz * j0) =
+                    u32x4{__float_as_uint(va[0]), __float_as_uint(va[1]), __float_as_uint(va[2]),
+                          __float_as_uint(va[3])};
+                *(lds_u32x4 *)(size_t)(i_hi + esz * j0) =
+                    u32x4{__float_as_uint(vc[0]), __float_as_uint(vc[1]), __float_as_uint(vc[2]),
+                          __float_as_uint(vc[3])};
+            } else {
+                *(lds_u32x2 *)(size_t)(i_lo + esz * j0) = u32x2{pack2<DT>(va[0], va[1]), pack2<DT>(va[2], va[3])};
+                *(lds_u32x2 *)(size_t)(i_hi + esz * j0) = u32x2{pack2<DT>(vc[0], vc[1]), pack2<DT>(vc[2], vc[3])};
+            }
+        }
+        if constexpr (HALF) {
+            wave_sync();
+            // 8. coalesced row stores of this column block
+            store(32u * jb, std::integral_constant<uint32_t, 32>{});
+            wave_sync();  // the next block's park overwrites this one
+        }
+    }
+    if constexpr (!HALF) {
+        wave_sync();
+        consumed();
+        // 8. coalesced row stores (16 bytes per lane)
+        store(0u, std::integral_constant<uint32_t, 64>{});
+    }
+    if (B.status[ti] != nullptr && lane == 0)
+        ((int32_t HH_GLOBAL *)B.status[ti])[t] = ok ? HH_OK : HH_ERR_CORRUPTED_DATA;
+}
+
 template <int DT, bool DW, int NP>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_decode_kernel(TileBatch Bk,
                                                                    const u32x4 *__restrict__ basis) {
@@ -265,9 +530,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
         uint32_t ti = 0;
         while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
         const uint32_t t = gt - B.start[ti];
-        const uint32_t k = B.k[ti], cols = B.cols[ti];
-        const uint32_t nsc = (k + 31) >> 5;
-        const uint32_t nib_off = 512 + 2 * nsc;
 
         // This tile's bytes are staged in LDS.  Fetch the next tile now; it is
         // staged at the end of this iteration, long after the loads landed
@@ -277,236 +539,257 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
         prefetch_tile<DW, NP>(B, has_next ? gt + stride : gt, lane, pf);
         wave_sync();
 
-        // 1. bitmap row `lane`: set-bit count and exclusive prefix over rows
-        const uint64_t bits = reinterpret_cast<const uint64_t *>(pay)[lane];
-        const uint32_t cnt = (uint32_t)__popcll(bits);
-        const uint32_t incl = wave_incl_sum(cnt);
-        const bool ok = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) == k;
-        const uint32_t pre = incl - cnt;
-
-        // 2. per-tile power-of-two prescale from the largest scale exponent
-        const uint16_t *sc16 = reinterpret_cast<const uint16_t *>(pay + 512);
-        uint32_t emax = 0;
-        for (uint32_t g = lane; g < nsc; g += 64) {
-            const uint32_t ex = ((uint32_t)sc16[g] >> 10) & 31u;
-            emax = ex > emax ? ex : emax;
-        }
-        emax = wave_max_u5(emax);
-        // coefficients are scaled by 2^E (|C 2^E| < 4); the basis carries 2^8
-        const int E = 13 - (int)emax;
-        const float pe = pow2f(E);
-
-        // 3. dense table of the retained coefficients, 8 per lane per pass:
-        //    V[r] = hi | lo << 16 with hi + lo = (q_r - 8) * scale * 2^E
-        //    exactly.  The scaled scale s = scale * 2^E (11 significant bits)
-        //    is split into s_hi (its top 8 bits) + s_lo (the other 3); with
-        //    |q - 8| <= 8 (at most 3 significant bits) both (q - 8) s_hi and
-        //    (q - 8) s_lo are exact f16 products, formed two at a time by
-        //    packed f16 multiplies.
-        if (ok) {
-            const uint16_t *nib16 = reinterpret_cast<const uint16_t *>(pay + nib_off);
-            for (uint32_t c8 = lane; 8 * c8 < k; c8 += 64) {
-                const uint32_t r0 = 8 * c8;
-                // nibbles r0 .. r0+7, low first (bytes past the tile's end
-                // are staged slack; their entries lie past V[k - 1])
-                const uint32_t n32 = (uint32_t)nib16[2 * c8] | ((uint32_t)nib16[2 * c8 + 1] << 16);
-                const float sf = (float)__builtin_bit_cast(_Float16, sc16[r0 >> 5]) * pe;
-                const float shi = __uint_as_float(__float_as_uint(sf) & 0xffff0000u);
-                const half2v sc = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(shi, sf - shi));
-                uint32_t v[8];
+        tile_body<DT, false>(B, ti, t, pay, V, wbase, mtab, lane, one, n4, [&]() {
+            // stage the next tile's bytes (the current ones are no longer needed)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    // f16 (1024 + q) for nibbles e and e + 4, minus 1032
-                    const uint32_t y = ((n32 >> (4 * e)) & 0x000f000fu) | 0x64006400u;
-                    const half2v q = __builtin_bit_cast(half2v, y) - half2v{(_Float16)1032.0f, (_Float16)1032.0f};
-                    v[e] = __builtin_bit_cast(uint32_t, half2v{q.x, q.x} * sc);
-                    v[e + 4] = __builtin_bit_cast(uint32_t, half2v{q.y, q.y} * sc);
-                }
-                u32x4 *dst = reinterpret_cast<u32x4 *>(V + r0);
-                dst[0] = u32x4{v[0], v[1], v[2], v[3]};
-                dst[1] = u32x4{v[4], v[5], v[6], v[7]};
-            }
-        }
+            for (int i = 0; i < NP; i++)
+                *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
+        });
         wave_sync();
+    }
+}
 
-        // 4. GEMM1 A fragments.  A[upar][vpar][s] holds, for row
-        //    u = 2 l32 + upar, the columns v = 2 pi(16 s + 8 h + e) + vpar,
-        //    e = 0..7.  For fixed (upar, s) these are two runs of 8
-        //    consecutive columns, v0 = 32 s + 16 run + 8 h: even offsets feed
-        //    vpar 0, odd offsets vpar 1.
-        const uint64_t bits_r[2] = {__shfl(bits, 2 * l32), __shfl(bits, 2 * l32 + 1)};
-        const uint32_t pre_r[2] = {__shfl(pre, 2 * l32), __shfl(pre, 2 * l32 + 1)};
-        // 5. GEMM1 (even/odd halves of the column frequencies), one row
-        //    parity at a time so that only its A fragments are live:
-        //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
-        //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
-        floatx16 acc[2][2];
-#pragma unroll
-        for (int up = 0; up < 2; up++) {
-            u32x4 ahi[2][2], alo[2][2];  // [vpar][s]
-            const uint64_t b64 = ok ? bits_r[up] : 0ull;
-            // the row shifted so that column 8 h is bit 0: every column this
-            // lane needs sits at a compile-time bit position
-            const uint64_t bh = b64 >> (8 * h);
-            const uint32_t wd[2] = {(uint32_t)bh, (uint32_t)(bh >> 32)};
-            const uint32_t rank_h = pre_r[up] + (uint32_t)__popcll(b64 & ((1ull << (8 * h)) - 1ull));
-            // LDS byte address of V[rank]; a column that is not retained
-            // masks it to 0, the zero word
-            uint32_t diff = wbase + 4 * rank_h;
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-#pragma unroll
-                for (int run = 0; run < 2; run++) {
-                    const uint32_t word = wd[s];
-                    uint32_t a[8];  // LDS address of each column's table entry, or 0
-#pragma unroll
-                    for (int o = 0; o < 8; o++) {
-                        // all-ones when column 16 run + o of the word is retained
-                        const int32_t m = (int32_t)(word << (31 - (16 * run + o))) >> 31;
-                        a[o] = (uint32_t)m & diff;
-                        diff = (uint32_t)((int32_t)diff + m * n4);  // v_mad_i32_i24
-                    }
-                    // columns 16 run + 8 .. 16 run + 15 of this word belong to the
-                    // other lane half
-                    diff += (uint32_t)__popc((word >> (16 * run + 8)) & 0xffu) << 2;
-                    // dword p of a fragment packs elements e = 2p, 2p + 1 (this run
-                    // supplies e = 4 run .. 4 run + 3, at offsets 2 (e - 4 run) + vpar);
-                    // a table entry is f16 hi | f16 lo << 16
-                    uint32_t w[8];
-#pragma unroll
-                    for (int o = 0; o < 8; o++) w[o] = lds_load(a[o]);
-#pragma unroll
-                    for (int vp = 0; vp < 2; vp++) {
-                        ahi[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
-                        alo[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
-                        ahi[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
-                        alo[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
-                    }
-                }
-            }
-#pragma unroll
-            for (int vp = 0; vp < 2; vp++) {
-                acc[up][vp] = floatx16{};
-#pragma unroll
-                for (int s = 0; s < 2; s++) {
-                    const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
-                    const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
-                    acc[up][vp] = mfma(ahi[vp][s], mh, acc[up][vp]);
-                    acc[up][vp] = mfma(ahi[vp][s], ml, acc[up][vp]);
-                    acc[up][vp] = mfma(alo[vp][s], mh, acc[up][vp]);
-                    acc[up][vp] = mfma(alo[vp][s], ml, acc[up][vp]);
-                }
-            }
+// ---- LZ4 blocks and their tiles in one launch ------------------------------
+//
+// One persistent workgroup per CU takes a contiguous range of the launch's
+// LZ4 blocks, each holding whole tiles of one tensor (block j of tensor i:
+// tiles [j tpb, j tpb + tpb) of it, the last block the rest).  Its first np
+// waves are producers: producer p decodes blocks p, p + np, p + 2 np, ... of
+// the range with the LDS-ring decoder (lz4_ring.hpp, the whole output kept in
+// LDS: at most kFusedMax bytes) into a ring of nbuf block buffers (block i of
+// the range into buffer i mod nbuf).  The other nc waves are consumers:
+// consumer c decodes tiles c, c + nc, c + 2 nc, ... of the range, in that
+// order, straight from the buffers with tile_body (one 32-column block of the
+// output parked at a time).  The tile bytes never reach HBM, and the LZ4
+// parse of later blocks runs while the consumers work on earlier ones.
+//
+// Two LDS words per buffer order the two sides:
+//   ready[x]  1 + the number of the block the buffer holds, stored by its
+//             producer once the bytes are in LDS;
+//   done[x]   how many of that block's tiles have been read, counted by the
+//             consumers; a producer refills buffer x with block i only once
+//             done[x] equals the tile count of block i - nbuf, and clears it
+//             before publishing block i.
+// No wait can deadlock: the lowest-numbered block not yet decoded waits only
+// for the tiles of an earlier (decoded) block, whose consumers wait only for
+// blocks before those tiles, all decoded.  Every wait is bounded all the same
+// (kSpinLimit polls); one that runs out (not expected) raises the
+// workgroup's abort word, every wave of the workgroup then leaves, and the
+// block record of the block waited on reports HH_ERR_DEVICE.
+//
+// A block that fails (status as the batched LZ4 kernel writes it) or decodes
+// to fewer bytes than its tiles take leaves the rest zeroed: those tiles fail
+// their bitmap count (tile status HH_ERR_CORRUPTED_DATA, zeros out).
+// The input stage holds a whole block's compressed bytes (LZ4's worst case
+// for kFusedMax bytes, 16,432, plus 15 bytes of misalignment and the 256-byte
+// window), so each block is staged with one batch of loads.
+constexpr uint32_t kFusedStageData = 17 * 1024;
+using FusedRing = ring::RingDec<16384, kFusedStageData, true>;
+constexpr uint32_t kFusedMax = 16384 - 32;
+constexpr uint32_t kFusedBuf = 16384;  // a block buffer: the decoder's ring
+constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a producer's input stage
+constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: tile_body's register budget
+constexpr int kFusedProducers = 2;
+constexpr uint32_t kFusedMaxBufs = 8;
+constexpr uint32_t kFusedLdsMax = 160u * 1024u;
+constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
+
+struct FusedBlocks {
+    const uint8_t *in;
+    uint64_t in_total;
+    const uint64_t *in_off;  // indexed by global block number
+    const uint32_t *in_len;
+    hh_block_status *status;
+    uint32_t blk_base;                    // global number of this launch's block 0
+    uint32_t blk_start[kMaxTensors + 1];  // first block of each tensor, launch-relative
+    uint32_t tpb;                         // tiles per block
+    uint32_t np, nbuf;                    // producer waves, block buffers
+    uint32_t stage_off, buf_off;          // LDS byte offsets of the stages and the buffers
+};
+
+// Workgroup LDS layout after the shared part: [block descriptor][ready[8],
+// done[8], abort][consumer areas][producer stages][block buffers].
+constexpr uint32_t kFusedFOff = kSharedBytes;
+constexpr uint32_t kFusedFlagsOff = kFusedFOff + ((sizeof(FusedBlocks) + 15u) & ~15u);
+constexpr uint32_t kFusedFlagWords = 2 * kFusedMaxBufs + 1;
+constexpr uint32_t kFusedConsOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
+
+typedef uint32_t __attribute__((address_space(3))) lds_word;
+
+// Polls the LDS word at `w` until it reads `want` (true), or the abort word
+// is raised or the poll limit runs out (false; the latter raises it).
+__device__ __forceinline__ bool fused_wait(uint32_t w, uint32_t want, uint32_t abort_w, int lane) {
+    for (uint32_t it = 0;; it++) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)__hip_atomic_load((lds_word *)(size_t)w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (v == want) return true;
+        const uint32_t ab = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)__hip_atomic_load((lds_word *)(size_t)abort_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (ab != 0) return false;
+        if (it == kSpinLimit) {
+            if (lane == 0)
+                __hip_atomic_store((lds_word *)(size_t)abort_w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return false;
         }
-        wave_sync();
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
 
-        // 6. butterfly in place: acc[upar][0] = E + O = S[u][n],
-        //    acc[upar][1] = E - O = S[u][63 - n]
-#pragma unroll
-        for (int up = 0; up < 2; up++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float e = acc[up][0][r], o = acc[up][1][r];
-                acc[up][0][r] = e + o;
-                acc[up][1][r] = e - o;
-            }
+template <int DT>
+__global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(TileBatch Bk, FusedBlocks Fk,
+                                                                              const u32x4 *__restrict__ basis) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    // wave-uniform (scalar) wave number: roles and block choices are scalar
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t nthr = blockDim.x;
+    u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(TileBatch) / 4); i += nthr)
+        reinterpret_cast<uint32_t *>(smem + kBatchOff)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(FusedBlocks) / 4); i += nthr)
+        reinterpret_cast<uint32_t *>(smem + kFusedFOff)[i] = reinterpret_cast<const uint32_t *>(&Fk)[i];
+    for (uint32_t i = threadIdx.x; i < kMTabBytes / 16; i += nthr) mtab[i] = basis[i];
+    if (threadIdx.x < kFusedFlagWords) reinterpret_cast<uint32_t *>(smem + kFusedFlagsOff)[threadIdx.x] = 0u;
+    if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();  // the only workgroup barrier: the two roles never meet at one
+    const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem + kBatchOff);
+    // the LDS copy serves the indexed block table; pointers come from the
+    // kernel arguments, where the compiler knows them to be global
+    const FusedBlocks &F = *reinterpret_cast<const FusedBlocks *>(smem + kFusedFOff);
+    const uint32_t ready_w = kFusedFlagsOff, done_w = kFusedFlagsOff + 4 * kFusedMaxBufs;
+    const uint32_t abort_w = kFusedFlagsOff + 8 * kFusedMaxBufs;
+    const uint32_t nblk = F.blk_start[B.n];
+    const uint32_t b_lo = (uint32_t)((uint64_t)nblk * blockIdx.x / gridDim.x);
+    const uint32_t b_hi = (uint32_t)((uint64_t)nblk * (blockIdx.x + 1) / gridDim.x);
+    const uint32_t np = Fk.np, nbuf = Fk.nbuf, nc = (nthr >> 6) - np;
+
+    // block lb -> tensor, first tile, tile count
+    auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
+        ti = 0;
+        while (ti + 1 < B.n && lb >= F.blk_start[ti + 1]) ti++;
+        t0 = (lb - F.blk_start[ti]) * F.tpb;
+        nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
+    };
+    auto report = [&](uint32_t lb) {  // a wait ran out
+        if (lane == 0) {
+            hh_block_status st;
+            st.code = HH_ERR_DEVICE;
+            st.detail = HH_CORRUPT_NONE;
+            st.position = 0;
+            st.required = 0;
+            st.written = 0;
+            ((hh_block_status *)Fk.status)[Fk.blk_base + lb] = st;
         }
+    };
 
-        // 7. GEMM2 transposed, per S column block jb (jb = 0: j = n;
-        //    jb = 1: j = 63 - n): X^T[j][i] = sum_u S[u][j] M[u][i], with S
-        //    (GEMM1's accumulators) as the A operand and the M fragments as B,
-        //    split by u parity into E2 (upar 0) and O2 (upar 1).  Lane l32 then
-        //    holds output rows i = l32 and 63 - i (X[63 - i][j] = E2 - O2) and
-        //    register r the column j = (r & 3) + 8 (r >> 2) + 4 h (or 63 minus
-        //    it): four consecutive columns per register quad, parked in LDS as
-        //    one 8-byte (16-bit outputs) or 16-byte (f32) write per row.
-        const float os = pow2f(-(E + 16));
-        const uint32_t i_lo = wbase + (uint32_t)l32 * kParkPitch<DT>;
-        const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * kParkPitch<DT>;
-        constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
-#pragma unroll
-        for (int jb = 0; jb < 2; jb++) {
-            floatx16 x2[2];
-            x2[0] = floatx16{};
-            x2[1] = floatx16{};
-#pragma unroll
-            for (int up = 0; up < 2; up++) {
-#pragma unroll
-                for (int s = 0; s < 2; s++) {
-                    u32x4 shi, slo;
-#pragma unroll
-                    for (int p = 0; p < 4; p++) {
-                        const int r0 = 8 * s + 2 * p;
-                        uint32_t hp, lp;
-                        split2(acc[up][jb][r0], acc[up][jb][r0 + 1], one, hp, lp);
-                        shi[p] = hp;
-                        slo[p] = lp;
-                    }
-                    const u32x4 mh = mtab[((0 * 2 + up) * 2 + s) * 64 + lane];
-                    const u32x4 ml = mtab[((1 * 2 + up) * 2 + s) * 64 + lane];
-                    x2[up] = mfma(shi, mh, x2[up]);
-                    x2[up] = mfma(shi, ml, x2[up]);
-                    x2[up] = mfma(slo, mh, x2[up]);
+    if (wave < np) {
+        // ---- producer
+        uint8_t *stage = smem + Fk.stage_off + wave * kFusedStage + FusedRing::kSFront;
+        for (uint32_t lb = b_lo + wave; lb < b_hi; lb += np) {
+            const uint32_t x = (lb - b_lo) % nbuf;
+            if (lb - b_lo >= nbuf) {  // the buffer's previous block must be read
+                uint32_t pti, pt0, pnt;
+                locate(lb - nbuf, pti, pt0, pnt);
+                if (!fused_wait(done_w + 4 * x, pnt, abort_w, lane)) {
+                    report(lb);
+                    break;
                 }
             }
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float va[4], vc[4];  // rows i and 63 - i, columns ascending
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int r = 4 * q + (jb == 0 ? t : 3 - t);
-                    const float o2 = x2[1][r] * os;
-                    va[t] = __builtin_fmaf(x2[0][r], os, o2);
-                    vc[t] = __builtin_fmaf(x2[0][r], os, -o2);
-                }
-                // first of the four columns
-                const uint32_t j0 = jb == 0 ? 8 * q + 4 * h : 60 - 8 * q - 4 * h;
-                if constexpr (DT == HH_F32) {
-                    *(lds_u32x4 *)(size_t)(i_lo + esz * j0) =
-                        u32x4{__float_as_uint(va[0]), __float_as_uint(va[1]), __float_as_uint(va[2]),
-                              __float_as_uint(va[3])};
-                    *(lds_u32x4 *)(size_t)(i_hi + esz * j0) =
-                        u32x4{__float_as_uint(vc[0]), __float_as_uint(vc[1]), __float_as_uint(vc[2]),
-                              __float_as_uint(vc[3])};
-                } else {
-                    *(lds_u32x2 *)(size_t)(i_lo + esz * j0) = u32x2{pack2<DT>(va[0], va[1]), pack2<DT>(va[2], va[3])};
-                    *(lds_u32x2 *)(size_t)(i_hi + esz * j0) = u32x2{pack2<DT>(vc[0], vc[1]), pack2<DT>(vc[2], vc[3])};
-                }
+            if (lane == 0)
+                __hip_atomic_store((lds_word *)(size_t)(done_w + 4 * x), 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            uint32_t ti, t0, nt;
+            locate(lb, ti, t0, nt);
+            const uint32_t cap = nt * B.tb[ti];
+            uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+            const uint32_t gb = Fk.blk_base + lb;
+            int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
+            uint64_t pos = 0, req = 0;
+            const uint64_t ioff = Fk.in_off[gb];
+            const uint32_t ilen = Fk.in_len[gb];
+            FusedRing d;
+            d.ring = rbuf;
+            d.stage = stage;
+            d.gbuf = Fk.in;
+            d.gsz = Fk.in_total;
+            d.ioff = ioff;
+            d.a0 = 0;
+            d.obase = nullptr;
+            d.cap = cap;
+            d.sb = 0;
+            d.at_end = false;
+            d.wso = ring::kNoWin;
+            d.w = 0;
+            d.op = 0;
+            d.fl = 0;
+            // a copy of the lane number the compiler cannot see through: the
+            // decoder's lane-derived addresses are then computed per block
+            // instead of being hoisted out of the loop and held in registers
+            int dl = lane;
+            asm volatile("" : "+v"(dl));
+            d.lane = dl;
+            if (ioff > Fk.in_total || (uint64_t)ilen > Fk.in_total - ioff) {
+                code = HH_ERR_INVALID_ARGUMENT;
+            } else {
+                ring::parse_block(d, ilen, code, detail, pos, req);
             }
+            // bytes of the block's tiles that were not produced read as zeros
+            const uint32_t good = code == HH_OK ? d.op : 0u;
+            if (good < cap) {
+                wave_sync();
+                wave_zero_fill(rbuf + good, cap - good, lane);
+            }
+            if (lane == 0) {
+                hh_block_status st;
+                st.code = code;
+                st.detail = detail;
+                st.position = pos;
+                st.required = req;
+                st.written = good;
+                ((hh_block_status *)Fk.status)[gb] = st;
+            }
+            wave_sync();  // every lane's buffer writes are issued before the release
+            if (lane == 0)
+                __hip_atomic_store((lds_word *)(size_t)(ready_w + 4 * x), lb + 1u, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        wave_sync();
-
-        // stage the next tile's bytes (the current ones are no longer needed)
-#pragma unroll
-        for (int i = 0; i < NP; i++)
-            *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
-
-        // 8. coalesced row stores (16 bytes per lane)
-        const uint32_t tpr = B.tiles_per_row[ti];
-        const uint32_t tr = t / tpr, tc = t % tpr;
-        const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
-        if constexpr (DT == HH_F32) {
-            float HH_GLOBAL *o = (float HH_GLOBAL *)B.out[ti] + base;
-#pragma unroll
-            for (int it = 0; it < 16; it++) {
-                const int row = 4 * it + (lane >> 4), c4 = (lane & 15) * 4;
-                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c4) =
-                    *(lds_u32x4 *)(size_t)(wbase + row * kParkPitch<DT> + 4 * c4);
+    } else {
+        // ---- consumer
+        const uint32_t c = wave - np;
+        const float one = Bk.one;
+        const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
+        const uint32_t wbase = kFusedConsOff + c * B.wave_lds;
+        uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
+        // tile `off` of block lb of the range: this wave's next one
+        uint32_t lb = b_lo, off = c, ti = 0, t0 = 0, nt = 0;
+        if (lb < b_hi) locate(lb, ti, t0, nt);
+        for (;;) {
+            while (lb < b_hi && off >= nt) {
+                off -= nt;
+                lb++;
+                if (lb < b_hi) locate(lb, ti, t0, nt);
             }
-        } else {
-            uint16_t HH_GLOBAL *o = (uint16_t HH_GLOBAL *)B.out[ti] + base;
-#pragma unroll
-            for (int it = 0; it < 8; it++) {
-                const int row = 8 * it + (lane >> 3), c8 = (lane & 7) * 8;
-                // rows are 8-byte aligned in the park: two 8-byte reads
-                const uint32_t a0 = wbase + row * kParkPitch<DT> + 2 * c8;
-                const u32x2 lo = *(lds_u32x2 *)(size_t)a0, hi = *(lds_u32x2 *)(size_t)(a0 + 8);
-                *(u32x4 HH_GLOBAL *)(o + (size_t)row * cols + c8) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            if (lb >= b_hi) break;
+            const uint32_t x = (lb - b_lo) % nbuf;
+            if (!fused_wait(ready_w + 4 * x, lb + 1u, abort_w, lane)) {
+                report(lb);
+                break;
             }
+            const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+            // an opaque copy of the lane number: the lane-derived addresses
+            // of tile_body are recomputed per tile rather than held (spilled)
+            // across the loop
+            int tl = lane;
+            asm volatile("" : "+v"(tl));
+            tile_body<DT, true>(B, ti, t0 + off, rbuf + off * B.tb[ti], V, wbase, mtab, tl, one, n4, [&]() {
+                // count the tile's bytes as read (their LDS reads complete)
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                if (lane == 0)
+                    __hip_atomic_fetch_add((lds_word *)(size_t)(done_w + 4 * x), 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            });
+            off += nc;
         }
-        if (B.status[ti] != nullptr && lane == 0)
-            ((int32_t HH_GLOBAL *)B.status[ti])[t] = ok ? HH_OK : HH_ERR_CORRUPTED_DATA;
-        wave_sync();
     }
 }
 
@@ -599,5 +882,96 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
     }
     return hipSuccess;
 }
+
+
+hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint32_t tpb, const uint8_t *d_in,
+                                 uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
+                                 hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
+                                 hipStream_t s) {
+    uint32_t blk = 0;  // global block number of the next tensor's first block
+    for (uint32_t i = 0; i < n;) {
+        TileBatch B;
+        FusedBlocks F;
+        std::memset(&B, 0, sizeof(B));
+        std::memset(&F, 0, sizeof(F));
+        F.in = d_in;
+        F.in_total = in_total;
+        F.in_off = d_in_off;
+        F.in_len = d_in_len;
+        F.status = d_status;
+        F.blk_base = blk;
+        F.tpb = tpb;
+        uint32_t max_k = 0, total = 0, nb = 0;
+        for (; i < n && B.n < (uint32_t)kMaxTensors; i++) {
+            const hh_hctt_tensor &T = tensors[i];
+            const uint32_t nt = (T.rows / 64) * (T.cols / 64);
+            if (nt == 0) continue;
+            const uint32_t j = B.n++;
+            B.out[j] = T.d_out;
+            B.status[j] = T.d_tile_status;
+            B.start[j] = total;
+            B.tiles_per_row[j] = T.cols / 64;
+            B.cols[j] = T.cols;
+            B.k[j] = T.k;
+            B.tb[j] = (uint32_t)hh_hctt_tile_bytes(T.k);
+            F.blk_start[j] = nb;
+            total += nt;
+            nb += (nt + tpb - 1) / tpb;
+            max_k = T.k > max_k ? T.k : max_k;
+        }
+        if (B.n == 0) continue;
+        B.start[B.n] = total;
+        F.blk_start[B.n] = nb;
+        B.one = 1.0f;
+        B.neg4 = -4;
+        // per consumer: the V table shares space with one parked column block
+        const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);
+        const uint32_t obytes = 64 * (dtype == HH_F32 ? kHalfPitch<HH_F32> : kHalfPitch<HH_BF16>);
+        B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
+        B.wave_lds = B.vo_bytes;
+        // one workgroup per CU: kFusedMaxWaves waves (fewer consumers when
+        // their areas leave room for fewer than 3 block buffers)
+        F.np = kFusedProducers;
+        uint32_t nc = kFusedMaxWaves - kFusedProducers, nbuf = 0;
+        const uint32_t fixed = kFusedConsOff + F.np * kFusedStage;
+        for (;;) {
+            const uint32_t used = fixed + nc * B.wave_lds;
+            nbuf = used < kFusedLdsMax ? (kFusedLdsMax - used) / kFusedBuf : 0u;
+            if (nbuf >= 3 || nc == 1) break;
+            nc--;
+        }
+        if (nbuf < 2) return hipErrorInvalidValue;  // not reached: tiles are at most 3 KiB (k <= 4096)
+        if (nbuf > kFusedMaxBufs) nbuf = kFusedMaxBufs;
+        F.nbuf = nbuf;
+        F.stage_off = kFusedConsOff + nc * B.wave_lds;
+        F.buf_off = F.stage_off + F.np * kFusedStage;
+        const uint32_t lds = F.buf_off + nbuf * kFusedBuf;
+        const uint32_t threads = 64u * (F.np + nc);
+        uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256);
+        if (grid > nb) grid = nb;
+        const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
+        hipError_t e = hipSuccess;
+#define HH_LAUNCH_FUSED(DTV)                                                                                \
+    do {                                                                                                    \
+        e = hipFuncSetAttribute((const void *)hctt_lz4_fused_kernel<DTV>,                                   \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
+        if (e != hipSuccess) return e;                                                                      \
+        hipLaunchKernelGGL((hctt_lz4_fused_kernel<DTV>), dim3(grid), dim3(threads), lds, s, B, F, basis);       \
+    } while (0)
+        switch (dtype) {
+            case HH_F32: HH_LAUNCH_FUSED(HH_F32); break;
+            case HH_F16: HH_LAUNCH_FUSED(HH_F16); break;
+            case HH_BF16: HH_LAUNCH_FUSED(HH_BF16); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef HH_LAUNCH_FUSED
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        blk += nb;
+    }
+    return hipSuccess;
+}
+
+uint32_t fused_block_max() { return kFusedMax; }
 
 }  // namespace hh

@@ -212,6 +212,28 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
                                  hh_block_status *d_status, const hh_hctt_tensor *tensors,
                                  uint32_t ntensors, int32_t out_dtype, void *stream);
 
+/* hh_hctt_decode_lz4_batch in one launch with the tile bytes kept on chip:
+ * HctReader::decompress_all (haagenti-hct/src/tensor.rs:417-515) and
+ * GpuDecompressor::decompress_batch_to_gpu (haagenti-cuda/src/decompress.rs:
+ * 282-293) fused, no d_scratch.  Each LZ4 block holds whole tiles of one
+ * tensor: tensor i's blocks are the next ceil(ntiles_i / tiles_per_block)
+ * entries of d_in_off / d_in_len (tensor 0's first), each decompressing to
+ * tiles_per_block tiles (a tensor's last block to the rest), at most
+ * HH_FUSED_BLOCK_BYTES of tile bytes per block (HH_ERR_UNSUPPORTED
+ * otherwise); nblocks must be their total.  tensors[i].d_tiles / tiles_len
+ * are not used.  d_status receives one record per block as
+ * hh_lz4_decompress_batch writes it (the expected size is the block's tile
+ * bytes); the tile bytes a block does not produce (all of a failed block's)
+ * read as zeros, so those tiles report HH_ERR_CORRUPTED_DATA with zero
+ * output.  Asynchronous on the stream.  One persistent workgroup per CU
+ * takes a run of blocks: two of its waves decode blocks into LDS block
+ * buffers while the others decode the tiles of blocks already in LDS. */
+#define HH_FUSED_BLOCK_BYTES 16352u
+int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                 const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,
+                                 hh_block_status *d_status, const hh_hctt_tensor *tensors, uint32_t ntensors,
+                                 uint32_t tiles_per_block, int32_t out_dtype, void *stream);
+
 /* Size of the tile-byte array hh_hctt_decode_lz4_batch_noalloc uses: 64 MiB
  * (a Llama-3-8B layer's tiles at 30 % retention take 64,110,592 bytes). */
 #define HH_NOALLOC_SCRATCH_BYTES (64ull << 20)

@@ -1,0 +1,192 @@
+"""hh_hctt_decode_lz4_fused: LZ4 blocks of whole tiles and their tiles in one
+launch, the tile bytes kept in LDS (HctReader::decompress_all,
+crates/haagenti-hct/src/tensor.rs:417-515, with the per-tile decode of
+GpuDecompressor::decompress_batch_to_gpu, crates/haagenti-cuda/src/
+decompress.rs:282-293, fused).
+
+The tile arithmetic is the same code as the two-launch path
+(hh_hctt_decode_lz4_batch), so every output is compared bit for bit with
+that path (itself checked against the oracle at 1e-3 x RMS in
+test_gpu_llama_layers.py), and one tensor per layer against the oracle
+directly.  A block that fails or decodes short gets the batched LZ4 kernel's
+status record, and its tiles report HH_ERR_CORRUPTED_DATA with zero output
+while every other tile is unaffected."""
+import numpy as np
+import pytest
+
+import gpu_util as G
+import layer_util as LU
+import oracle_lib as O
+from test_gpu_llama_layers import check_against_oracle, decode
+
+pytestmark = pytest.mark.gpu
+
+
+def H():
+    import haagenti_amd as h
+    return h
+
+
+def encode_fixed(Hm, shapes, ks, seed, tpb):
+    """A layer whose every tensor is cut into blocks of tpb whole tiles (the
+    last block of a tensor the rest), in the layout encode_layer returns."""
+    rng = np.random.default_rng(seed)
+    comp = Hm.Lz4Compressor()
+    parts, in_off, in_len, out_off, out_cap, tensors = [], [], [], [], [], []
+    pos = spos = 0
+    for (name, rows, cols), k in zip(shapes, ks):
+        w = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+        tiles = Hm.hctt_encode(w, k)
+        tb = Hm.hctt_tile_bytes(k)
+        for s in range(0, tiles.size, tpb * tb):
+            chunk = tiles[s:s + tpb * tb]
+            c = comp.compress(chunk.tobytes())
+            parts.append(c)
+            in_off.append(pos)
+            in_len.append(len(c))
+            out_off.append(spos + s)
+            out_cap.append(chunk.size)
+            pos += len(c)
+        tensors.append(dict(name=name, rows=rows, cols=cols, k=k, soff=spos, tiles=tiles))
+        spos += tiles.size
+    return dict(blob=np.frombuffer(b"".join(parts), np.uint8), in_off=np.array(in_off, np.uint64),
+                in_len=np.array(in_len, np.uint32), out_off=np.array(out_off, np.uint64),
+                out_cap=np.array(out_cap, np.uint32), tensors=tensors, scratch_bytes=spos)
+
+
+def fused(L, dtype, tpb, blob=None, expect_rc=0):
+    Hm = H()
+    T = G.torch()
+    d_in = G.dev(L["blob"] if blob is None else blob)
+    in_off, in_len = G.dev(L["in_off"]), G.dev(L["in_len"])
+    n = L["in_off"].size
+    status = T.zeros(n * 32, dtype=T.uint8, device="cuda")
+    tdt = {Hm.F32: T.float32, Hm.BF16: T.bfloat16, Hm.F16: T.float16}[dtype]
+    outs, tst, desc = [], [], []
+    for t in L["tensors"]:
+        o = T.full((t["rows"] * t["cols"],), 7.0, dtype=tdt, device="cuda")
+        s = T.full(((t["rows"] // 64) * (t["cols"] // 64),), -1, dtype=T.int32, device="cuda")
+        outs.append(o)
+        tst.append(s)
+        desc.append((t["rows"], t["cols"], t["k"], o, s))
+    print(f"[fused] {len(desc)} tensors, {n} blocks of {tpb} tiles, dtype {dtype}", flush=True)
+    rc = G.ctx().hctt_decode_lz4_fused(d_in, d_in.numel(), in_off, in_len, n, status, desc, tpb, dtype,
+                                       stream=G.stream())
+    assert rc == expect_rc
+    G.sync()
+    st = np.frombuffer(status.cpu().numpy().tobytes(), dtype=np.dtype(
+        [("code", "<i4"), ("detail", "<i4"), ("position", "<u8"), ("required", "<u8"), ("written", "<u8")]))
+    return outs, st, tst
+
+
+def test_llama3_8b_layer_fused_equals_two_launch_path():
+    Hm = H()
+    T = G.torch()
+    k = Hm.hctt_retain_count(0.3)
+    L = LU.encode_layer(Hm, LU.L8B, [k] * 7, seed=8)
+    tpb = 16384 // Hm.hctt_tile_bytes(k)
+    assert tpb == 13
+    for dtype in (Hm.F32, Hm.BF16):
+        fo, st, fs = fused(L, dtype, tpb)
+        assert (st["code"] == 0).all() and (st["written"] == L["out_cap"]).all()
+        assert all((s.cpu().numpy() == 0).all() for s in fs)
+        bo, codes, scratch, _ = decode(L, dtype)
+        del scratch
+        assert (codes == 0).all()
+        for t, a, b in zip(L["tensors"], fo, bo):
+            assert T.equal(a.view(T.int32 if dtype == Hm.F32 else T.int16),
+                           b.view(T.int32 if dtype == Hm.F32 else T.int16)), (t["name"], dtype)
+        if dtype == Hm.F32:
+            check_against_oracle(dict(tensors=L["tensors"][1:2]), fo[1:2])
+        del fo, bo
+
+
+def test_mixed_retention_fixed_blocks_vs_oracle():
+    Hm = H()
+    rng = np.random.default_rng(41)
+    shapes = [("a", 512, 1024), ("b", 1024, 512), ("c", 256, 2048), ("d", 640, 384)]
+    ks = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, len(shapes))]
+    tpb = min(Hm.FUSED_BLOCK_BYTES // Hm.hctt_tile_bytes(k) for k in ks)
+    L = encode_fixed(Hm, shapes, ks, seed=42, tpb=tpb)
+    fo, st, fs = fused(L, Hm.F32, tpb)
+    assert (st["code"] == 0).all()
+    assert all((s.cpu().numpy() == 0).all() for s in fs)
+    check_against_oracle(L, fo)
+    # the same tiles through the two-launch path: bit-identical
+    bo, codes, scratch, _ = decode(L, Hm.F32)
+    assert (codes == 0).all()
+    T = G.torch()
+    for a, b in zip(fo, bo):
+        assert T.equal(a.view(T.int32), b.view(T.int32))
+
+
+def test_failed_and_short_blocks_poison_only_their_tiles():
+    Hm = H()
+    T = G.torch()
+    shapes = [("a", 256, 512), ("b", 512, 256)]
+    ks = [Hm.hctt_retain_count(0.3), Hm.hctt_retain_count(0.2)]
+    tpb = 5
+    L = encode_fixed(Hm, shapes, ks, seed=43, tpb=tpb)
+    n = L["in_off"].size
+    blob = L["blob"].copy()
+    # block 2: a corrupted offset field is far past the output (CORRUPTED);
+    # block n - 3: the stream ends early (decodes short or fails)
+    bad = [2, n - 3]
+    lens = L["in_len"].copy()
+    o2 = int(L["in_off"][2])
+    blob[o2 + 1:o2 + int(lens[2])] ^= 0x5A
+    lens[n - 3] = max(1, lens[n - 3] // 3)
+    L2 = dict(L, in_len=lens)
+    fo, st, fs = fused(L2, Hm.F32, tpb, blob=blob)
+    # the records are the batched LZ4 kernel's for the same blocks and sizes
+    d_in = G.dev(blob)
+    ref_st = T.zeros(n * 32, dtype=T.uint8, device="cuda")
+    scratch = T.zeros(L["scratch_bytes"], dtype=T.uint8, device="cuda")
+    G.ctx().lz4_decompress_batch(d_in, d_in.numel(), G.dev(L["in_off"]), G.dev(lens), scratch,
+                                 G.dev(L["out_off"]), G.dev(L["out_cap"]), n, ref_st, stream=G.stream())
+    G.sync()
+    ref = np.frombuffer(ref_st.cpu().numpy().tobytes(), dtype=st.dtype)
+    for f in ("code", "detail", "position", "required"):
+        assert np.array_equal(st[f], ref[f]), f
+    short = [b for b in bad if ref["code"][b] != 0 or ref["written"][b] < L["out_cap"][b]]
+    assert len(short) == 2
+    # map blocks to tiles and check the poisoning
+    bo, codes, sc, _ = decode(L, Hm.F32)
+    blk = 0
+    for t, a, b, s in zip(L["tensors"], fo, bo, fs):
+        nt = (t["rows"] // 64) * (t["cols"] // 64)
+        stt = s.cpu().numpy()
+        a_np = a.cpu().numpy().reshape(t["rows"] // 64, 64, t["cols"] // 64, 64)
+        b_np = b.cpu().numpy().reshape(t["rows"] // 64, 64, t["cols"] // 64, 64)
+        tpr = t["cols"] // 64
+        for j in range((nt + tpb - 1) // tpb):
+            g = blk + j
+            good = int(st["written"][g]) if st["code"][g] == 0 else 0
+            tb = Hm.hctt_tile_bytes(t["k"])
+            for tt in range(j * tpb, min(nt, (j + 1) * tpb)):
+                r, c = divmod(tt, tpr)
+                lo, hi = (tt - j * tpb) * tb, (tt - j * tpb + 1) * tb
+                if hi <= good:      # every byte of the tile produced
+                    assert stt[tt] == 0
+                    assert np.array_equal(a_np[r, :, c, :].view(np.int32), b_np[r, :, c, :].view(np.int32))
+                elif lo >= good:    # none: all zero bytes
+                    assert g in bad
+                    assert stt[tt] == Hm.CORRUPTED_DATA, (t["name"], g, tt)
+                    assert (a_np[r, :, c, :] == 0).all()
+        blk += (nt + tpb - 1) // tpb
+
+
+def test_argument_errors():
+    Hm = H()
+    k = Hm.hctt_retain_count(0.3)
+    L = encode_fixed(Hm, [("a", 128, 128)], [k], seed=44, tpb=2)
+    assert L["in_off"].size == 2
+    T = G.torch()
+    d_in = G.dev(L["blob"])
+    st = T.zeros(64, dtype=T.uint8, device="cuda")
+    o = T.empty(128 * 128, dtype=T.float32, device="cuda")
+    args = (d_in, d_in.numel(), G.dev(L["in_off"]), G.dev(L["in_len"]))
+    assert G.ctx().hctt_decode_lz4_fused(*args, 3, st, [(128, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
+    assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], 14) == Hm.UNSUPPORTED
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(100, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], 2) == Hm.OK

@@ -129,6 +129,12 @@ def test_pipeline_streams_70b_layers_with_overlap():
             print(f"[pipeline] layer {i} {t['name']}: {err / rms:.2e} x RMS", flush=True)
             assert err <= TOL * rms
 
+    # hold the copy stream (a bounded clock spin, ~20 ms) so that both units
+    # are enqueued before the first copy starts: the overlap below then does
+    # not depend on how fast this host returns from submit
+    copy_s, _ = pipe.streams
+    with T.cuda.stream(T.cuda.ExternalStream(copy_s)):
+        T.cuda._sleep(50_000_000)
     t0 = submit(0)
     t1 = submit(1)                                # copy of layer 1 under the decode of layer 0
     pipe.wait(t0)
