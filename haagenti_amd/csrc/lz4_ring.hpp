@@ -31,9 +31,9 @@
 // misalignment of the block's output address, so that 16-aligned virtual
 // positions are 16-aligned addresses; the ring slot of position v is
 // v mod R):
-//  * copies are split into pieces of at most kP bytes, each followed by the
-//    flush check, so at most R - kP bytes are ever pending and a piece never
-//    overwrites a pending byte;
+//  * copies are split into pieces of at most kP bytes (literals: kPL), each
+//    followed by the flush check (a flush once kFlushAt = R - 2 max(kP, kPL)
+//    bytes are pending), so a piece never overwrites a pending byte;
 //  * a piece writes slots of positions at least R behind it, i.e. more than
 //    kNear behind its start, which no near match reads.
 // Every read is clamped to the caller's buffers and every write stays inside
@@ -78,8 +78,12 @@ struct RingDec {
     static_assert(S % 1024 == 0 && S >= 1024, "stage is whole KiB");
     static constexpr uint32_t kRM = R - 1;
     static constexpr uint32_t kP = 992;             // largest piece: at most 63 chunks
+    // literal pieces: kLitU chunks per lane (LDS mode has no flush
+    // bookkeeping; a small ring keeps one so that flushes stay rare)
+    static constexpr uint32_t kLitU = LDS ? 4 : R >= 8192 ? 2 : 1;
+    static constexpr uint32_t kPL = 64u * 16u * kLitU - 16u;
     static constexpr uint32_t kNear = R - 32;       // offsets served from the ring
-    static constexpr uint32_t kFlushAt = R - 2 * kP;
+    static constexpr uint32_t kFlushAt = R - 2 * (kPL > kP ? kPL : kP);
     static constexpr uint32_t kSFront = 16;         // stage under-read (first chunk of a literal)
     static constexpr uint32_t kSPad = 272;          // window and realign over-read
     static constexpr uint32_t kLds = R + kSFront + S + kSPad;
@@ -324,13 +328,10 @@ struct RingDec {
     }
 
     // A literal piece of n bytes (n <= kPL) from stage byte src to the ring
-    // at op, LDS mode only: lane l writes chunks l, l + 64, l + 128, l + 192
-    // of the piece (16-byte chunks aligned in virtual positions), all stage
-    // reads issued before the first write.  Chunk rules as in piece<0>.
-    static constexpr uint32_t kLitU = 4;
-    static constexpr uint32_t kPL = LDS ? 64u * 16u * kLitU - 16u : kP;
+    // at op: lane l writes chunks l, l + 64, ... of the piece (16-byte chunks
+    // aligned in virtual positions), all stage reads issued before the first
+    // write.  Chunk rules as in piece<0>.
     __device__ __forceinline__ void piece_lit(uint32_t src, uint32_t n) {
-        static_assert(LDS, "wide pieces leave no room for the flush bookkeeping");
         const uint32_t v = op + a0;
         const uint32_t c0 = v & ~15u;
         const uint32_t nch = ((v + n + 15u) >> 4) - (v >> 4);  // <= 64 kLitU
@@ -475,10 +476,7 @@ __device__ __forceinline__ void parse_block(RingDec<R, S, LDS> &d, uint32_t ilen
                 }
                 uint32_t n = rem < D::kPL ? rem : D::kPL;
                 if (n > S - so) n = S - so;
-                if constexpr (LDS)
-                    d.piece_lit(so, n);
-                else
-                    d.template piece<0>(so, n, 0);
+                d.piece_lit(so, n);
                 ip += n;
                 rem -= n;
                 d.check_flush();
