@@ -314,7 +314,6 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     floatx16 acc[2][2];
 #pragma unroll
     for (int up = 0; up < 2; up++) {
-        u32x4 ahi[2][2], alo[2][2];  // [vpar][s]
         const uint64_t b64 = ok ? bits_r[up] : 0ull;
         // the row shifted so that column 8 h is bit 0: every column this
         // lane needs sits at a compile-time bit position
@@ -324,8 +323,12 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
         // LDS byte address of V[rank]; a column that is not retained
         // masks it to 0, the zero word
         uint32_t diff = wbase + 4 * rank_h;
+        acc[up][0] = floatx16{};
+        acc[up][1] = floatx16{};
+        // one k step at a time: its A fragments are gathered, then used
 #pragma unroll
         for (int s = 0; s < 2; s++) {
+            u32x4 ahi[2], alo[2];  // [vpar]
 #pragma unroll
             for (int run = 0; run < 2; run++) {
                 const uint32_t word = wd[s];
@@ -348,24 +351,20 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                 for (int o = 0; o < 8; o++) w[o] = lds_load(a[o]);
 #pragma unroll
                 for (int vp = 0; vp < 2; vp++) {
-                    ahi[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
-                    alo[vp][s][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
-                    ahi[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
-                    alo[vp][s][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
+                    ahi[vp][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x05040100u);
+                    alo[vp][2 * run] = __builtin_amdgcn_perm(w[2 + vp], w[vp], 0x07060302u);
+                    ahi[vp][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x05040100u);
+                    alo[vp][2 * run + 1] = __builtin_amdgcn_perm(w[6 + vp], w[4 + vp], 0x07060302u);
                 }
             }
-        }
 #pragma unroll
-        for (int vp = 0; vp < 2; vp++) {
-            acc[up][vp] = floatx16{};
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
+            for (int vp = 0; vp < 2; vp++) {
                 const u32x4 mh = mtab[((0 * 2 + vp) * 2 + s) * 64 + lane];
                 const u32x4 ml = mtab[((1 * 2 + vp) * 2 + s) * 64 + lane];
-                acc[up][vp] = mfma(ahi[vp][s], mh, acc[up][vp]);
-                acc[up][vp] = mfma(ahi[vp][s], ml, acc[up][vp]);
-                acc[up][vp] = mfma(alo[vp][s], mh, acc[up][vp]);
-                acc[up][vp] = mfma(alo[vp][s], ml, acc[up][vp]);
+                acc[up][vp] = mfma(ahi[vp], mh, acc[up][vp]);
+                acc[up][vp] = mfma(ahi[vp], ml, acc[up][vp]);
+                acc[up][vp] = mfma(alo[vp], mh, acc[up][vp]);
+                acc[up][vp] = mfma(alo[vp], ml, acc[up][vp]);
             }
         }
     }
@@ -561,38 +560,54 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 // consumer c decodes tiles c, c + nc, c + 2 nc, ... of the range, in that
 // order, straight from the buffers with tile_body (one 32-column block of the
 // output parked at a time).  The tile bytes never reach HBM, and the LZ4
-// parse of later blocks runs while the consumers work on earlier ones.
+// parse of a block runs while consumers already decode its first tiles.
 //
 // Two LDS words per buffer order the two sides:
-//   ready[x]  1 + the number of the block the buffer holds, stored by its
-//             producer once the bytes are in LDS;
-//   done[x]   how many of that block's tiles have been read, counted by the
-//             consumers; a producer refills buffer x with block i only once
-//             done[x] equals the tile count of block i - nbuf, and clears it
-//             before publishing block i.
+//   state[x]    (64 bits) 1 + the number of the block the buffer holds, and
+//               the block's progress: the bytes decoded so far (published
+//               after every sequence), then kStFinal (with kStFailed for a
+//               block that failed) once the block is complete;
+//   confirm[x]  how many of that block's tiles are settled: read, with the
+//               block final.  A producer refills buffer x with block i only
+//               once state[x] names block i - nbuf (which another producer
+//               may place there late) and confirm[x] equals its tile count;
+//               it clears confirm[x] before publishing block i.
+// A consumer decodes a tile as soon as the progress covers its bytes.  When
+// its block is not final yet, the tile stays pending (at most one per
+// consumer) until the consumer sees the block final; if the block failed, the
+// consumer then rewrites the tile as zeros with HH_ERR_CORRUPTED_DATA.  A
+// failed block's producer zeroes the buffer from the first tile it had not
+// released, and consumers of a block already final and failed write zeros
+// and the status without decoding, so every tile of a failed block ends up
+// zeros + HH_ERR_CORRUPTED_DATA, as with the two-launch path.  A block that
+// decodes short (no error) leaves the rest of its buffer zeroed: those tiles
+// fail their bitmap count.
+//
 // No wait can deadlock: the lowest-numbered block not yet decoded waits only
 // for the tiles of an earlier (decoded) block, whose consumers wait only for
-// blocks before those tiles, all decoded.  Every wait is bounded all the same
-// (kSpinLimit polls); one that runs out (not expected) raises the
-// workgroup's abort word, every wave of the workgroup then leaves, and the
-// block record of the block waited on reports HH_ERR_DEVICE.
+// blocks before those tiles, all decoded, or for an earlier block to become
+// final.  Every wait is bounded all the same (kSpinLimit polls); one that
+// runs out (not expected) raises the workgroup's abort word, every wave of
+// the workgroup then leaves, and the block record of the block waited on
+// reports HH_ERR_DEVICE.
 //
-// A block that fails (status as the batched LZ4 kernel writes it) or decodes
-// to fewer bytes than its tiles take leaves the rest zeroed: those tiles fail
-// their bitmap count (tile status HH_ERR_CORRUPTED_DATA, zeros out).
-// The input stage holds a whole block's compressed bytes (LZ4's worst case
-// for kFusedMax bytes, 16,432, plus 15 bytes of misalignment and the 256-byte
-// window), so each block is staged with one batch of loads.
-constexpr uint32_t kFusedStageData = 17 * 1024;
+// The input stage holds 8 KiB of a block's compressed bytes (a 16 KiB block
+// is staged in two or three batches of loads); a stage holding the whole
+// block needs more registers for its loads than 4 waves per SIMD leave.
+constexpr uint32_t kFusedStageData = 8 * 1024;
 using FusedRing = ring::RingDec<16384, kFusedStageData, true>;
 constexpr uint32_t kFusedMax = 16384 - 32;
 constexpr uint32_t kFusedBuf = 16384;  // a block buffer: the decoder's ring
 constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a producer's input stage
-constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: tile_body's register budget
-constexpr int kFusedProducers = 2;
+constexpr int kFusedMaxWaves = 16;     // 4 per SIMD: 128 registers, tile_body's budget
+constexpr int kFusedProducers = 3;
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
+// low word of a buffer's state: progress bytes and the final flags
+constexpr uint32_t kStBytes = 0xffffu;
+constexpr uint32_t kStFinal = 1u << 30;
+constexpr uint32_t kStFailed = 1u << 29;
 
 struct FusedBlocks {
     const uint8_t *in;
@@ -607,28 +622,56 @@ struct FusedBlocks {
     uint32_t stage_off, buf_off;          // LDS byte offsets of the stages and the buffers
 };
 
-// Workgroup LDS layout after the shared part: [block descriptor][ready[8],
-// done[8], abort][consumer areas][producer stages][block buffers].
+// Workgroup LDS layout after the shared part: [block descriptor][state[8]
+// (8 bytes each), confirm[8], abort][consumer areas][producer stages][block
+// buffers].
 constexpr uint32_t kFusedFOff = kSharedBytes;
 constexpr uint32_t kFusedFlagsOff = kFusedFOff + ((sizeof(FusedBlocks) + 15u) & ~15u);
-constexpr uint32_t kFusedFlagWords = 2 * kFusedMaxBufs + 1;
+constexpr uint32_t kFusedStateOff = kFusedFlagsOff;
+constexpr uint32_t kFusedConfirmOff = kFusedStateOff + 8 * kFusedMaxBufs;
+constexpr uint32_t kFusedAbortOff = kFusedConfirmOff + 4 * kFusedMaxBufs;
+constexpr uint32_t kFusedFlagWords = (kFusedAbortOff + 4 - kFusedFlagsOff) / 4;
 constexpr uint32_t kFusedConsOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
 
 typedef uint32_t __attribute__((address_space(3))) lds_word;
+typedef uint64_t __attribute__((address_space(3))) lds_dword;
 
-// Polls the LDS word at `w` until it reads `want` (true), or the abort word
-// is raised or the poll limit runs out (false; the latter raises it).
-__device__ __forceinline__ bool fused_wait(uint32_t w, uint32_t want, uint32_t abort_w, int lane) {
+// The lane number, computed where it is used from a mask the compiler cannot
+// see through: values derived from it are then recomputed inside a loop
+// instead of being hoisted and held (or spilled) across it.
+__device__ __forceinline__ int opaque_lane() {
+    uint32_t m = ~0u;
+    asm volatile("" : "+s"(m));
+    return (int)__builtin_amdgcn_mbcnt_hi(m, __builtin_amdgcn_mbcnt_lo(m, 0u));
+}
+
+__device__ __forceinline__ uint64_t lds_load_acq(uint32_t a, uint64_t) {
+    return __hip_atomic_load((lds_dword *)(size_t)a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t lds_load_acq(uint32_t a, uint32_t) {
+    return __hip_atomic_load((lds_word *)(size_t)a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint64_t uniform(uint64_t v) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
+// Polls the LDS word (32 or 64 bits, by T) at LDS address w until ok(value)
+// holds (true, the value in v), or the abort word is raised or the poll
+// limit runs out (false; the latter raises it).
+template <typename T, typename Pred>
+__device__ __forceinline__ bool fused_poll(uint32_t w, int lane, T &v, Pred &&ok) {
     for (uint32_t it = 0;; it++) {
-        const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane(
-            (int)__hip_atomic_load((lds_word *)(size_t)w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
-        if (v == want) return true;
-        const uint32_t ab = (uint32_t)__builtin_amdgcn_readfirstlane(
-            (int)__hip_atomic_load((lds_word *)(size_t)abort_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        v = uniform(lds_load_acq(w, T{}));
+        if (ok(v)) return true;
+        const uint32_t ab = uniform(
+            __hip_atomic_load((lds_word *)(size_t)kFusedAbortOff, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         if (ab != 0) return false;
         if (it == kSpinLimit) {
             if (lane == 0)
-                __hip_atomic_store((lds_word *)(size_t)abort_w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store((lds_word *)(size_t)kFusedAbortOff, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -656,12 +699,12 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // the LDS copy serves the indexed block table; pointers come from the
     // kernel arguments, where the compiler knows them to be global
     const FusedBlocks &F = *reinterpret_cast<const FusedBlocks *>(smem + kFusedFOff);
-    const uint32_t ready_w = kFusedFlagsOff, done_w = kFusedFlagsOff + 4 * kFusedMaxBufs;
-    const uint32_t abort_w = kFusedFlagsOff + 8 * kFusedMaxBufs;
     const uint32_t nblk = F.blk_start[B.n];
     const uint32_t b_lo = (uint32_t)((uint64_t)nblk * blockIdx.x / gridDim.x);
     const uint32_t b_hi = (uint32_t)((uint64_t)nblk * (blockIdx.x + 1) / gridDim.x);
     const uint32_t np = Fk.np, nbuf = Fk.nbuf, nc = (nthr >> 6) - np;
+    auto state_w = [](uint32_t x) { return kFusedStateOff + 8u * x; };
+    auto confirm_w = [](uint32_t x) { return kFusedConfirmOff + 4u * x; };
 
     // block lb -> tensor, first tile, tile count
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
@@ -670,8 +713,8 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         t0 = (lb - F.blk_start[ti]) * F.tpb;
         nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
     };
-    auto report = [&](uint32_t lb) {  // a wait ran out
-        if (lane == 0) {
+    auto report = [&](uint32_t lb, int ln) {  // a wait ran out
+        if (ln == 0) {
             hh_block_status st;
             st.code = HH_ERR_DEVICE;
             st.detail = HH_CORRUPT_NONE;
@@ -686,21 +729,32 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         // ---- producer
         uint8_t *stage = smem + Fk.stage_off + wave * kFusedStage + FusedRing::kSFront;
         for (uint32_t lb = b_lo + wave; lb < b_hi; lb += np) {
+            const int ln = opaque_lane();
             const uint32_t x = (lb - b_lo) % nbuf;
-            if (lb - b_lo >= nbuf) {  // the buffer's previous block must be read
-                uint32_t pti, pt0, pnt;
+            if (lb - b_lo >= nbuf) {
+                // the buffer's previous block (lb - nbuf, possibly another
+                // producer's) must have been placed there, then settled: its
+                // confirm count is only meaningful once its stamp is up
+                uint32_t pti, pt0, pnt, v;
+                uint64_t sv;
                 locate(lb - nbuf, pti, pt0, pnt);
-                if (!fused_wait(done_w + 4 * x, pnt, abort_w, lane)) {
-                    report(lb);
+                if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == lb - nbuf + 1u; }) ||
+                    !fused_poll(confirm_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
+                    report(lb, ln);
                     break;
                 }
             }
-            if (lane == 0)
-                __hip_atomic_store((lds_word *)(size_t)(done_w + 4 * x), 0u, __ATOMIC_RELAXED,
+            const uint64_t stamp = (uint64_t)(lb + 1u) << 32;
+            if (ln == 0) {
+                __hip_atomic_store((lds_word *)(size_t)confirm_w(x), 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
             uint32_t ti, t0, nt;
             locate(lb, ti, t0, nt);
-            const uint32_t cap = nt * B.tb[ti];
+            const uint32_t tb = B.tb[ti];
+            const uint32_t cap = nt * tb;
             uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
             const uint32_t gb = Fk.blk_base + lb;
             int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
@@ -722,35 +776,44 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             d.w = 0;
             d.op = 0;
             d.fl = 0;
-            // a copy of the lane number the compiler cannot see through: the
-            // decoder's lane-derived addresses are then computed per block
-            // instead of being hoisted out of the loop and held in registers
-            int dl = lane;
-            asm volatile("" : "+v"(dl));
-            d.lane = dl;
+            d.lane = ln;
+            // bytes published to the consumers so far (every lane's copies
+            // are issued: each copy piece ends with a wave barrier)
+            uint32_t published = 0;
+            auto publish = [&](uint32_t op) {
+                if (op >= published + tb) {
+                    published = op;
+                    if (ln == 0)
+                        __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | op, __ATOMIC_RELEASE,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            };
             if (ioff > Fk.in_total || (uint64_t)ilen > Fk.in_total - ioff) {
                 code = HH_ERR_INVALID_ARGUMENT;
             } else {
-                ring::parse_block(d, ilen, code, detail, pos, req);
+                ring::parse_block(d, ilen, code, detail, pos, req, false, publish);
             }
-            // bytes of the block's tiles that were not produced read as zeros
-            const uint32_t good = code == HH_OK ? d.op : 0u;
-            if (good < cap) {
+            // a complete block: the bytes it did not produce read as zeros; a
+            // failed one: zeros from its first tile not released to the
+            // consumers (released tiles are rewritten by their consumers)
+            const uint32_t zfrom = code == HH_OK ? d.op : (published / tb) * tb;
+            if (zfrom < cap) {
                 wave_sync();
-                wave_zero_fill(rbuf + good, cap - good, lane);
+                wave_zero_fill(rbuf + zfrom, cap - zfrom, ln);
             }
-            if (lane == 0) {
+            if (ln == 0) {
                 hh_block_status st;
                 st.code = code;
                 st.detail = detail;
                 st.position = pos;
                 st.required = req;
-                st.written = good;
+                st.written = code == HH_OK ? d.op : 0u;
                 ((hh_block_status *)Fk.status)[gb] = st;
             }
             wave_sync();  // every lane's buffer writes are issued before the release
-            if (lane == 0)
-                __hip_atomic_store((lds_word *)(size_t)(ready_w + 4 * x), lb + 1u, __ATOMIC_RELEASE,
+            if (ln == 0)
+                __hip_atomic_store((lds_dword *)(size_t)state_w(x),
+                                   stamp | cap | kStFinal | (code == HH_OK ? 0u : kStFailed), __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {
@@ -760,6 +823,47 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
         const uint32_t wbase = kFusedConsOff + c * B.wave_lds;
         uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
+        auto settle = [&](uint32_t x, int ln) {
+            // the tile's LDS reads are complete (their values fed the V table)
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            if (ln == 0)
+                __hip_atomic_fetch_add((lds_word *)(size_t)confirm_w(x), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        // zeros and HH_ERR_CORRUPTED_DATA for tile t of tensor ti (a tile of
+        // a failed block), after this wave's earlier stores have completed
+        auto fail_tile = [&](uint32_t ti, uint32_t t, int ln) {
+            constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
+            constexpr uint32_t per_row = 64u * esz / 16u;
+            constexpr uint32_t rows_per = 64u / per_row;
+            const uint32_t cols = B.cols[ti], tpr = B.tiles_per_row[ti];
+            const size_t base = (size_t)(64u * (t / tpr)) * cols + 64u * (t % tpr);
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[ti];
+            for (uint32_t it = 0; it < 64u / rows_per; it++) {
+                const uint32_t row = rows_per * it + (uint32_t)ln / per_row;
+                *(u32x4 HH_GLOBAL *)(o + esz * (base + (size_t)row * cols) + 16u * ((uint32_t)ln % per_row)) =
+                    u32x4{0u, 0u, 0u, 0u};
+            }
+            if (B.status[ti] != nullptr && ln == 0)
+                ((int32_t HH_GLOBAL *)B.status[ti])[t] = HH_ERR_CORRUPTED_DATA;
+        };
+        // the tile decoded before its block was final
+        bool pending = false;
+        uint32_t p_lb = 0, p_x = 0, p_ti = 0, p_t = 0;
+        auto resolve = [&](int ln) -> bool {
+            uint64_t v;
+            if (!fused_poll(state_w(p_x), ln, v, [&](uint64_t s) {
+                    return (uint32_t)(s >> 32) == p_lb + 1u && ((uint32_t)s & kStFinal) != 0u;
+                })) {
+                report(p_lb, ln);
+                return false;
+            }
+            if ((uint32_t)v & kStFailed) fail_tile(p_ti, p_t, ln);
+            settle(p_x, ln);
+            pending = false;
+            return true;
+        };
         // tile `off` of block lb of the range: this wave's next one
         uint32_t lb = b_lo, off = c, ti = 0, t0 = 0, nt = 0;
         if (lb < b_hi) locate(lb, ti, t0, nt);
@@ -770,26 +874,39 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 if (lb < b_hi) locate(lb, ti, t0, nt);
             }
             if (lb >= b_hi) break;
+            const int ln = opaque_lane();
+            if (pending && !resolve(ln)) break;
             const uint32_t x = (lb - b_lo) % nbuf;
-            if (!fused_wait(ready_w + 4 * x, lb + 1u, abort_w, lane)) {
-                report(lb);
+            const uint32_t tb = B.tb[ti];
+            const uint32_t need = (off + 1u) * tb;
+            uint64_t v;
+            if (!fused_poll(state_w(x), ln, v, [&](uint64_t s) {
+                    // the tile's bytes are there (kStFinal exceeds any need)
+                    return (uint32_t)(s >> 32) == lb + 1u && ((uint32_t)s & (kStFinal | kStBytes)) >= need;
+                })) {
+                report(lb, ln);
                 break;
             }
-            const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
-            // an opaque copy of the lane number: the lane-derived addresses
-            // of tile_body are recomputed per tile rather than held (spilled)
-            // across the loop
-            int tl = lane;
-            asm volatile("" : "+v"(tl));
-            tile_body<DT, true>(B, ti, t0 + off, rbuf + off * B.tb[ti], V, wbase, mtab, tl, one, n4, [&]() {
-                // count the tile's bytes as read (their LDS reads complete)
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-                if (lane == 0)
-                    __hip_atomic_fetch_add((lds_word *)(size_t)(done_w + 4 * x), 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP);
-            });
+            const bool fin = ((uint32_t)v & kStFinal) != 0u;
+            if (fin && ((uint32_t)v & kStFailed)) {
+                fail_tile(ti, t0 + off, ln);
+                settle(x, ln);
+            } else {
+                const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+                tile_body<DT, true>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln, one, n4, [&]() {
+                    if (fin) settle(x, ln);
+                });
+                if (!fin) {
+                    pending = true;
+                    p_lb = lb;
+                    p_x = x;
+                    p_ti = ti;
+                    p_t = t0 + off;
+                }
+            }
             off += nc;
         }
+        if (pending) resolve(opaque_lane());
     }
 }
 

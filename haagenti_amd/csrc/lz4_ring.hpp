@@ -406,10 +406,15 @@ struct RingDec {
 // into d; on return code / detail / pos / req hold the outcome (HH_OK or the
 // reference's error record) and d.op the bytes decoded.  The caller flushes
 // the rest of a successful block.  `staged`: the caller has already staged
-// the input from 0 on (put_stage(0, ...)).
-template <uint32_t R, uint32_t S, bool LDS>
+// the input from 0 on (put_stage(0, ...)).  `progress(op)` runs after each
+// sequence's copies (every lane; the output bytes before op are final).
+struct NoProgress {
+    __device__ __forceinline__ void operator()(uint32_t) const {}
+};
+template <uint32_t R, uint32_t S, bool LDS, typename Progress = NoProgress>
 __device__ __forceinline__ void parse_block(RingDec<R, S, LDS> &d, uint32_t ilen, int32_t &code, int32_t &detail,
-                                            uint64_t &pos, uint64_t &req, bool staged = false) {
+                                            uint64_t &pos, uint64_t &req, bool staged = false,
+                                            Progress &&progress = Progress{}) {
     using D = RingDec<R, S, LDS>;
     const uint32_t end = ilen;
     uint32_t ip = 0;
@@ -562,6 +567,7 @@ __device__ __forceinline__ void parse_block(RingDec<R, S, LDS> &d, uint32_t ilen
                 d.check_flush();
             }
         }
+        progress(d.op);
     }
 }
 
