@@ -550,64 +550,61 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 
 // ---- LZ4 blocks and their tiles in one launch ------------------------------
 //
-// One persistent workgroup per CU takes a contiguous range of the launch's
-// LZ4 blocks, each holding whole tiles of one tensor (block j of tensor i:
-// tiles [j tpb, j tpb + tpb) of it, the last block the rest).  Its first np
-// waves are producers: producer p decodes blocks p, p + np, p + 2 np, ... of
-// the range with the LDS-ring decoder (lz4_ring.hpp, the whole output kept in
+// One persistent workgroup per CU takes an equal run of the launch's tiles
+// and the LZ4 blocks that hold them (each block holds whole tiles of one
+// tensor: block j of tensor i tiles [j tpb, j tpb + tpb) of it, the last
+// block the rest; a block at either end of a run is decoded by both
+// workgroups that share it).  Its first np waves are producers: producer p
+// decodes blocks p, p + np, p + 2 np, ... of the range with the LDS-ring
+// decoder (lz4_ring.hpp, the whole output kept in
 // LDS: at most kFusedMax bytes) into a ring of nbuf block buffers (block i of
 // the range into buffer i mod nbuf).  The other nc waves are consumers:
-// consumer c decodes tiles c, c + nc, c + 2 nc, ... of the range, in that
-// order, straight from the buffers with tile_body (one 32-column block of the
-// output parked at a time).  The tile bytes never reach HBM, and the LZ4
+// consumer c decodes tiles c, c + nc, c + 2 nc, ... of the run, in that
+// order, straight from the buffers with tile_body (the whole output tile
+// parked in LDS, then stored).  The tile bytes never reach HBM, and the LZ4
 // parse of a block runs while consumers already decode its first tiles.
 //
 // Two LDS words per buffer order the two sides:
-//   state[x]    (64 bits) 1 + the number of the block the buffer holds, and
-//               the block's progress: the bytes decoded so far (published
-//               after every sequence), then kStFinal (with kStFailed for a
-//               block that failed) once the block is complete;
-//   confirm[x]  how many of that block's tiles are settled: read, with the
-//               block final.  A producer refills buffer x with block i only
-//               once state[x] names block i - nbuf (which another producer
-//               may place there late) and confirm[x] equals its tile count;
-//               it clears confirm[x] before publishing block i.
-// A consumer decodes a tile as soon as the progress covers its bytes.  When
-// its block is not final yet, the tile stays pending (at most one per
-// consumer) until the consumer sees the block final; if the block failed, the
-// consumer then rewrites the tile as zeros with HH_ERR_CORRUPTED_DATA.  A
-// failed block's producer zeroes the buffer from the first tile it had not
-// released, and consumers of a block already final and failed write zeros
-// and the status without decoding, so every tile of a failed block ends up
-// zeros + HH_ERR_CORRUPTED_DATA, as with the two-launch path.  A block that
-// decodes short (no error) leaves the rest of its buffer zeroed: those tiles
-// fail their bitmap count.
+//   state[x]  (64 bits) 1 + the number of the block the buffer holds, and
+//             the bytes of it decoded so far (published after every
+//             sequence; the block's tile bytes in full once it is complete);
+//   done[x]   how many of that block's tiles have been read.  A producer
+//             refills buffer x with block i only once state[x] names block
+//             i - nbuf (which another producer may place there late) and
+//             done[x] equals its tile count; it clears done[x] before
+//             publishing block i.
+// A consumer decodes a tile as soon as the published bytes cover it.  Two
+// LDS bitmaps over the workgroup's blocks record which are complete and
+// which failed.  A failed block's producer zeroes its buffer from the first
+// tile it had not released (those tiles then fail their bitmap count), and
+// after the last tile each consumer waits for every block of the run to be
+// complete and rewrites its own tiles of the failed ones as zeros with
+// HH_ERR_CORRUPTED_DATA: every tile of a failed block ends up so, as with the
+// two-launch path.  A block that decodes short (no error) leaves the rest of
+// its buffer zeroed: those tiles fail their bitmap count.
 //
 // No wait can deadlock: the lowest-numbered block not yet decoded waits only
 // for the tiles of an earlier (decoded) block, whose consumers wait only for
-// blocks before those tiles, all decoded, or for an earlier block to become
-// final.  Every wait is bounded all the same (kSpinLimit polls); one that
+// blocks before those tiles, all decoded; the consumers' final wait is for
+// producers that wait on nothing but tiles already read.  Every wait is bounded all the same (kSpinLimit polls); one that
 // runs out (not expected) raises the workgroup's abort word, every wave of
 // the workgroup then leaves, and the block record of the block waited on
 // reports HH_ERR_DEVICE.
 //
 // The input stage holds 8 KiB of a block's compressed bytes (a 16 KiB block
-// is staged in two or three batches of loads); a stage holding the whole
-// block needs more registers for its loads than 4 waves per SIMD leave.
+// is staged in two or three batches of loads), leaving the LDS to the
+// consumers' whole-tile output parks and three block buffers.
 constexpr uint32_t kFusedStageData = 8 * 1024;
 using FusedRing = ring::RingDec<16384, kFusedStageData, true>;
 constexpr uint32_t kFusedMax = 16384 - 32;
 constexpr uint32_t kFusedBuf = 16384;  // a block buffer: the decoder's ring
 constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a producer's input stage
-constexpr int kFusedMaxWaves = 16;     // 4 per SIMD: 128 registers, tile_body's budget
-constexpr int kFusedProducers = 3;
+constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's budget
+constexpr int kFusedProducers = 2;
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
-// low word of a buffer's state: progress bytes and the final flags
-constexpr uint32_t kStBytes = 0xffffu;
-constexpr uint32_t kStFinal = 1u << 30;
-constexpr uint32_t kStFailed = 1u << 29;
+constexpr uint32_t kFusedMaxRange = 4096;  // blocks per workgroup (the bitmaps' size)
 
 struct FusedBlocks {
     const uint8_t *in;
@@ -623,14 +620,16 @@ struct FusedBlocks {
 };
 
 // Workgroup LDS layout after the shared part: [block descriptor][state[8]
-// (8 bytes each), confirm[8], abort][consumer areas][producer stages][block
-// buffers].
+// (8 bytes each), done[8], abort, the complete and failed bitmaps][consumer
+// areas][producer stages][block buffers].
 constexpr uint32_t kFusedFOff = kSharedBytes;
 constexpr uint32_t kFusedFlagsOff = kFusedFOff + ((sizeof(FusedBlocks) + 15u) & ~15u);
 constexpr uint32_t kFusedStateOff = kFusedFlagsOff;
-constexpr uint32_t kFusedConfirmOff = kFusedStateOff + 8 * kFusedMaxBufs;
-constexpr uint32_t kFusedAbortOff = kFusedConfirmOff + 4 * kFusedMaxBufs;
-constexpr uint32_t kFusedFlagWords = (kFusedAbortOff + 4 - kFusedFlagsOff) / 4;
+constexpr uint32_t kFusedDoneOff = kFusedStateOff + 8 * kFusedMaxBufs;
+constexpr uint32_t kFusedAbortOff = kFusedDoneOff + 4 * kFusedMaxBufs;
+constexpr uint32_t kFusedFinalOff = kFusedAbortOff + 4;
+constexpr uint32_t kFusedFailOff = kFusedFinalOff + kFusedMaxRange / 8;
+constexpr uint32_t kFusedFlagWords = (kFusedFailOff + kFusedMaxRange / 8 - kFusedFlagsOff) / 4;
 constexpr uint32_t kFusedConsOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
 
 typedef uint32_t __attribute__((address_space(3))) lds_word;
@@ -692,19 +691,16 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(FusedBlocks) / 4); i += nthr)
         reinterpret_cast<uint32_t *>(smem + kFusedFOff)[i] = reinterpret_cast<const uint32_t *>(&Fk)[i];
     for (uint32_t i = threadIdx.x; i < kMTabBytes / 16; i += nthr) mtab[i] = basis[i];
-    if (threadIdx.x < kFusedFlagWords) reinterpret_cast<uint32_t *>(smem + kFusedFlagsOff)[threadIdx.x] = 0u;
+    for (uint32_t i = threadIdx.x; i < kFusedFlagWords; i += nthr) reinterpret_cast<uint32_t *>(smem + kFusedFlagsOff)[i] = 0u;
     if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();  // the only workgroup barrier: the two roles never meet at one
     const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem + kBatchOff);
     // the LDS copy serves the indexed block table; pointers come from the
     // kernel arguments, where the compiler knows them to be global
     const FusedBlocks &F = *reinterpret_cast<const FusedBlocks *>(smem + kFusedFOff);
-    const uint32_t nblk = F.blk_start[B.n];
-    const uint32_t b_lo = (uint32_t)((uint64_t)nblk * blockIdx.x / gridDim.x);
-    const uint32_t b_hi = (uint32_t)((uint64_t)nblk * (blockIdx.x + 1) / gridDim.x);
     const uint32_t np = Fk.np, nbuf = Fk.nbuf, nc = (nthr >> 6) - np;
     auto state_w = [](uint32_t x) { return kFusedStateOff + 8u * x; };
-    auto confirm_w = [](uint32_t x) { return kFusedConfirmOff + 4u * x; };
+    auto done_w = [](uint32_t x) { return kFusedDoneOff + 4u * x; };
 
     // block lb -> tensor, first tile, tile count
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
@@ -712,6 +708,31 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         while (ti + 1 < B.n && lb >= F.blk_start[ti + 1]) ti++;
         t0 = (lb - F.blk_start[ti]) * F.tpb;
         nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
+    };
+    // The workgroup's run: launch tiles [t_lo, t_hi) (an equal share), in the
+    // blocks [b_lo, b_hi); a block at either end is decoded here and by the
+    // neighbouring workgroup, each taking its own tiles of it.
+    const uint32_t ntile = B.start[B.n];
+    const uint32_t t_lo = (uint32_t)((uint64_t)ntile * blockIdx.x / gridDim.x);
+    const uint32_t t_hi = (uint32_t)((uint64_t)ntile * (blockIdx.x + 1) / gridDim.x);
+    auto block_of = [&](uint32_t t) {
+        uint32_t ti = 0;
+        while (ti + 1 < B.n && t >= B.start[ti + 1]) ti++;
+        return F.blk_start[ti] + (t - B.start[ti]) / F.tpb;
+    };
+    const uint32_t b_lo = t_lo < t_hi ? block_of(t_lo) : 0u;
+    const uint32_t b_hi = t_lo < t_hi ? block_of(t_hi - 1u) + 1u : 0u;
+    // bit lb - b_lo of a bitmap: LDS word address and mask
+    auto bit_w = [&](uint32_t base, uint32_t lb) { return base + 4u * ((lb - b_lo) >> 5); };
+    auto bit_m = [&](uint32_t lb) { return 1u << ((lb - b_lo) & 31u); };
+    // block lb: tensor, first tile, and the run's tiles of it as block
+    // offsets [j_lo, j_hi)
+    auto run_part = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &j_lo, uint32_t &j_hi) {
+        uint32_t nt;
+        locate(lb, ti, t0, nt);
+        const uint32_t gs = B.start[ti] + t0;
+        j_lo = t_lo > gs ? t_lo - gs : 0u;
+        j_hi = t_hi < gs + nt ? t_hi - gs : nt;
     };
     auto report = [&](uint32_t lb, int ln) {  // a wait ran out
         if (ln == 0) {
@@ -734,19 +755,21 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             if (lb - b_lo >= nbuf) {
                 // the buffer's previous block (lb - nbuf, possibly another
                 // producer's) must have been placed there, then settled: its
-                // confirm count is only meaningful once its stamp is up
-                uint32_t pti, pt0, pnt, v;
+                // done count is only meaningful once its stamp is up; the
+                // count to wait for is the run's tiles of that block
+                uint32_t pti, pt0, pjl, pjh, v;
                 uint64_t sv;
-                locate(lb - nbuf, pti, pt0, pnt);
+                run_part(lb - nbuf, pti, pt0, pjl, pjh);
+                const uint32_t pnt = pjh - pjl;
                 if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == lb - nbuf + 1u; }) ||
-                    !fused_poll(confirm_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
+                    !fused_poll(done_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
                     report(lb, ln);
                     break;
                 }
             }
             const uint64_t stamp = (uint64_t)(lb + 1u) << 32;
             if (ln == 0) {
-                __hip_atomic_store((lds_word *)(size_t)confirm_w(x), 0u, __ATOMIC_RELAXED,
+                __hip_atomic_store((lds_word *)(size_t)done_w(x), 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
                 __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -811,10 +834,15 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 ((hh_block_status *)Fk.status)[gb] = st;
             }
             wave_sync();  // every lane's buffer writes are issued before the release
-            if (ln == 0)
-                __hip_atomic_store((lds_dword *)(size_t)state_w(x),
-                                   stamp | cap | kStFinal | (code == HH_OK ? 0u : kStFailed), __ATOMIC_RELEASE,
+            if (ln == 0) {
+                if (code != HH_OK)
+                    __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFailOff, lb), bit_m(lb), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFinalOff, lb), bit_m(lb), __ATOMIC_RELEASE,
+                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | cap, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
     } else {
         // ---- consumer
@@ -823,13 +851,6 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
         const uint32_t wbase = kFusedConsOff + c * B.wave_lds;
         uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
-        auto settle = [&](uint32_t x, int ln) {
-            // the tile's LDS reads are complete (their values fed the V table)
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-            if (ln == 0)
-                __hip_atomic_fetch_add((lds_word *)(size_t)confirm_w(x), 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_WORKGROUP);
-        };
         // zeros and HH_ERR_CORRUPTED_DATA for tile t of tensor ti (a tile of
         // a failed block), after this wave's earlier stores have completed
         auto fail_tile = [&](uint32_t ti, uint32_t t, int ln) {
@@ -848,65 +869,65 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             if (B.status[ti] != nullptr && ln == 0)
                 ((int32_t HH_GLOBAL *)B.status[ti])[t] = HH_ERR_CORRUPTED_DATA;
         };
-        // the tile decoded before its block was final
-        bool pending = false;
-        uint32_t p_lb = 0, p_x = 0, p_ti = 0, p_t = 0;
-        auto resolve = [&](int ln) -> bool {
-            uint64_t v;
-            if (!fused_poll(state_w(p_x), ln, v, [&](uint64_t s) {
-                    return (uint32_t)(s >> 32) == p_lb + 1u && ((uint32_t)s & kStFinal) != 0u;
-                })) {
-                report(p_lb, ln);
-                return false;
-            }
-            if ((uint32_t)v & kStFailed) fail_tile(p_ti, p_t, ln);
-            settle(p_x, ln);
-            pending = false;
-            return true;
-        };
-        // tile `off` of block lb of the range: this wave's next one
-        uint32_t lb = b_lo, off = c, ti = 0, t0 = 0, nt = 0;
-        if (lb < b_hi) locate(lb, ti, t0, nt);
+        // tile `off` of block lb: this wave's next one (run tile j belongs
+        // to consumer j mod nc)
+        uint32_t lb = b_lo, off = 0, ti = 0, t0 = 0, jl = 0, jh = 0;
+        bool aborted = false;
+        if (lb < b_hi) {
+            run_part(lb, ti, t0, jl, jh);
+            off = jl + c;
+        }
         for (;;) {
-            while (lb < b_hi && off >= nt) {
-                off -= nt;
+            while (lb < b_hi && off >= jh) {
+                off -= jh;
                 lb++;
-                if (lb < b_hi) locate(lb, ti, t0, nt);
+                if (lb < b_hi) {
+                    run_part(lb, ti, t0, jl, jh);
+                    off += jl;
+                }
             }
             if (lb >= b_hi) break;
             const int ln = opaque_lane();
-            if (pending && !resolve(ln)) break;
             const uint32_t x = (lb - b_lo) % nbuf;
             const uint32_t tb = B.tb[ti];
             const uint32_t need = (off + 1u) * tb;
             uint64_t v;
             if (!fused_poll(state_w(x), ln, v, [&](uint64_t s) {
-                    // the tile's bytes are there (kStFinal exceeds any need)
-                    return (uint32_t)(s >> 32) == lb + 1u && ((uint32_t)s & (kStFinal | kStBytes)) >= need;
+                    return (uint32_t)(s >> 32) == lb + 1u && (uint32_t)s >= need;  // the tile's bytes are there
                 })) {
                 report(lb, ln);
+                aborted = true;
                 break;
             }
-            const bool fin = ((uint32_t)v & kStFinal) != 0u;
-            if (fin && ((uint32_t)v & kStFailed)) {
-                fail_tile(ti, t0 + off, ln);
-                settle(x, ln);
-            } else {
-                const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
-                tile_body<DT, true>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln, one, n4, [&]() {
-                    if (fin) settle(x, ln);
-                });
-                if (!fin) {
-                    pending = true;
-                    p_lb = lb;
-                    p_x = x;
-                    p_ti = ti;
-                    p_t = t0 + off;
-                }
-            }
+            const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+            tile_body<DT, false>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln, one, n4, [&]() {
+                // the tile's LDS reads are complete (their values fed the V table)
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                if (ln == 0)
+                    __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            });
             off += nc;
         }
-        if (pending) resolve(opaque_lane());
+        // every block of the run complete: rewrite this wave's tiles of the
+        // failed ones
+        if (!aborted) {
+            const int ln = opaque_lane();
+            for (uint32_t b = b_lo; b < b_hi; b++) {
+                uint32_t v, bti, bt0, bjl, bjh;
+                if (!fused_poll(bit_w(kFusedFinalOff, b), ln, v, [&](uint32_t w) { return (w & bit_m(b)) != 0u; })) {
+                    report(b, ln);
+                    break;
+                }
+                run_part(b, bti, bt0, bjl, bjh);
+                const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b),
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (f & bit_m(b)) {
+                    const uint32_t r0 = B.start[bti] + bt0 + bjl - t_lo;  // run index of tile bjl
+                    for (uint32_t j = bjl + (c + nc - r0 % nc) % nc; j < bjh; j += nc) fail_tile(bti, bt0 + j, ln);
+                }
+            }
+        }
     }
 }
 
@@ -1041,9 +1062,9 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
         F.blk_start[B.n] = nb;
         B.one = 1.0f;
         B.neg4 = -4;
-        // per consumer: the V table shares space with one parked column block
+        // per consumer: the V table shares space with the parked output tile
         const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);
-        const uint32_t obytes = 64 * (dtype == HH_F32 ? kHalfPitch<HH_F32> : kHalfPitch<HH_BF16>);
+        const uint32_t obytes = 64 * (dtype == HH_F32 ? kParkPitch<HH_F32> : kParkPitch<HH_BF16>);
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
         B.wave_lds = B.vo_bytes;
         // one workgroup per CU: kFusedMaxWaves waves (fewer consumers when
@@ -1066,6 +1087,11 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
         const uint32_t threads = 64u * (F.np + nc);
         uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256);
         if (grid > nb) grid = nb;
+        // equal runs of tiles; a run spans at most its tile count + 1 blocks,
+        // which must fit the bitmaps
+        if (grid > total) grid = total;
+        if ((total + grid - 1) / grid > kFusedMaxRange - 1)
+            grid = (total + kFusedMaxRange - 2) / (kFusedMaxRange - 1);
         const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
         hipError_t e = hipSuccess;
 #define HH_LAUNCH_FUSED(DTV)                                                                                \
