@@ -643,15 +643,16 @@ def wl_hct3(args, torch, H, O):
     torch.cuda.synchronize()
     ms_step = T.mean_s() * 1e3 / args.steps
     per = ms_step / 1e3
-    flop = 4.0 * n ** 3          # two n x n x n GEMMs
+    flop = 4.0 * n ** 3          # the two dense n x n x n products of the transform
     achieved = flop / per / 1e12
     peak = 2500.0
     roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
-            "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA, 2 + 3 passes, f32 accumulation; "
-                       "+ bitmap scatter and the amax / scale passes)"),
+            "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA on the even / odd split of the "
+                       "cosine bases: half-depth products, 2 + 3 passes, f32 accumulation; + butterfly, "
+                       "bitmap scatter and the amax / scale passes)"),
             "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
-            "mfma_type": "f16", "mfma_flop_per_launch": 5 * 2 * n ** 3}
+            "mfma_type": "f16", "mfma_flop_per_launch": 5 * n ** 3}
     return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, "f16-split-mfma/f32",
                 "synthetic (4096x4096 N(0,0.02), torch seed 17, turbo defaults)",
                 {"rows": n, "cols": n, "retention": 0.20, "coefficients": int(keep),

@@ -86,6 +86,7 @@ struct GemmArgs {
     uint32_t d_rows, d_cols;      // extent written (planes: the padded extent)
     uint32_t ksteps;
     uint32_t tiles_m, tiles_n;
+    uint32_t m_split, b_koff;     // tiles at m0 >= m_split (when not 0) read Bt from column b_koff
 };
 
 // OUT: HH_F32 / HH_F16 / HH_BF16, or kOutPlanes (f16 hi / lo planes).
@@ -120,7 +121,8 @@ __global__ __launch_bounds__(kThreads, 1) void dct_gemm_kernel(GemmArgs g) {
         const uint16_t *base = p == 0 ? g.a_hi : p == 1 ? g.a_lo : p == 2 ? g.b_hi : g.b_lo;
         const uint32_t ld = p < 2 ? g.lda : g.ldb;
         const uint32_t r0 = p < 2 ? m0 : n0;
-        src[i] = base + (size_t)(r0 + row) * ld + k;
+        const uint32_t koff = p >= 2 && g.m_split != 0u && m0 >= g.m_split ? g.b_koff : 0u;
+        src[i] = base + (size_t)(r0 + row) * ld + k + koff;
         dst[i] = p * kPlane + rb * kBlock;
     }
     auto issue = [&](uint32_t step) {
@@ -256,6 +258,99 @@ __global__ __launch_bounds__(256) void operand_planes_kernel(const float *__rest
     if (lo) lo[idx] = (_Float16)(v - (float)h);
 }
 
+// The even / odd split of B_n^T: P[m][k] = B_n[2k + (m >= n/2)][m mod n/2],
+// an n x n/2 plane pair (n a multiple of 512: no padding).
+__global__ __launch_bounds__(256) void basis_split_planes_kernel(uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
+                                                                 uint32_t n) {
+    const uint32_t nh = n / 2;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)n * nh) return;
+    const uint32_t m = (uint32_t)(idx / nh), k = (uint32_t)(idx % nh);
+    const uint32_t f = 2u * k + (m >= nh ? 1u : 0u), i = m % nh;
+    const uint64_t q = ((uint64_t)f * (2ull * i + 1ull)) % (4ull * n);
+    const double sf = f == 0 ? sqrt(1.0 / (double)n) : sqrt(2.0 / (double)n);
+    const double b = sf * cospi((double)q / (2.0 * (double)n));
+    const _Float16 h = (_Float16)b;
+    const _Float16 l = (_Float16)(b - (double)h);
+    hi[idx] = __builtin_bit_cast(uint16_t, h);
+    lo[idx] = __builtin_bit_cast(uint16_t, l);
+}
+
+// operand_planes_kernel with the columns in even / odd order: column k of
+// the matrix goes to k / 2, or cols / 2 + k / 2 when odd (cols even, rows
+// padded to Rp with zeros).  Each thread takes two adjacent columns.
+__global__ __launch_bounds__(256) void operand_planes_eo_kernel(const float *__restrict__ x, uint32_t rows,
+                                                                uint32_t cols, uint32_t ld,
+                                                                const float *__restrict__ scale,
+                                                                _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                                                uint32_t Rp) {
+    const uint32_t ch = cols / 2;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)Rp * ch) return;
+    const uint32_t r = (uint32_t)(idx / ch), k2 = (uint32_t)(idx % ch);
+    float ve = 0.0f, vo = 0.0f;
+    if (r < rows) {
+        const float sc = *scale;
+        ve = x[(size_t)r * ld + 2u * k2] * sc;
+        vo = x[(size_t)r * ld + 2u * k2 + 1u] * sc;
+    }
+    const size_t oe = (size_t)r * cols + k2, oo = oe + ch;
+    const _Float16 he = (_Float16)ve, ho = (_Float16)vo;
+    hi[oe] = he;
+    hi[oo] = ho;
+    if (lo) {
+        lo[oe] = (_Float16)(ve - (float)he);
+        lo[oo] = (_Float16)(vo - (float)ho);
+    }
+}
+
+// The butterfly of an even / odd split product (see launch_dct_butterfly);
+// each thread takes four adjacent columns of one row pair.
+template <int OUT>
+__global__ __launch_bounds__(256) void butterfly_kernel(const float *__restrict__ y, uint32_t mh, uint32_t n,
+                                                        const float *__restrict__ scale, void *__restrict__ out,
+                                                        uint32_t ldd) {
+    const uint32_t nq = n / 4;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)mh * nq) return;
+    const uint32_t m = (uint32_t)(idx / nq), c = 4u * (uint32_t)(idx % nq);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 e = *reinterpret_cast<const f4 *>(y + (size_t)m * n + c);
+    const f4 o = *reinterpret_cast<const f4 *>(y + (size_t)(mh + m) * n + c);
+    const uint32_t m2 = 2u * mh - 1u - m;
+    if constexpr (OUT == kOutPlanes) {
+        // columns c, c + 2 -> c / 2, c / 2 + 1; c + 1, c + 3 -> n/2 + the same
+        const f4 a = e + o, b = e - o;
+        _Float16 *hi = reinterpret_cast<_Float16 *>(out), *lo = hi + (size_t)2 * mh * n;
+        const uint32_t ce = c / 2, co = n / 2 + c / 2;
+        auto put2 = [&](uint32_t row, float v0, float v1, uint32_t col) {
+            const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+            const size_t o2 = (size_t)row * n + col;
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<h2 *>(hi + o2) = h2{h0, h1};
+            *reinterpret_cast<h2 *>(lo + o2) = h2{(_Float16)(v0 - (float)h0), (_Float16)(v1 - (float)h1)};
+        };
+        put2(m, a[0], a[2], ce);
+        put2(m, a[1], a[3], co);
+        put2(m2, b[0], b[2], ce);
+        put2(m2, b[1], b[3], co);
+    } else {
+        const float sc = scale ? *scale : 1.0f;
+        const f4 a = (e + o) * sc, b = (e - o) * sc;
+        if constexpr (OUT == HH_F32) {
+            *reinterpret_cast<f4 *>(reinterpret_cast<float *>(out) + (size_t)m * ldd + c) = a;
+            *reinterpret_cast<f4 *>(reinterpret_cast<float *>(out) + (size_t)m2 * ldd + c) = b;
+        } else {
+            typedef uint16_t u4 __attribute__((ext_vector_type(4)));
+            auto cv = [](float v) { return (uint16_t)(OUT == HH_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v)); };
+            *reinterpret_cast<u4 *>(reinterpret_cast<uint16_t *>(out) + (size_t)m * ldd + c) =
+                u4{cv(a[0]), cv(a[1]), cv(a[2]), cv(a[3])};
+            *reinterpret_cast<u4 *>(reinterpret_cast<uint16_t *>(out) + (size_t)m2 * ldd + c) =
+                u4{cv(b[0]), cv(b[1]), cv(b[2]), cv(b[3])};
+        }
+    }
+}
+
 template <bool BLO, int OUT>
 hipError_t launch_one(const GemmArgs &g, hipStream_t s) {
     hipError_t e = hipFuncSetAttribute((const void *)dct_gemm_kernel<BLO, OUT>,
@@ -287,6 +382,38 @@ hipError_t launch_operand_planes(const float *x, uint32_t rows, uint32_t cols, u
     return hipGetLastError();
 }
 
+hipError_t launch_dct_basis_split_planes(uint16_t *hi, uint16_t *lo, uint32_t n, hipStream_t s) {
+    const uint64_t total = (uint64_t)n * (n / 2);
+    hipLaunchKernelGGL(basis_split_planes_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, hi, lo, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_operand_planes_eo(const float *x, uint32_t rows, uint32_t cols, uint32_t ld, const float *scale,
+                                    uint16_t *hi, uint16_t *lo, hipStream_t s) {
+    const uint32_t Rp = dct_planes_rows(rows);
+    const uint64_t total = (uint64_t)Rp * (cols / 2);
+    hipLaunchKernelGGL(operand_planes_eo_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, x, rows,
+                       cols, ld, scale, reinterpret_cast<_Float16 *>(hi), reinterpret_cast<_Float16 *>(lo), Rp);
+    return hipGetLastError();
+}
+
+hipError_t launch_dct_butterfly(const float *y, uint32_t mh, uint32_t n, bool eo_planes, const float *scale,
+                                int32_t dtype, void *out, uint32_t ldd, hipStream_t s) {
+    const uint64_t total = (uint64_t)mh * (n / 4);
+    const dim3 grid((uint32_t)((total + 255) / 256));
+    if (eo_planes)
+        hipLaunchKernelGGL(butterfly_kernel<kOutPlanes>, grid, dim3(256), 0, s, y, mh, n, scale, out, ldd);
+    else if (dtype == HH_F32)
+        hipLaunchKernelGGL(butterfly_kernel<HH_F32>, grid, dim3(256), 0, s, y, mh, n, scale, out, ldd);
+    else if (dtype == HH_F16)
+        hipLaunchKernelGGL(butterfly_kernel<HH_F16>, grid, dim3(256), 0, s, y, mh, n, scale, out, ldd);
+    else if (dtype == HH_BF16)
+        hipLaunchKernelGGL(butterfly_kernel<HH_BF16>, grid, dim3(256), 0, s, y, mh, n, scale, out, ldd);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_dct_gemm(const DctGemm &p, hipStream_t s) {
     if (p.M == 0 || p.N == 0) return hipSuccess;
     GemmArgs g;
@@ -294,8 +421,10 @@ hipError_t launch_dct_gemm(const DctGemm &p, hipStream_t s) {
     g.a_lo = p.a_lo;
     g.b_hi = p.b_hi;
     g.b_lo = p.b_lo;
-    g.lda = dct_planes_cols(p.K);
-    g.ldb = dct_planes_cols(p.K);
+    g.lda = p.lda ? p.lda : dct_planes_cols(p.K);
+    g.ldb = p.ldb ? p.ldb : dct_planes_cols(p.K);
+    g.m_split = p.m_split;
+    g.b_koff = p.b_koff;
     g.out_scale = p.out_scale;
     g.d = p.d;
     g.tiles_m = (p.M + kTile - 1) / kTile;

@@ -260,14 +260,14 @@ hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_o
     return hipGetLastError();
 }
 
-// The context's cached basis planes of B_n (or B_n^T); two are kept, the
-// older is replaced.
-static int32_t planes_for(hh_context *ctx, uint32_t n, bool transposed, hipStream_t s, const uint16_t **hi,
+// The context's cached basis planes: kind 0 B_n, 1 B_n^T, 2 the even / odd
+// split of B_n^T; two are kept, the older is replaced.
+static int32_t planes_for(hh_context *ctx, uint32_t n, int kind, hipStream_t s, const uint16_t **hi,
                           const uint16_t **lo) {
-    const uint64_t plane = (uint64_t)dct_planes_rows(n) * dct_planes_cols(n);
+    const uint64_t plane = kind == 2 ? (uint64_t)n * (n / 2) : (uint64_t)dct_planes_rows(n) * dct_planes_cols(n);
     for (int i = 0; i < 2; i++) {
         hh_context::Basis &b = ctx->dct_basis[i];
-        if (b.hl && b.n == n && b.transposed == transposed) {
+        if (b.hl && b.n == n && b.kind == kind) {
             b.stamp = ++ctx->dct_stamp;
             *hi = b.hl;
             *lo = b.hl + plane;
@@ -291,12 +291,121 @@ static int32_t planes_for(hh_context *ctx, uint32_t n, bool transposed, hipStrea
         return from_hip(e);
     }
     b.n = n;
-    b.transposed = transposed;
+    b.kind = kind;
     b.stamp = ++ctx->dct_stamp;
-    e = launch_dct_basis_planes(b.hl, b.hl + plane, n, transposed, s);
+    e = kind == 2 ? launch_dct_basis_split_planes(b.hl, b.hl + plane, n, s)
+                  : launch_dct_basis_planes(b.hl, b.hl + plane, n, kind == 1, s);
     if (e != hipSuccess) return from_hip(e);
     *hi = b.hl;
     *lo = b.hl + plane;
+    return HH_OK;
+}
+
+// The context's transform scratch, at least `need` bytes.
+static int32_t split_scratch(hh_context *ctx, size_t need, hipStream_t s) {
+    if (ctx->split_bytes >= need) return HH_OK;
+    if (ctx->d_split) {
+        hipError_t e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = hipFree(ctx->d_split);
+        ctx->d_split = nullptr;
+        ctx->split_bytes = 0;
+        if (e != hipSuccess) return from_hip(e);
+    }
+    hipError_t e = hipMalloc(&ctx->d_split, need);
+    if (e != hipSuccess) {
+        ctx->d_split = nullptr;
+        return from_hip(e);
+    }
+    ctx->split_bytes = need;
+    return HH_OK;
+}
+
+// Inverse 2-D DCT of an h x w matrix (both multiples of 512) on the even /
+// odd split of the cosine bases: B_n[k][n - 1 - i] = (-1)^k B_n[k][i], so
+// row i < n/2 of B_n^T X is E_i + O_i and row n - 1 - i is E_i - O_i, with
+// E over the even frequencies and O over the odd ones -- two products of
+// half the depth in one launch (the stacked split basis against the input's
+// planes with their columns in even / odd order), then a butterfly pass.
+//   P  = butterfly(split(B_w)^T (C 2^e)^T)     (w x h, as even / odd planes)
+//   X  = 2^-e butterfly(split(B_h)^T P^T)      (h x w)
+static int32_t dct2d_eo(hh_context *ctx, const float *d_in, float *d_out, uint32_t h, uint32_t w, hipStream_t s,
+                        bool f16_exact, int32_t cvt_dtype, void *cvt_out, bool *converted) {
+    const uint16_t *wh, *wl, *hh_, *hl;
+    int32_t rc = planes_for(ctx, w, 2, s, &wh, &wl);
+    if (rc != HH_OK) return rc;
+    rc = planes_for(ctx, h, 2, s, &hh_, &hl);
+    if (rc != HH_OK) return rc;
+    if (h == w) {
+        wh = hh_;
+        wl = hl;
+    }
+    const uint32_t np = 1024;
+    const uint64_t total = (uint64_t)h * w;
+    // scratch: maxima and constants, the input's planes, the stacked E / O
+    // products (f32), the intermediate's planes
+    const size_t off_in = ((np + 4) * sizeof(float) + 255) & ~(size_t)255;
+    const size_t off_y = off_in + ((total * (f16_exact ? 2 : 4) + 255) & ~(uint64_t)255);
+    const size_t off_mid = off_y + total * 4;
+    rc = split_scratch(ctx, off_mid + total * 4, s);
+    if (rc != HH_OK) return rc;
+    uint8_t *sp = reinterpret_cast<uint8_t *>(ctx->d_split);
+    float *partial = reinterpret_cast<float *>(sp);
+    float *consts = partial + np;
+    uint16_t *in_hi = reinterpret_cast<uint16_t *>(sp + off_in);
+    uint16_t *in_lo = f16_exact ? nullptr : in_hi + total;
+    float *y = reinterpret_cast<float *>(sp + off_y);
+    uint16_t *mid_hi = reinterpret_cast<uint16_t *>(sp + off_mid);
+    uint16_t *mid_lo = mid_hi + total;
+    hipLaunchKernelGGL(amax_kernel, dim3(np), dim3(256), 0, s, d_in, total, partial);
+    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, partial, np, w, consts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e);
+    e = launch_operand_planes_eo(d_in, h, w, w, consts + 2, in_hi, in_lo, s);
+    if (e != hipSuccess) return from_hip(e);
+    DctGemm g1;
+    g1.a_hi = wh;
+    g1.a_lo = wl;
+    g1.b_hi = in_hi;
+    g1.b_lo = in_lo;
+    g1.out_scale = nullptr;
+    g1.d = y;
+    g1.ldd = h;
+    g1.d_dtype = HH_F32;
+    g1.d_planes = false;
+    g1.M = w;
+    g1.N = h;
+    g1.K = w / 2;
+    g1.lda = w / 2;
+    g1.ldb = w;
+    g1.m_split = w / 2;
+    g1.b_koff = w / 2;
+    e = launch_dct_gemm(g1, s);
+    if (e == hipSuccess) e = launch_dct_butterfly(y, w / 2, h, true, nullptr, HH_F32, mid_hi, 0, s);
+    if (e != hipSuccess) return from_hip(e);
+    DctGemm g2;
+    g2.a_hi = hh_;
+    g2.a_lo = hl;
+    g2.b_hi = mid_hi;
+    g2.b_lo = mid_lo;
+    g2.out_scale = nullptr;
+    g2.d = y;
+    g2.ldd = w;
+    g2.d_dtype = HH_F32;
+    g2.d_planes = false;
+    g2.M = h;
+    g2.N = w;
+    g2.K = h / 2;
+    g2.lda = h / 2;
+    g2.ldb = h;
+    g2.m_split = h / 2;
+    g2.b_koff = h / 2;
+    e = launch_dct_gemm(g2, s);
+    const bool cvt = cvt_out != nullptr;
+    if (e == hipSuccess)
+        e = launch_dct_butterfly(y, h / 2, w, false, consts + 3, cvt ? cvt_dtype : HH_F32, cvt ? cvt_out : d_out,
+                                 w, s);
+    if (e != hipSuccess) return from_hip(e);
+    if (converted) *converted = cvt;
     return HH_OK;
 }
 
@@ -309,10 +418,18 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
     const uint64_t total = (uint64_t)h * w;
     // the inverse needs B^T planes, the forward B planes; a square matrix
     // uses one set for both products
+    // the inverse of a matrix whose sides are multiples of 512 runs on the
+    // even / odd split of the bases (half the MFMA work, see dct2d_eo)
+    // (its last pass stores four outputs at a time: 16-byte aligned f32 or
+    // 8-byte aligned 16-bit outputs)
+    const uintptr_t out_addr = (uintptr_t)(inverse && cvt_out != nullptr ? cvt_out : (void *)d_out);
+    const bool out_aligned = (out_addr & (inverse && cvt_out != nullptr ? 7u : 15u)) == 0;
+    if (inverse && h % 512u == 0 && w % 512u == 0 && out_aligned)
+        return dct2d_eo(ctx, d_in, d_out, h, w, s, f16_exact, cvt_dtype, cvt_out, converted);
     const uint16_t *wh, *wl, *hh_, *hl;
-    int32_t rc = planes_for(ctx, w, inverse, s, &wh, &wl);
+    int32_t rc = planes_for(ctx, w, inverse ? 1 : 0, s, &wh, &wl);
     if (rc != HH_OK) return rc;
-    rc = planes_for(ctx, h, inverse, s, &hh_, &hl);
+    rc = planes_for(ctx, h, inverse ? 1 : 0, s, &hh_, &hl);
     if (rc != HH_OK) return rc;
     if (h == w) {  // the second lookup may have replaced the first's slot
         wh = hh_;
@@ -327,21 +444,8 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
     const size_t off_in = ((np + 4) * sizeof(float) + 255) & ~(size_t)255;  // after the maxima and constants
     const size_t off_mid = off_in + ((in_plane * (need_lo ? 4 : 2) + 255) & ~(uint64_t)255);
     const size_t need = off_mid + mid_plane * 4;
-    if (ctx->split_bytes < need) {
-        if (ctx->d_split) {
-            hipError_t e = hipStreamSynchronize(s);
-            if (e == hipSuccess) e = hipFree(ctx->d_split);
-            ctx->d_split = nullptr;
-            ctx->split_bytes = 0;
-            if (e != hipSuccess) return from_hip(e);
-        }
-        hipError_t e = hipMalloc(&ctx->d_split, need);
-        if (e != hipSuccess) {
-            ctx->d_split = nullptr;
-            return from_hip(e);
-        }
-        ctx->split_bytes = need;
-    }
+    rc = split_scratch(ctx, need, s);
+    if (rc != HH_OK) return rc;
     uint8_t *sp = reinterpret_cast<uint8_t *>(ctx->d_split);
     float *partial = reinterpret_cast<float *>(sp);
     float *consts = partial + np;

@@ -19,12 +19,12 @@ struct hh_context {
     // (grown on demand, kept until the context is destroyed).
     void *d_scratch = nullptr;
     size_t scratch_bytes = 0;
-    // Whole-matrix DCT bases B_n (or B_n^T) as f16 hi / lo planes
-    // (dct_gemm.hip), two cached.
+    // Whole-matrix DCT bases as f16 hi / lo planes (dct_gemm.hip), two
+    // cached: kind 0 B_n, 1 B_n^T, 2 the even / odd split of B_n^T.
     struct Basis {
         uint32_t n = 0;
-        bool transposed = false;
-        uint16_t *hl = nullptr;  // hi plane then lo plane, dct_planes_rows(n) x dct_planes_cols(n) each
+        int kind = 0;
+        uint16_t *hl = nullptr;  // hi plane then lo plane
         uint64_t stamp = 0;
     };
     Basis dct_basis[2];
@@ -188,6 +188,9 @@ hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_o
 // with d_planes the hi / lo planes of the next product's Bt (its padded
 // extent, zeros included; lo follows hi at dct_planes_rows(M) x
 // dct_planes_cols(N) elements).
+// lda / ldb: the planes' row strides when not dct_planes_cols(K) (0: that);
+// rows m >= m_split (when not 0, a multiple of 256) read Bt from column
+// b_koff on.
 struct DctGemm {
     const uint16_t *a_hi, *a_lo, *b_hi, *b_lo;
     const float *out_scale;  // device scalar, or null for 1
@@ -196,12 +199,29 @@ struct DctGemm {
     int32_t d_dtype;
     bool d_planes;
     uint32_t M, N, K;
+    uint32_t lda = 0, ldb = 0, m_split = 0, b_koff = 0;
 };
 hipError_t launch_dct_gemm(const DctGemm &p, hipStream_t s);
 uint32_t dct_planes_rows(uint32_t n);
 uint32_t dct_planes_cols(uint32_t n);
 // hi / lo planes of B_n (P[m][k] = B_n[m][k]) or of B_n^T.
 hipError_t launch_dct_basis_planes(uint16_t *hi, uint16_t *lo, uint32_t n, bool transposed, hipStream_t s);
+// The even / odd split of B_n^T (n a multiple of 512): an n x n/2 plane
+// pair, rows m < n/2 holding B_n[2k][m] and rows n/2 + m holding
+// B_n[2k + 1][m] (k < n/2).
+hipError_t launch_dct_basis_split_planes(uint16_t *hi, uint16_t *lo, uint32_t n, hipStream_t s);
+// launch_operand_planes with the columns in even / odd order (column k to
+// k / 2, or cols / 2 + k / 2 when odd; cols a multiple of 32).
+hipError_t launch_operand_planes_eo(const float *x, uint32_t rows, uint32_t cols, uint32_t ld, const float *scale,
+                                    uint16_t *hi, uint16_t *lo, hipStream_t s);
+// The butterfly of an even / odd split product: y (2 mh x n f32, row stride
+// n) holds E in rows [0, mh) and O in rows [mh, 2 mh); row m of the result
+// is E_m + O_m and row 2 mh - 1 - m is E_m - O_m (m < mh).  eo_planes: the
+// result as f16 hi / lo planes with its columns in even / odd order (the
+// next product's Bt, 2 mh x n, lo at 2 mh n elements after hi); else the
+// result times *scale (null: 1) in dtype, row stride ldd.
+hipError_t launch_dct_butterfly(const float *y, uint32_t mh, uint32_t n, bool eo_planes, const float *scale,
+                                int32_t dtype, void *out, uint32_t ldd, hipStream_t s);
 // hi (and lo, unless null) planes of an f32 rows x cols matrix (row stride
 // ld) times *scale.
 hipError_t launch_operand_planes(const float *x, uint32_t rows, uint32_t cols, uint32_t ld, const float *scale,

@@ -135,7 +135,8 @@ def test_decompress_16bit_outputs_and_device_variant():
     assert np.array_equal(out.cpu().numpy().view(np.uint32), f32.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 64), (1, 77), (77, 1), (37, 53), (200, 120), (512, 512)])
+@pytest.mark.parametrize("rows,cols", [(64, 64), (1, 77), (77, 1), (37, 53), (200, 120), (512, 512), (1024, 512),
+                                       (512, 1536)])
 def test_idct_dct_2d(rows, cols):
     T = G.torch()
     rng = np.random.default_rng(rows + 7 * cols)
@@ -150,6 +151,45 @@ def test_idct_dct_2d(rows, cols):
     y = T.empty_like(d_c)
     G.ctx().dct_2d(x, rows, cols, y, stream=G.stream())
     assert rel_err(y.cpu().numpy(), c) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols,k,l", [(512, 1024, 5, 30), (1024, 512, 0, 1), (512, 512, 511, 256)])
+def test_idct_even_odd_split_single_coefficient(rows, cols, k, l):
+    # sides that are multiples of 512 take the even / odd split of the bases:
+    # one coefficient of either frequency parity per axis lands in the right
+    # rows (i and n - 1 - i) with the right sign
+    T = G.torch()
+    c = np.zeros((rows, cols), np.float32)
+    c[k, l] = 1.0
+    x = T.empty(rows, cols, dtype=T.float32, device="cuda")
+    G.ctx().idct_2d(T.from_numpy(c).cuda(), rows, cols, x)
+
+    def basis(n, kk):
+        s = np.sqrt((1.0 if kk == 0 else 2.0) / n)
+        return s * np.cos(np.pi * kk * (2 * np.arange(n) + 1) / (2 * n))
+    ref = np.outer(basis(rows, k), basis(cols, l))
+    assert np.abs(x.cpu().numpy() - ref).max() <= 1e-6
+
+
+def test_decompress_even_odd_split_vs_oracle_and_16bit():
+    # a 1024 x 512 HCT3 tensor: the split inverse against the oracle, and its
+    # bf16 / f16 outputs the rounding of its f32 output
+    Hm = H()
+    T = G.torch()
+    rng = np.random.default_rng(1536)
+    shape = (1024, 512)
+    total = 1024 * 512
+    data = container([random_fragment(rng, total, 0.25), random_fragment(rng, total, 0.05)])
+    got = dec().decompress_to_gpu(data, shape, stream=G.stream()).cpu().numpy()
+    rc, ref = O.hct3_decode(data, shape)
+    assert rc == O.OK
+    err = rel_err(got, ref)
+    print(f"shape {shape}: max|gpu - oracle| = {err:.2e} x RMS")
+    assert err <= TOL
+    b16 = dec().decompress_to_gpu(data, shape, dtype=Hm.BF16).view(T.int16).cpu().numpy().view(np.uint16)
+    h16 = dec().decompress_to_gpu(data, shape, dtype=Hm.F16).view(T.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(b16, G.bf16_bits(got))
+    assert np.array_equal(h16, G.f16_bits(got))
 
 
 def test_idct_single_coefficient_closed_form():
