@@ -190,3 +190,102 @@ def test_argument_errors():
     assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], 14) == Hm.UNSUPPORTED
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(100, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], 2) == Hm.OK
+
+
+def both_paths(L, dtype, tpb, blob=None, lens=None):
+    """The same blocks through the fused call and the two-launch call:
+    outputs, tile statuses and block records (the two-launch path's LZ4
+    records are hh_lz4_decompress_batch's)."""
+    L2 = dict(L)
+    if blob is not None:
+        L2["blob"] = blob
+    if lens is not None:
+        L2["in_len"] = lens
+    fo, st, fs = fused(L2, dtype, tpb)
+    bo, codes, scratch, bs = decode(L2, dtype)
+    del scratch
+    return fo, st, fs, bo, codes, bs
+
+
+def assert_same(T, dtype, fo, fs, bo, bs):
+    Hm = H()
+    view = T.int32 if dtype == Hm.F32 else T.int16
+    for i, (a, b, sa, sb) in enumerate(zip(fo, bo, fs, bs)):
+        assert T.equal(a.view(view), b.view(view)), i
+        assert T.equal(sa, sb), i
+
+
+def test_many_tensors_small_blocks_f16():
+    # ten tensors (two launches of at most eight), blocks of one and of three
+    # tiles, f16 output
+    Hm = H()
+    T = G.torch()
+    rng = np.random.default_rng(51)
+    shapes = [("t%d" % i, r, c) for i, (r, c) in enumerate(
+        [(64, 64), (128, 64), (64, 192), (192, 128), (64, 64), (256, 64), (128, 128), (64, 320), (320, 64),
+         (128, 192)])]
+    ks = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, len(shapes))]
+    for tpb in (1, 3):
+        L = encode_fixed(Hm, shapes, ks, seed=52 + tpb, tpb=tpb)
+        fo, st, fs, bo, codes, bs = both_paths(L, Hm.F16, tpb)
+        assert (st["code"] == 0).all() and (codes == 0).all()
+        assert all((s.cpu().numpy() == 0).all() for s in fs)
+        assert_same(T, Hm.F16, fo, fs, bo, bs)
+
+
+def test_large_retention_tiles():
+    # k = 4096 (2,816-byte tiles, 5 per block) and k = 3000 (7 per block):
+    # fewer consumer waves fit the LDS next to the block buffers
+    Hm = H()
+    T = G.torch()
+    for k, shape in ((4096, ("a", 320, 256)), (3000, ("b", 256, 448))):
+        tpb = Hm.FUSED_BLOCK_BYTES // Hm.hctt_tile_bytes(k)
+        L = encode_fixed(Hm, [shape], [k], seed=k, tpb=tpb)
+        fo, st, fs, bo, codes, bs = both_paths(L, Hm.F32, tpb)
+        assert (st["code"] == 0).all() and (codes == 0).all()
+        assert_same(T, Hm.F32, fo, fs, bo, bs)
+        check_against_oracle(L, fo)
+
+
+def test_failed_blocks_at_run_boundaries():
+    # 188 blocks of two tiles over up to 256 workgroups: nearly every block is
+    # shared by two workgroups' runs; ten corrupted blocks poison all of
+    # their tiles in both, exactly as the two-launch path does
+    Hm = H()
+    T = G.torch()
+    shapes = [("a", 1024, 512), ("b", 512, 1024), ("c", 768, 640)]
+    ks = [Hm.hctt_retain_count(0.3), Hm.hctt_retain_count(0.2), Hm.hctt_retain_count(0.4)]
+    tpb = 2
+    L = encode_fixed(Hm, shapes, ks, seed=61, tpb=tpb)
+    n = L["in_off"].size
+    assert n == 188
+    rng = np.random.default_rng(62)
+    bad = sorted(rng.choice(n, 10, replace=False).tolist())
+    blob = L["blob"].copy()
+    for b in bad:
+        o = int(L["in_off"][b])
+        blob[o + 1:o + int(L["in_len"][b])] ^= 0x5A
+    fo, st, fs, bo, codes, bs = both_paths(L, Hm.F32, tpb, blob=blob)
+    assert (st["code"][bad] != 0).all() and (np.delete(st["code"], bad) == 0).all()
+    assert np.array_equal(st["code"], codes)
+    assert_same(T, Hm.F32, fo, fs, bo, bs)
+    # and the corrupted tiles are zeros
+    corrupted = sum(int((s.cpu().numpy() == Hm.CORRUPTED_DATA).sum()) for s in fs)
+    assert corrupted == tpb * len(bad)  # every tensor's tile count is even: full blocks
+    for t, a, s in zip(L["tensors"], fo, fs):
+        a = a.cpu().numpy().reshape(t["rows"] // 64, 64, t["cols"] // 64, 64)
+        for tt in np.nonzero(s.cpu().numpy() == Hm.CORRUPTED_DATA)[0]:
+            r, c = divmod(int(tt), t["cols"] // 64)
+            assert (a[r, :, c, :] == 0).all()
+
+
+def test_fewer_tiles_than_workgroups():
+    # two tiles in all: two workgroups, one tile each, sharing the one block
+    Hm = H()
+    T = G.torch()
+    k = Hm.hctt_retain_count(0.25)
+    L = encode_fixed(Hm, [("a", 64, 128)], [k], seed=71, tpb=2)
+    assert L["in_off"].size == 1
+    fo, st, fs, bo, codes, bs = both_paths(L, Hm.BF16, 2)
+    assert (st["code"] == 0).all()
+    assert_same(T, Hm.BF16, fo, fs, bo, bs)
