@@ -235,8 +235,8 @@ __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, i
 // with this wave's V table / output park at LDS byte offset wbase (V is the
 // same area as a pointer).  `consumed` runs once the tile's bytes are no
 // longer read: right after the V table is built (HALF), or just before the
-// output stores (whole-tile park).
-template <int DT, bool HALF, typename Hook>
+// output stores (whole-tile park; EARLY: right after the V table there too).
+template <int DT, bool HALF, bool EARLY = false, typename Hook>
 __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint32_t t, const uint8_t *pay,
                                           uint32_t *V, uint32_t wbase, const u32x4 *mtab, int lane, float one,
                                           int32_t n4, Hook &&consumed) {
@@ -298,7 +298,7 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     }
     wave_sync();
     // the tile's bytes have all been read (their values feed the V stores)
-    if constexpr (HALF) consumed();
+    if constexpr (HALF || EARLY) consumed();
 
     // 4. GEMM1 A fragments.  A[upar][vpar][s] holds, for row
     //    u = 2 l32 + upar, the columns v = 2 pi(16 s + 8 h + e) + vpar,
@@ -482,7 +482,7 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     }
     if constexpr (!HALF) {
         wave_sync();
-        consumed();
+        if constexpr (!EARLY) consumed();
         // 8. coalesced row stores (16 bytes per lane)
         store(0u, std::integral_constant<uint32_t, 64>{});
     }
@@ -554,53 +554,64 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 // and the LZ4 blocks that hold them (each block holds whole tiles of one
 // tensor: block j of tensor i tiles [j tpb, j tpb + tpb) of it, the last
 // block the rest; a block at either end of a run is decoded by both
-// workgroups that share it).  Its first np waves are producers: producer p
-// decodes blocks p, p + np, p + 2 np, ... of the range with the LDS-ring
-// decoder (lz4_ring.hpp, the whole output kept in
-// LDS: at most kFusedMax bytes) into a ring of nbuf block buffers (block i of
-// the range into buffer i mod nbuf).  The other nc waves are consumers:
-// consumer c decodes tiles c, c + nc, c + 2 nc, ... of the run, in that
-// order, straight from the buffers with tile_body (the whole output tile
-// parked in LDS, then stored).  The tile bytes never reach HBM, and the LZ4
-// parse of a block runs while consumers already decode its first tiles.
+// workgroups that share it, each taking its own tiles of it).  Every wave
+// of the workgroup does both kinds of work, claimed from two LDS counters:
+//   next_block  the run's blocks are decoded in order, each by the wave that
+//               claims it, with the LDS-ring decoder (lz4_ring.hpp, the whole
+//               output kept in LDS: at most kFusedMax bytes) into a ring of
+//               nbuf block buffers (block i of the range into buffer
+//               i mod nbuf);
+//   next_tile   the run's tiles are decoded in order, each by the wave that
+//               claims it, straight from the block buffer with tile_body (the
+//               whole output tile parked in LDS, then stored).
+// A wave first claims the next block if its buffer is free (compare and
+// swap: only a free buffer's block is ever claimed this way), else the next
+// tile; a claimed tile whose block nobody has claimed yet makes its wave
+// claim and decode the blocks up to it first (waiting for their buffers).
+// A wave's LDS area is its tile's V table and output park, or its input
+// stage while it decodes a block.  The tile bytes never reach HBM, and the
+// LZ4 parse of a block runs while other waves already decode its first
+// tiles.
 //
-// Two LDS words per buffer order the two sides:
+// Two LDS words per buffer order the two kinds of work:
 //   state[x]  (64 bits) 1 + the number of the block the buffer holds, and
-//             the bytes of it decoded so far (published after every
-//             sequence; the block's tile bytes in full once it is complete);
-//   done[x]   how many of that block's tiles have been read.  A producer
-//             refills buffer x with block i only once state[x] names block
-//             i - nbuf (which another producer may place there late) and
-//             done[x] equals its tile count; it clears done[x] before
-//             publishing block i.
-// A consumer decodes a tile as soon as the published bytes cover it.  Two
-// LDS bitmaps over the workgroup's blocks record which are complete and
-// which failed.  A failed block's producer zeroes its buffer from the first
-// tile it had not released (those tiles then fail their bitmap count), and
-// after the last tile each consumer waits for every block of the run to be
-// complete and rewrites its own tiles of the failed ones as zeros with
-// HH_ERR_CORRUPTED_DATA: every tile of a failed block ends up so, as with the
-// two-launch path.  A block that decodes short (no error) leaves the rest of
-// its buffer zeroed: those tiles fail their bitmap count.
+//             the bytes of it decoded so far (published after LZ4
+//             sequences; the whole block only by its final store);
+//   done[x]   how many of that block's tiles have been read.  Block i may
+//             take buffer x once state[x] names block i - nbuf (placed
+//             there by another wave, possibly late) and done[x] equals that
+//             block's tile count in the run; its decoder clears done[x]
+//             before publishing block i.
+// A tile is decoded as soon as the published bytes cover it.  Two LDS
+// bitmaps over the workgroup's blocks record which are complete and which
+// failed.  A failed block's decoder zeroes its buffer from the first tile it
+// had not released (those tiles then fail their bitmap count).  After its
+// last tile each wave waits until its stores are done and counts itself
+// finished; once every block of the run is complete, if one failed, the
+// waves wait for each other and rewrite the failed blocks' tiles (run tile r
+// by wave r mod W) as zeros with HH_ERR_CORRUPTED_DATA: every tile of a
+// failed block ends up so, as with the two-launch path.  A block that
+// decodes short (no error) leaves the rest of its buffer zeroed: those tiles
+// fail their bitmap count.
 //
-// No wait can deadlock: the lowest-numbered block not yet decoded waits only
-// for the tiles of an earlier (decoded) block, whose consumers wait only for
-// blocks before those tiles, all decoded; the consumers' final wait is for
-// producers that wait on nothing but tiles already read.  Every wait is bounded all the same (kSpinLimit polls); one that
-// runs out (not expected) raises the workgroup's abort word, every wave of
-// the workgroup then leaves, and the block record of the block waited on
-// reports HH_ERR_DEVICE.
+// No wait can deadlock: a wave waits on a buffer only for block i, whose
+// buffer's previous block i - nbuf has all its run tiles claimed (they come
+// before a claimed tile of block i or later); a tile's wave waits for its
+// block's bytes, whose decoder waits only on lower blocks; every such chain
+// descends to a block whose buffer is free.  Every wait is bounded all the
+// same (kSpinLimit polls); one that runs out (not expected) raises the
+// workgroup's abort word, every wave then leaves, and the block record of
+// the block waited on reports HH_ERR_DEVICE.
 //
 // The input stage holds 8 KiB of a block's compressed bytes (a 16 KiB block
-// is staged in two or three batches of loads), leaving the LDS to the
-// consumers' whole-tile output parks and three block buffers.
+// is staged in two or three batches of loads): it fits a wave's tile area,
+// which leaves the rest of the LDS to three block buffers.
 constexpr uint32_t kFusedStageData = 8 * 1024;
 using FusedRing = ring::RingDec<16384, kFusedStageData, true>;
 constexpr uint32_t kFusedMax = 16384 - 32;
 constexpr uint32_t kFusedBuf = 16384;  // a block buffer: the decoder's ring
-constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a producer's input stage
+constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a decoder's input stage
 constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's budget
-constexpr int kFusedProducers = 2;
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
@@ -615,22 +626,25 @@ struct FusedBlocks {
     uint32_t blk_base;                    // global number of this launch's block 0
     uint32_t blk_start[kMaxTensors + 1];  // first block of each tensor, launch-relative
     uint32_t tpb;                         // tiles per block
-    uint32_t np, nbuf;                    // producer waves, block buffers
-    uint32_t stage_off, buf_off;          // LDS byte offsets of the stages and the buffers
+    uint32_t nbuf;                        // block buffers
+    uint32_t buf_off;                     // LDS byte offset of the buffers
 };
 
 // Workgroup LDS layout after the shared part: [block descriptor][state[8]
-// (8 bytes each), done[8], abort, the complete and failed bitmaps][consumer
-// areas][producer stages][block buffers].
+// (8 bytes each), done[8], abort, next_block, next_tile, finished, the
+// complete and failed bitmaps][wave areas][block buffers].
 constexpr uint32_t kFusedFOff = kSharedBytes;
 constexpr uint32_t kFusedFlagsOff = kFusedFOff + ((sizeof(FusedBlocks) + 15u) & ~15u);
 constexpr uint32_t kFusedStateOff = kFusedFlagsOff;
 constexpr uint32_t kFusedDoneOff = kFusedStateOff + 8 * kFusedMaxBufs;
 constexpr uint32_t kFusedAbortOff = kFusedDoneOff + 4 * kFusedMaxBufs;
-constexpr uint32_t kFusedFinalOff = kFusedAbortOff + 4;
+constexpr uint32_t kFusedNextBlockOff = kFusedAbortOff + 4;
+constexpr uint32_t kFusedNextTileOff = kFusedNextBlockOff + 4;
+constexpr uint32_t kFusedFinishedOff = kFusedNextTileOff + 4;
+constexpr uint32_t kFusedFinalOff = kFusedFinishedOff + 4;
 constexpr uint32_t kFusedFailOff = kFusedFinalOff + kFusedMaxRange / 8;
 constexpr uint32_t kFusedFlagWords = (kFusedFailOff + kFusedMaxRange / 8 - kFusedFlagsOff) / 4;
-constexpr uint32_t kFusedConsOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
+constexpr uint32_t kFusedWaveOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
 
 typedef uint32_t __attribute__((address_space(3))) lds_word;
 typedef uint64_t __attribute__((address_space(3))) lds_dword;
@@ -681,8 +695,7 @@ template <int DT>
 __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(TileBatch Bk, FusedBlocks Fk,
                                                                               const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63;
-    // wave-uniform (scalar) wave number: roles and block choices are scalar
+    // wave-uniform (scalar) wave number
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t nthr = blockDim.x;
     u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
@@ -693,12 +706,12 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     for (uint32_t i = threadIdx.x; i < kMTabBytes / 16; i += nthr) mtab[i] = basis[i];
     for (uint32_t i = threadIdx.x; i < kFusedFlagWords; i += nthr) reinterpret_cast<uint32_t *>(smem + kFusedFlagsOff)[i] = 0u;
     if (threadIdx.x == 0) *reinterpret_cast<u32x4 *>(smem + kZeroOff) = u32x4{0u, 0u, 0u, 0u};
-    __syncthreads();  // the only workgroup barrier: the two roles never meet at one
+    __syncthreads();  // the only workgroup barrier
     const TileBatch &B = *reinterpret_cast<const TileBatch *>(smem + kBatchOff);
     // the LDS copy serves the indexed block table; pointers come from the
     // kernel arguments, where the compiler knows them to be global
     const FusedBlocks &F = *reinterpret_cast<const FusedBlocks *>(smem + kFusedFOff);
-    const uint32_t np = Fk.np, nbuf = Fk.nbuf, nc = (nthr >> 6) - np;
+    const uint32_t nw = nthr >> 6, nbuf = Fk.nbuf;
     auto state_w = [](uint32_t x) { return kFusedStateOff + 8u * x; };
     auto done_w = [](uint32_t x) { return kFusedDoneOff + 4u * x; };
 
@@ -710,18 +723,26 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
     };
     // The workgroup's run: launch tiles [t_lo, t_hi) (an equal share), in the
-    // blocks [b_lo, b_hi); a block at either end is decoded here and by the
-    // neighbouring workgroup, each taking its own tiles of it.
-    const uint32_t ntile = B.start[B.n];
+    // blocks [b_lo, b_hi).
+    const uint32_t ntile = Bk.start[Bk.n];
     const uint32_t t_lo = (uint32_t)((uint64_t)ntile * blockIdx.x / gridDim.x);
     const uint32_t t_hi = (uint32_t)((uint64_t)ntile * (blockIdx.x + 1) / gridDim.x);
-    auto block_of = [&](uint32_t t) {
-        uint32_t ti = 0;
+    // launch tile t -> tensor, block, block offset
+    auto tile_at = [&](uint32_t t, uint32_t &ti, uint32_t &lb, uint32_t &off) {
+        ti = 0;
         while (ti + 1 < B.n && t >= B.start[ti + 1]) ti++;
-        return F.blk_start[ti] + (t - B.start[ti]) / F.tpb;
+        const uint32_t j = t - B.start[ti];
+        lb = F.blk_start[ti] + j / F.tpb;
+        off = j % F.tpb;
     };
-    const uint32_t b_lo = t_lo < t_hi ? block_of(t_lo) : 0u;
-    const uint32_t b_hi = t_lo < t_hi ? block_of(t_hi - 1u) + 1u : 0u;
+    uint32_t b_lo = 0, b_hi = 0;
+    if (t_lo < t_hi) {
+        uint32_t ti, lb, off;
+        tile_at(t_lo, ti, lb, off);
+        b_lo = lb;
+        tile_at(t_hi - 1u, ti, lb, off);
+        b_hi = lb + 1u;
+    }
     // bit lb - b_lo of a bitmap: LDS word address and mask
     auto bit_w = [&](uint32_t base, uint32_t lb) { return base + 4u * ((lb - b_lo) >> 5); };
     auto bit_m = [&](uint32_t lb) { return 1u << ((lb - b_lo) & 31u); };
@@ -745,188 +766,242 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             ((hh_block_status *)Fk.status)[Fk.blk_base + lb] = st;
         }
     };
+    // this wave's LDS area: a tile's V table and output park, or the input
+    // stage of the block it decodes
+    const uint32_t wbase = kFusedWaveOff + wave * B.wave_lds;
+    uint8_t *stage = smem + wbase + FusedRing::kSFront;
+    uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
 
-    if (wave < np) {
-        // ---- producer
-        uint8_t *stage = smem + Fk.stage_off + wave * kFusedStage + FusedRing::kSFront;
-        for (uint32_t lb = b_lo + wave; lb < b_hi; lb += np) {
-            const int ln = opaque_lane();
-            const uint32_t x = (lb - b_lo) % nbuf;
-            if (lb - b_lo >= nbuf) {
-                // the buffer's previous block (lb - nbuf, possibly another
-                // producer's) must have been placed there, then settled: its
-                // done count is only meaningful once its stamp is up; the
-                // count to wait for is the run's tiles of that block
-                uint32_t pti, pt0, pjl, pjh, v;
-                uint64_t sv;
-                run_part(lb - nbuf, pti, pt0, pjl, pjh);
-                const uint32_t pnt = pjh - pjl;
-                if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == lb - nbuf + 1u; }) ||
-                    !fused_poll(done_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
-                    report(lb, ln);
-                    break;
-                }
-            }
-            const uint64_t stamp = (uint64_t)(lb + 1u) << 32;
-            if (ln == 0) {
-                __hip_atomic_store((lds_word *)(size_t)done_w(x), 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-            uint32_t ti, t0, nt;
-            locate(lb, ti, t0, nt);
-            const uint32_t tb = B.tb[ti];
-            const uint32_t cap = nt * tb;
-            uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
-            const uint32_t gb = Fk.blk_base + lb;
-            int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
-            uint64_t pos = 0, req = 0;
-            const uint64_t ioff = Fk.in_off[gb];
-            const uint32_t ilen = Fk.in_len[gb];
-            FusedRing d;
-            d.ring = rbuf;
-            d.stage = stage;
-            d.gbuf = Fk.in;
-            d.gsz = Fk.in_total;
-            d.ioff = ioff;
-            d.a0 = 0;
-            d.obase = nullptr;
-            d.cap = cap;
-            d.sb = 0;
-            d.at_end = false;
-            d.wso = ring::kNoWin;
-            d.w = 0;
-            d.op = 0;
-            d.fl = 0;
-            d.lane = ln;
-            // bytes published to the consumers so far (every lane's copies
-            // are issued: each copy piece ends with a wave barrier)
-            uint32_t published = 0;
-            auto publish = [&](uint32_t op) {
-                if (op >= published + tb) {
-                    published = op;
-                    if (ln == 0)
-                        __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | op, __ATOMIC_RELEASE,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-            };
-            if (ioff > Fk.in_total || (uint64_t)ilen > Fk.in_total - ioff) {
-                code = HH_ERR_INVALID_ARGUMENT;
-            } else {
-                ring::parse_block(d, ilen, code, detail, pos, req, false, publish);
-            }
-            // a complete block: the bytes it did not produce read as zeros; a
-            // failed one: zeros from its first tile not released to the
-            // consumers (released tiles are rewritten by their consumers)
-            const uint32_t zfrom = code == HH_OK ? d.op : (published / tb) * tb;
-            if (zfrom < cap) {
-                wave_sync();
-                wave_zero_fill(rbuf + zfrom, cap - zfrom, ln);
-            }
-            if (ln == 0) {
-                hh_block_status st;
-                st.code = code;
-                st.detail = detail;
-                st.position = pos;
-                st.required = req;
-                st.written = code == HH_OK ? d.op : 0u;
-                ((hh_block_status *)Fk.status)[gb] = st;
-            }
-            wave_sync();  // every lane's buffer writes are issued before the release
-            if (ln == 0) {
-                if (code != HH_OK)
-                    __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFailOff, lb), bit_m(lb), __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFinalOff, lb), bit_m(lb), __ATOMIC_RELEASE,
-                                      __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | cap, __ATOMIC_RELEASE,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+    // may block lb take its buffer now?  (once true, true until lb is placed)
+    auto buf_free = [&](uint32_t lb) {
+        if (lb - b_lo < nbuf) return true;
+        const uint32_t x = (lb - b_lo) % nbuf;
+        const uint64_t sv = uniform(lds_load_acq(state_w(x), uint64_t{}));
+        if ((uint32_t)(sv >> 32) != lb - nbuf + 1u) return false;
+        uint32_t pti, pt0, pjl, pjh;
+        run_part(lb - nbuf, pti, pt0, pjl, pjh);
+        return uniform(lds_load_acq(done_w(x), uint32_t{})) == pjh - pjl;
+    };
+    // the next block to claim (the word counts the run's blocks claimed)
+    auto next_block = [&]() {
+        return b_lo + uniform(__hip_atomic_load((lds_word *)(size_t)kFusedNextBlockOff, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP));
+    };
+    // claims block nb if it is still the next one
+    auto claim = [&](uint32_t nb, int ln) {
+        uint32_t e = nb - b_lo;
+        if (ln == 0)
+            __hip_atomic_compare_exchange_strong((lds_word *)(size_t)kFusedNextBlockOff, &e, nb - b_lo + 1u,
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return uniform(e) == nb - b_lo;
+    };
+    // decodes block lb (claimed by this wave) into its buffer, after waiting
+    // for the buffer; false when a wait ran out
+    auto decode = [&](uint32_t lb) {
+        const int ln = opaque_lane();
+        const uint32_t x = (lb - b_lo) % nbuf;
+        if (lb - b_lo >= nbuf) {
+            // the buffer's previous block (lb - nbuf, possibly placed late by
+            // another wave) must have been placed there, then read: its done
+            // count is only meaningful once its stamp is up
+            uint32_t pti, pt0, pjl, pjh, v;
+            uint64_t sv;
+            run_part(lb - nbuf, pti, pt0, pjl, pjh);
+            const uint32_t pnt = pjh - pjl;
+            if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == lb - nbuf + 1u; }) ||
+                !fused_poll(done_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
+                report(lb, ln);
+                return false;
             }
         }
-    } else {
-        // ---- consumer
-        const uint32_t c = wave - np;
-        const float one = Bk.one;
-        const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
-        const uint32_t wbase = kFusedConsOff + c * B.wave_lds;
-        uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
-        // zeros and HH_ERR_CORRUPTED_DATA for tile t of tensor ti (a tile of
-        // a failed block), after this wave's earlier stores have completed
-        auto fail_tile = [&](uint32_t ti, uint32_t t, int ln) {
-            constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
-            constexpr uint32_t per_row = 64u * esz / 16u;
-            constexpr uint32_t rows_per = 64u / per_row;
-            const uint32_t cols = B.cols[ti], tpr = B.tiles_per_row[ti];
+        const uint64_t stamp = (uint64_t)(lb + 1u) << 32;
+        if (ln == 0) {
+            __hip_atomic_store((lds_word *)(size_t)done_w(x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        uint32_t ti, t0, nt;
+        locate(lb, ti, t0, nt);
+        const uint32_t tb = B.tb[ti];
+        const uint32_t cap = nt * tb;
+        uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+        const uint32_t gb = Fk.blk_base + lb;
+        int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
+        uint64_t pos = 0, req = 0;
+        const uint64_t ioff = Fk.in_off[gb];
+        const uint32_t ilen = Fk.in_len[gb];
+        FusedRing d;
+        d.ring = rbuf;
+        d.stage = stage;
+        d.gbuf = Fk.in;
+        d.gsz = Fk.in_total;
+        d.ioff = ioff;
+        d.a0 = 0;
+        d.obase = nullptr;
+        d.cap = cap;
+        d.sb = 0;
+        d.at_end = false;
+        d.wso = ring::kNoWin;
+        d.w = 0;
+        d.op = 0;
+        d.fl = 0;
+        d.lane = ln;
+        // bytes published so far (every lane's copies are issued: each copy
+        // piece ends with a wave barrier).  The whole block is published only
+        // by the final state store below: were the last tile released here,
+        // the block could be counted done and its buffer refilled before
+        // that store, which would then overwrite the new block's state.
+        uint32_t published = 0;
+        auto publish = [&](uint32_t op) {
+            if (op >= published + tb && op < cap) {
+                published = op;
+                if (ln == 0)
+                    __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | op, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        };
+        if (ioff > Fk.in_total || (uint64_t)ilen > Fk.in_total - ioff) {
+            code = HH_ERR_INVALID_ARGUMENT;
+        } else {
+            ring::parse_block(d, ilen, code, detail, pos, req, false, publish);
+        }
+        // a complete block: the bytes it did not produce read as zeros; a
+        // failed one: zeros from its first tile not released (released
+        // tiles are rewritten at the end)
+        const uint32_t zfrom = code == HH_OK ? d.op : (published / tb) * tb;
+        if (zfrom < cap) {
+            wave_sync();
+            wave_zero_fill(rbuf + zfrom, cap - zfrom, ln);
+        }
+        if (ln == 0) {
+            hh_block_status st;
+            st.code = code;
+            st.detail = detail;
+            st.position = pos;
+            st.required = req;
+            st.written = code == HH_OK ? d.op : 0u;
+            ((hh_block_status *)Fk.status)[gb] = st;
+        }
+        wave_sync();  // every lane's buffer writes are issued before the release
+        if (ln == 0) {
+            if (code != HH_OK)
+                __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFailOff, lb), bit_m(lb), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFinalOff, lb), bit_m(lb), __ATOMIC_RELEASE,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | cap, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        return true;
+    };
+
+    const float one = Bk.one;
+    const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
+    bool aborted = false;
+    for (;;) {
+        // the next block, when its buffer is free
+        {
+            const uint32_t nb = next_block();
+            if (nb < b_hi && buf_free(nb) && claim(nb, opaque_lane())) {
+                if (!decode(nb)) {
+                    aborted = true;
+                    break;
+                }
+                continue;
+            }
+        }
+        // else the next tile
+        const int ln = opaque_lane();
+        uint32_t r = 0;
+        if (ln == 0)
+            r = __hip_atomic_fetch_add((lds_word *)(size_t)kFusedNextTileOff, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        r = uniform(r);
+        if (r >= t_hi - t_lo) break;
+        uint32_t ti, lb, off;
+        tile_at(t_lo + r, ti, lb, off);
+        // its block and every one before it claimed (by this wave if need be)
+        for (;;) {
+            const uint32_t nb = next_block();
+            if (nb > lb) break;
+            if (claim(nb, opaque_lane()) && !decode(nb)) {
+                aborted = true;
+                break;
+            }
+        }
+        if (aborted) break;
+        const int ln2 = opaque_lane();
+        const uint32_t x = (lb - b_lo) % nbuf;
+        const uint32_t tb = B.tb[ti];
+        const uint32_t need = (off + 1u) * tb;
+        uint64_t v;
+        if (!fused_poll(state_w(x), ln2, v, [&](uint64_t s) {
+                return (uint32_t)(s >> 32) == lb + 1u && (uint32_t)s >= need;  // the tile's bytes are there
+            })) {
+            report(lb, ln2);
+            aborted = true;
+            break;
+        }
+        const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
+        tile_body<DT, false, true>(B, ti, t_lo + r - B.start[ti], rbuf + off * tb, V, wbase, mtab, ln2, one, n4,
+                                   [&]() {
+                                       // the tile's LDS reads are complete (their values fed the V table)
+                                       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                                       if (ln2 == 0)
+                                           __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u,
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                                   });
+    }
+    if (aborted) return;
+    // this wave's tile stores are complete: count it finished
+    const int ln = opaque_lane();
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    if (ln == 0)
+        __hip_atomic_fetch_add((lds_word *)(size_t)kFusedFinishedOff, 1u, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    // every block of the run complete; any failed?
+    bool any_failed = false;
+    for (uint32_t b = b_lo; b < b_hi; b++) {
+        uint32_t v;
+        if (!fused_poll(bit_w(kFusedFinalOff, b), ln, v, [&](uint32_t w) { return (w & bit_m(b)) != 0u; })) {
+            report(b, ln);
+            return;
+        }
+        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP));
+        any_failed = any_failed || (f & bit_m(b)) != 0u;
+    }
+    if (!any_failed) return;
+    // rewrite the failed blocks' tiles (run tile r by wave r mod nw) once
+    // every wave's own stores are complete
+    {
+        uint32_t v;
+        if (!fused_poll(kFusedFinishedOff, ln, v, [&](uint32_t c) { return c == nw; })) {
+            report(b_lo, ln);
+            return;
+        }
+    }
+    constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
+    constexpr uint32_t per_row = 64u * esz / 16u;
+    constexpr uint32_t rows_per = 64u / per_row;
+    for (uint32_t b = b_lo; b < b_hi; b++) {
+        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP));
+        if ((f & bit_m(b)) == 0u) continue;
+        uint32_t bti, bt0, bjl, bjh;
+        run_part(b, bti, bt0, bjl, bjh);
+        const uint32_t r0 = B.start[bti] + bt0 + bjl - t_lo;  // run index of tile bjl
+        const uint32_t cols = B.cols[bti], tpr = B.tiles_per_row[bti];
+        uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[bti];
+        for (uint32_t j = bjl + (wave + nw - r0 % nw) % nw; j < bjh; j += nw) {
+            const uint32_t t = bt0 + j;
             const size_t base = (size_t)(64u * (t / tpr)) * cols + 64u * (t % tpr);
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-            uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[ti];
             for (uint32_t it = 0; it < 64u / rows_per; it++) {
                 const uint32_t row = rows_per * it + (uint32_t)ln / per_row;
                 *(u32x4 HH_GLOBAL *)(o + esz * (base + (size_t)row * cols) + 16u * ((uint32_t)ln % per_row)) =
                     u32x4{0u, 0u, 0u, 0u};
             }
-            if (B.status[ti] != nullptr && ln == 0)
-                ((int32_t HH_GLOBAL *)B.status[ti])[t] = HH_ERR_CORRUPTED_DATA;
-        };
-        // tile `off` of block lb: this wave's next one (run tile j belongs
-        // to consumer j mod nc)
-        uint32_t lb = b_lo, off = 0, ti = 0, t0 = 0, jl = 0, jh = 0;
-        bool aborted = false;
-        if (lb < b_hi) {
-            run_part(lb, ti, t0, jl, jh);
-            off = jl + c;
-        }
-        for (;;) {
-            while (lb < b_hi && off >= jh) {
-                off -= jh;
-                lb++;
-                if (lb < b_hi) {
-                    run_part(lb, ti, t0, jl, jh);
-                    off += jl;
-                }
-            }
-            if (lb >= b_hi) break;
-            const int ln = opaque_lane();
-            const uint32_t x = (lb - b_lo) % nbuf;
-            const uint32_t tb = B.tb[ti];
-            const uint32_t need = (off + 1u) * tb;
-            uint64_t v;
-            if (!fused_poll(state_w(x), ln, v, [&](uint64_t s) {
-                    return (uint32_t)(s >> 32) == lb + 1u && (uint32_t)s >= need;  // the tile's bytes are there
-                })) {
-                report(lb, ln);
-                aborted = true;
-                break;
-            }
-            const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
-            tile_body<DT, false>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln, one, n4, [&]() {
-                // the tile's LDS reads are complete (their values fed the V table)
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-                if (ln == 0)
-                    __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP);
-            });
-            off += nc;
-        }
-        // every block of the run complete: rewrite this wave's tiles of the
-        // failed ones
-        if (!aborted) {
-            const int ln = opaque_lane();
-            for (uint32_t b = b_lo; b < b_hi; b++) {
-                uint32_t v, bti, bt0, bjl, bjh;
-                if (!fused_poll(bit_w(kFusedFinalOff, b), ln, v, [&](uint32_t w) { return (w & bit_m(b)) != 0u; })) {
-                    report(b, ln);
-                    break;
-                }
-                run_part(b, bti, bt0, bjl, bjh);
-                const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b),
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-                if (f & bit_m(b)) {
-                    const uint32_t r0 = B.start[bti] + bt0 + bjl - t_lo;  // run index of tile bjl
-                    for (uint32_t j = bjl + (c + nc - r0 % nc) % nc; j < bjh; j += nc) fail_tile(bti, bt0 + j, ln);
-                }
-            }
+            if (B.status[bti] != nullptr && ln == 0)
+                ((int32_t HH_GLOBAL *)B.status[bti])[t] = HH_ERR_CORRUPTED_DATA;
         }
     }
 }
@@ -1062,29 +1137,27 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
         F.blk_start[B.n] = nb;
         B.one = 1.0f;
         B.neg4 = -4;
-        // per consumer: the V table shares space with the parked output tile
+        // per wave: the V table shares space with the parked output tile, and
+        // both with the input stage of a block the wave decodes
         const uint32_t vbytes = 4 * ((max_k + 7u) & ~7u);
         const uint32_t obytes = 64 * (dtype == HH_F32 ? kParkPitch<HH_F32> : kParkPitch<HH_BF16>);
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
-        B.wave_lds = B.vo_bytes;
-        // one workgroup per CU: kFusedMaxWaves waves (fewer consumers when
-        // their areas leave room for fewer than 3 block buffers)
-        F.np = kFusedProducers;
-        uint32_t nc = kFusedMaxWaves - kFusedProducers, nbuf = 0;
-        const uint32_t fixed = kFusedConsOff + F.np * kFusedStage;
+        B.wave_lds = B.vo_bytes > kFusedStage ? B.vo_bytes : (kFusedStage + 15u) & ~15u;
+        // one workgroup per CU: kFusedMaxWaves waves (fewer when their areas
+        // leave room for fewer than 3 block buffers)
+        uint32_t nw = kFusedMaxWaves, nbuf = 0;
         for (;;) {
-            const uint32_t used = fixed + nc * B.wave_lds;
+            const uint32_t used = kFusedWaveOff + nw * B.wave_lds;
             nbuf = used < kFusedLdsMax ? (kFusedLdsMax - used) / kFusedBuf : 0u;
-            if (nbuf >= 3 || nc == 1) break;
-            nc--;
+            if (nbuf >= 3 || nw == 1) break;
+            nw--;
         }
         if (nbuf < 2) return hipErrorInvalidValue;  // not reached: tiles are at most 3 KiB (k <= 4096)
         if (nbuf > kFusedMaxBufs) nbuf = kFusedMaxBufs;
         F.nbuf = nbuf;
-        F.stage_off = kFusedConsOff + nc * B.wave_lds;
-        F.buf_off = F.stage_off + F.np * kFusedStage;
+        F.buf_off = kFusedWaveOff + nw * B.wave_lds;
         const uint32_t lds = F.buf_off + nbuf * kFusedBuf;
-        const uint32_t threads = 64u * (F.np + nc);
+        const uint32_t threads = 64u * nw;
         uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256);
         if (grid > nb) grid = nb;
         // equal runs of tiles; a run spans at most its tile count + 1 blocks,
