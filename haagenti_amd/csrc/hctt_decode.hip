@@ -550,20 +550,20 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 
 // ---- LZ4 blocks and their tiles in one launch ------------------------------
 //
-// One persistent workgroup per CU takes an equal run of the launch's tiles
-// and the LZ4 blocks that hold them (each block holds whole tiles of one
-// tensor: block j of tensor i tiles [j tpb, j tpb + tpb) of it, the last
-// block the rest; a block at either end of a run is decoded by both
-// workgroups that share it, each taking its own tiles of it).  Every wave
-// of the workgroup does both kinds of work, claimed from two LDS counters:
-//   next_block  the run's blocks are decoded in order, each by the wave that
-//               claims it, with the LDS-ring decoder (lz4_ring.hpp, the whole
-//               output kept in LDS: at most kFusedMax bytes) into a ring of
-//               nbuf block buffers (block i of the range into buffer
-//               i mod nbuf);
-//   next_tile   the run's tiles are decoded in order, each by the wave that
-//               claims it, straight from the block buffer with tile_body (the
-//               whole output tile parked in LDS, then stored).
+// One persistent workgroup per CU (G of them) takes the launch's blocks g,
+// g + G, g + 2 G, ... (its slots 0, 1, 2, ...) and all their tiles (each
+// block holds whole tiles of one tensor: block j of tensor i tiles
+// [j tpb, j tpb + tpb) of it, the last block the rest).  Every wave of the
+// workgroup does both kinds of work, claimed from two LDS counters:
+//   next_block  the slots' blocks are decoded in order, each by the wave
+//               that claims it, with the LDS-ring decoder (lz4_ring.hpp, the
+//               whole output kept in LDS: at most kFusedMax bytes) into a
+//               ring of nbuf block buffers (slot q into buffer q mod nbuf);
+//   next_tile   the slots' tiles are decoded in order (tile slot v: tile
+//               v mod tpb of slot v / tpb, skipped past a short block's
+//               tiles), each by the wave that claims it, straight from the
+//               block buffer with tile_body (the whole output tile parked in
+//               LDS, then stored).
 // A wave first claims the next block if its buffer is free (compare and
 // swap: only a free buffer's block is ever claimed this way), else the next
 // tile; a claimed tile whose block nobody has claimed yet makes its wave
@@ -574,31 +574,31 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 // tiles.
 //
 // Two LDS words per buffer order the two kinds of work:
-//   state[x]  (64 bits) 1 + the number of the block the buffer holds, and
+//   state[x]  (64 bits) 1 + the slot of the block the buffer holds, and
 //             the bytes of it decoded so far (published after LZ4
 //             sequences; the whole block only by its final store);
-//   done[x]   how many of that block's tiles have been read.  Block i may
-//             take buffer x once state[x] names block i - nbuf (placed
-//             there by another wave, possibly late) and done[x] equals that
-//             block's tile count in the run; its decoder clears done[x]
-//             before publishing block i.
+//   done[x]   how many of that block's tiles have been read.  Slot i may
+//             take buffer x once state[x] names slot i - nbuf (placed there
+//             by another wave, possibly late) and done[x] equals that
+//             block's tile count; its decoder clears done[x] before
+//             publishing slot i.
 // A tile is decoded as soon as the published bytes cover it.  Two LDS
-// bitmaps over the workgroup's blocks record which are complete and which
+// bitmaps over the workgroup's slots record which are complete and which
 // failed.  A failed block's decoder zeroes its buffer from the first tile it
 // had not released (those tiles then fail their bitmap count).  After its
 // last tile each wave waits until its stores are done and counts itself
-// finished; once every block of the run is complete, if one failed, the
-// waves wait for each other and rewrite the failed blocks' tiles (run tile r
-// by wave r mod W) as zeros with HH_ERR_CORRUPTED_DATA: every tile of a
-// failed block ends up so, as with the two-launch path.  A block that
-// decodes short (no error) leaves the rest of its buffer zeroed: those tiles
-// fail their bitmap count.
+// finished; once every block of the workgroup is complete, if one failed,
+// the waves wait for each other and rewrite the failed blocks' tiles (tile
+// j of a block by wave j mod W) as zeros with HH_ERR_CORRUPTED_DATA: every
+// tile of a failed block ends up so, as with the two-launch path.  A block
+// that decodes short (no error) leaves the rest of its buffer zeroed: those
+// tiles fail their bitmap count.
 //
-// No wait can deadlock: a wave waits on a buffer only for block i, whose
-// buffer's previous block i - nbuf has all its run tiles claimed (they come
-// before a claimed tile of block i or later); a tile's wave waits for its
-// block's bytes, whose decoder waits only on lower blocks; every such chain
-// descends to a block whose buffer is free.  Every wait is bounded all the
+// No wait can deadlock: a wave waits on a buffer only for slot i, whose
+// buffer's previous slot i - nbuf has all its tiles claimed (they come
+// before a claimed tile of slot i or later); a tile's wave waits for its
+// block's bytes, whose decoder waits only on lower slots; every such chain
+// descends to a slot whose buffer is free.  Every wait is bounded all the
 // same (kSpinLimit polls); one that runs out (not expected) raises the
 // workgroup's abort word, every wave then leaves, and the block record of
 // the block waited on reports HH_ERR_DEVICE.
@@ -615,7 +615,7 @@ constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
-constexpr uint32_t kFusedMaxRange = 4096;  // blocks per workgroup (the bitmaps' size)
+constexpr uint32_t kFusedMaxRange = 4096;  // slots per workgroup (the bitmaps' size)
 
 struct FusedBlocks {
     const uint8_t *in;
@@ -722,40 +722,17 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         t0 = (lb - F.blk_start[ti]) * F.tpb;
         nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
     };
-    // The workgroup's run: launch tiles [t_lo, t_hi) (an equal share), in the
-    // blocks [b_lo, b_hi).
-    const uint32_t ntile = Bk.start[Bk.n];
-    const uint32_t t_lo = (uint32_t)((uint64_t)ntile * blockIdx.x / gridDim.x);
-    const uint32_t t_hi = (uint32_t)((uint64_t)ntile * (blockIdx.x + 1) / gridDim.x);
-    // launch tile t -> tensor, block, block offset
-    auto tile_at = [&](uint32_t t, uint32_t &ti, uint32_t &lb, uint32_t &off) {
-        ti = 0;
-        while (ti + 1 < B.n && t >= B.start[ti + 1]) ti++;
-        const uint32_t j = t - B.start[ti];
-        lb = F.blk_start[ti] + j / F.tpb;
-        off = j % F.tpb;
-    };
-    uint32_t b_lo = 0, b_hi = 0;
-    if (t_lo < t_hi) {
-        uint32_t ti, lb, off;
-        tile_at(t_lo, ti, lb, off);
-        b_lo = lb;
-        tile_at(t_hi - 1u, ti, lb, off);
-        b_hi = lb + 1u;
-    }
-    // bit lb - b_lo of a bitmap: LDS word address and mask
-    auto bit_w = [&](uint32_t base, uint32_t lb) { return base + 4u * ((lb - b_lo) >> 5); };
-    auto bit_m = [&](uint32_t lb) { return 1u << ((lb - b_lo) & 31u); };
-    // block lb: tensor, first tile, and the run's tiles of it as block
-    // offsets [j_lo, j_hi)
-    auto run_part = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &j_lo, uint32_t &j_hi) {
-        uint32_t nt;
-        locate(lb, ti, t0, nt);
-        const uint32_t gs = B.start[ti] + t0;
-        j_lo = t_lo > gs ? t_lo - gs : 0u;
-        j_hi = t_hi < gs + nt ? t_hi - gs : nt;
-    };
-    auto report = [&](uint32_t lb, int ln) {  // a wait ran out
+    // The workgroup's blocks: launch blocks g, g + G, g + 2 G, ... (G
+    // workgroups), its q-th block lb(q) = g + q G, all of whose tiles it
+    // decodes; slot q of a workgroup is decoded into buffer q mod nbuf.
+    const uint32_t nblk = F.blk_start[B.n];
+    const uint32_t g = blockIdx.x, G = gridDim.x;
+    const uint32_t Q = nblk > g ? (nblk - g + G - 1u) / G : 0u;
+    auto lb_of = [&](uint32_t q) { return g + q * G; };
+    // bit q of a bitmap: LDS word address and mask
+    auto bit_w = [&](uint32_t base, uint32_t q) { return base + 4u * (q >> 5); };
+    auto bit_m = [&](uint32_t q) { return 1u << (q & 31u); };
+    auto report = [&](uint32_t q, int ln) {  // a wait ran out
         if (ln == 0) {
             hh_block_status st;
             st.code = HH_ERR_DEVICE;
@@ -763,7 +740,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             st.position = 0;
             st.required = 0;
             st.written = 0;
-            ((hh_block_status *)Fk.status)[Fk.blk_base + lb] = st;
+            ((hh_block_status *)Fk.status)[Fk.blk_base + lb_of(q)] = st;
         }
     };
     // this wave's LDS area: a tile's V table and output park, or the input
@@ -772,53 +749,53 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     uint8_t *stage = smem + wbase + FusedRing::kSFront;
     uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
 
-    // may block lb take its buffer now?  (once true, true until lb is placed)
-    auto buf_free = [&](uint32_t lb) {
-        if (lb - b_lo < nbuf) return true;
-        const uint32_t x = (lb - b_lo) % nbuf;
+    // may slot q take its buffer now?  (once true, true until q is placed)
+    auto buf_free = [&](uint32_t q) {
+        if (q < nbuf) return true;
+        const uint32_t x = q % nbuf;
         const uint64_t sv = uniform(lds_load_acq(state_w(x), uint64_t{}));
-        if ((uint32_t)(sv >> 32) != lb - nbuf + 1u) return false;
-        uint32_t pti, pt0, pjl, pjh;
-        run_part(lb - nbuf, pti, pt0, pjl, pjh);
-        return uniform(lds_load_acq(done_w(x), uint32_t{})) == pjh - pjl;
+        if ((uint32_t)(sv >> 32) != q - nbuf + 1u) return false;
+        uint32_t pti, pt0, pnt;
+        locate(lb_of(q - nbuf), pti, pt0, pnt);
+        return uniform(lds_load_acq(done_w(x), uint32_t{})) == pnt;
     };
-    // the next block to claim (the word counts the run's blocks claimed)
+    // the next slot to claim (the word counts the slots claimed)
     auto next_block = [&]() {
-        return b_lo + uniform(__hip_atomic_load((lds_word *)(size_t)kFusedNextBlockOff, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_WORKGROUP));
+        return uniform(
+            __hip_atomic_load((lds_word *)(size_t)kFusedNextBlockOff, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     };
-    // claims block nb if it is still the next one
-    auto claim = [&](uint32_t nb, int ln) {
-        uint32_t e = nb - b_lo;
+    // claims slot q if it is still the next one
+    auto claim = [&](uint32_t q, int ln) {
+        uint32_t e = q;
         if (ln == 0)
-            __hip_atomic_compare_exchange_strong((lds_word *)(size_t)kFusedNextBlockOff, &e, nb - b_lo + 1u,
+            __hip_atomic_compare_exchange_strong((lds_word *)(size_t)kFusedNextBlockOff, &e, q + 1u,
                                                  __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        return uniform(e) == nb - b_lo;
+        return uniform(e) == q;
     };
-    // decodes block lb (claimed by this wave) into its buffer, after waiting
-    // for the buffer; false when a wait ran out
-    auto decode = [&](uint32_t lb) {
+    // decodes slot q's block (claimed by this wave) into its buffer, after
+    // waiting for the buffer; false when a wait ran out
+    auto decode = [&](uint32_t q) {
         const int ln = opaque_lane();
-        const uint32_t x = (lb - b_lo) % nbuf;
-        if (lb - b_lo >= nbuf) {
-            // the buffer's previous block (lb - nbuf, possibly placed late by
-            // another wave) must have been placed there, then read: its done
-            // count is only meaningful once its stamp is up
-            uint32_t pti, pt0, pjl, pjh, v;
+        const uint32_t x = q % nbuf;
+        if (q >= nbuf) {
+            // the buffer's previous block (slot q - nbuf, possibly placed late
+            // by another wave) must have been placed there, then read: its
+            // done count is only meaningful once its stamp is up
+            uint32_t pti, pt0, pnt, v;
             uint64_t sv;
-            run_part(lb - nbuf, pti, pt0, pjl, pjh);
-            const uint32_t pnt = pjh - pjl;
-            if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == lb - nbuf + 1u; }) ||
+            locate(lb_of(q - nbuf), pti, pt0, pnt);
+            if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == q - nbuf + 1u; }) ||
                 !fused_poll(done_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
-                report(lb, ln);
+                report(q, ln);
                 return false;
             }
         }
-        const uint64_t stamp = (uint64_t)(lb + 1u) << 32;
+        const uint64_t stamp = (uint64_t)(q + 1u) << 32;
         if (ln == 0) {
             __hip_atomic_store((lds_word *)(size_t)done_w(x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+        const uint32_t lb = lb_of(q);
         uint32_t ti, t0, nt;
         locate(lb, ti, t0, nt);
         const uint32_t tb = B.tb[ti];
@@ -884,9 +861,9 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         wave_sync();  // every lane's buffer writes are issued before the release
         if (ln == 0) {
             if (code != HH_OK)
-                __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFailOff, lb), bit_m(lb), __ATOMIC_RELAXED,
+                __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFailOff, q), bit_m(q), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFinalOff, lb), bit_m(lb), __ATOMIC_RELEASE,
+            __hip_atomic_fetch_or((lds_word *)(size_t)bit_w(kFusedFinalOff, q), bit_m(q), __ATOMIC_RELEASE,
                                   __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp | cap, __ATOMIC_RELEASE,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -896,60 +873,63 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
 
     const float one = Bk.one;
     const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
+    const uint32_t tpb = F.tpb;
     bool aborted = false;
     for (;;) {
         // the next block, when its buffer is free
         {
-            const uint32_t nb = next_block();
-            if (nb < b_hi && buf_free(nb) && claim(nb, opaque_lane())) {
-                if (!decode(nb)) {
+            const uint32_t nq = next_block();
+            if (nq < Q && buf_free(nq) && claim(nq, opaque_lane())) {
+                if (!decode(nq)) {
                     aborted = true;
                     break;
                 }
                 continue;
             }
         }
-        // else the next tile
+        // else the next tile: slot v / tpb, tile v % tpb of its block (slots
+        // past a short block's tiles are skipped)
         const int ln = opaque_lane();
-        uint32_t r = 0;
+        uint32_t v = 0;
         if (ln == 0)
-            r = __hip_atomic_fetch_add((lds_word *)(size_t)kFusedNextTileOff, 1u, __ATOMIC_RELAXED,
+            v = __hip_atomic_fetch_add((lds_word *)(size_t)kFusedNextTileOff, 1u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
-        r = uniform(r);
-        if (r >= t_hi - t_lo) break;
-        uint32_t ti, lb, off;
-        tile_at(t_lo + r, ti, lb, off);
+        v = uniform(v);
+        const uint32_t q = v / tpb, off = v % tpb;
+        if (q >= Q) break;
+        uint32_t ti, t0, nt;
+        locate(lb_of(q), ti, t0, nt);
+        if (off >= nt) continue;
         // its block and every one before it claimed (by this wave if need be)
         for (;;) {
-            const uint32_t nb = next_block();
-            if (nb > lb) break;
-            if (claim(nb, opaque_lane()) && !decode(nb)) {
+            const uint32_t nq = next_block();
+            if (nq > q) break;
+            if (claim(nq, opaque_lane()) && !decode(nq)) {
                 aborted = true;
                 break;
             }
         }
         if (aborted) break;
         const int ln2 = opaque_lane();
-        const uint32_t x = (lb - b_lo) % nbuf;
+        const uint32_t x = q % nbuf;
         const uint32_t tb = B.tb[ti];
         const uint32_t need = (off + 1u) * tb;
-        uint64_t v;
-        if (!fused_poll(state_w(x), ln2, v, [&](uint64_t s) {
-                return (uint32_t)(s >> 32) == lb + 1u && (uint32_t)s >= need;  // the tile's bytes are there
+        uint64_t sv;
+        if (!fused_poll(state_w(x), ln2, sv, [&](uint64_t s) {
+                return (uint32_t)(s >> 32) == q + 1u && (uint32_t)s >= need;  // the tile's bytes are there
             })) {
-            report(lb, ln2);
+            report(q, ln2);
             aborted = true;
             break;
         }
         const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
-        tile_body<DT, false, true>(B, ti, t_lo + r - B.start[ti], rbuf + off * tb, V, wbase, mtab, ln2, one, n4,
-                                   [&]() {
-                                       // the tile's LDS reads are complete (their values fed the V table)
-                                       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-                                       if (ln2 == 0)
-                                           __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u,
-                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                                   });
+        tile_body<DT, false, true>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln2, one, n4, [&]() {
+            // the tile's LDS reads are complete (their values fed the V table)
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            if (ln2 == 0)
+                __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        });
     }
     if (aborted) return;
     // this wave's tile stores are complete: count it finished
@@ -958,41 +938,40 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     if (ln == 0)
         __hip_atomic_fetch_add((lds_word *)(size_t)kFusedFinishedOff, 1u, __ATOMIC_RELEASE,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
-    // every block of the run complete; any failed?
+    // every block of the workgroup complete; any failed?
     bool any_failed = false;
-    for (uint32_t b = b_lo; b < b_hi; b++) {
-        uint32_t v;
-        if (!fused_poll(bit_w(kFusedFinalOff, b), ln, v, [&](uint32_t w) { return (w & bit_m(b)) != 0u; })) {
-            report(b, ln);
+    for (uint32_t q = 0; q < Q; q++) {
+        uint32_t w;
+        if (!fused_poll(bit_w(kFusedFinalOff, q), ln, w, [&](uint32_t b) { return (b & bit_m(q)) != 0u; })) {
+            report(q, ln);
             return;
         }
-        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b), __ATOMIC_RELAXED,
+        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, q), __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
-        any_failed = any_failed || (f & bit_m(b)) != 0u;
+        any_failed = any_failed || (f & bit_m(q)) != 0u;
     }
     if (!any_failed) return;
-    // rewrite the failed blocks' tiles (run tile r by wave r mod nw) once
-    // every wave's own stores are complete
+    // rewrite the failed blocks' tiles (tile j of a block by wave j mod nw)
+    // once every wave's own stores are complete
     {
-        uint32_t v;
-        if (!fused_poll(kFusedFinishedOff, ln, v, [&](uint32_t c) { return c == nw; })) {
-            report(b_lo, ln);
+        uint32_t c;
+        if (!fused_poll(kFusedFinishedOff, ln, c, [&](uint32_t n) { return n == nw; })) {
+            report(0, ln);
             return;
         }
     }
     constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
     constexpr uint32_t per_row = 64u * esz / 16u;
     constexpr uint32_t rows_per = 64u / per_row;
-    for (uint32_t b = b_lo; b < b_hi; b++) {
-        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, b), __ATOMIC_RELAXED,
+    for (uint32_t q = 0; q < Q; q++) {
+        const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, q), __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
-        if ((f & bit_m(b)) == 0u) continue;
-        uint32_t bti, bt0, bjl, bjh;
-        run_part(b, bti, bt0, bjl, bjh);
-        const uint32_t r0 = B.start[bti] + bt0 + bjl - t_lo;  // run index of tile bjl
+        if ((f & bit_m(q)) == 0u) continue;
+        uint32_t bti, bt0, bnt;
+        locate(lb_of(q), bti, bt0, bnt);
         const uint32_t cols = B.cols[bti], tpr = B.tiles_per_row[bti];
         uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[bti];
-        for (uint32_t j = bjl + (wave + nw - r0 % nw) % nw; j < bjh; j += nw) {
+        for (uint32_t j = wave; j < bnt; j += nw) {
             const uint32_t t = bt0 + j;
             const size_t base = (size_t)(64u * (t / tpr)) * cols + 64u * (t % tpr);
             for (uint32_t it = 0; it < 64u / rows_per; it++) {
@@ -1158,13 +1137,11 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
         F.buf_off = kFusedWaveOff + nw * B.wave_lds;
         const uint32_t lds = F.buf_off + nbuf * kFusedBuf;
         const uint32_t threads = 64u * nw;
+        // workgroup g takes blocks g, g + grid, ...: at most kFusedMaxRange
+        // of them (the bitmaps' size)
         uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256);
         if (grid > nb) grid = nb;
-        // equal runs of tiles; a run spans at most its tile count + 1 blocks,
-        // which must fit the bitmaps
-        if (grid > total) grid = total;
-        if ((total + grid - 1) / grid > kFusedMaxRange - 1)
-            grid = (total + kFusedMaxRange - 2) / (kFusedMaxRange - 1);
+        if ((nb + grid - 1) / grid > kFusedMaxRange) grid = (nb + kFusedMaxRange - 1) / kFusedMaxRange;
         const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
         hipError_t e = hipSuccess;
 #define HH_LAUNCH_FUSED(DTV)                                                                                \
