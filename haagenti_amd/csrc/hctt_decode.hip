@@ -160,10 +160,10 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
 constexpr int kMaxTensors = 8;
 constexpr int kMaxPrefetch = 3;  // 16-byte loads per lane: tiles up to 3 KiB (k <= 4096)
-// Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs on the
-// 4-byte-aligned path with at most 2 KiB of tile bytes prefetched (168
-// registers, no spills; the LDS also fits 3 workgroups per CU), else 2.
-constexpr int kWavesPerSimd(int dt, bool dw, int np) { return dt != HH_F32 && dw && np == 2 ? 3 : 2; }
+// Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs with
+// at most 2 KiB of tile bytes prefetched (168 registers, no spills; the LDS
+// also fits 3 workgroups per CU), else 2.
+constexpr int kWavesPerSimd(int dt, bool dw, int np) { return dt != HH_F32 && np == 2 ? 3 : 2; }
 struct TileBatch {
     const uint8_t *tiles[kMaxTensors];
     void *out[kMaxTensors];
@@ -194,12 +194,16 @@ constexpr uint32_t kMTabOff = kBatchOff + kBatchBytes;
 constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 
 // Loads the bytes of global tile gt into registers, 16 bytes per lane per
-// KiB, always issuing NP loads (NP KiB cover the tile) (chunks past the tile end re-read
-// its last 16 bytes) so that the wait counts stay static.  Register chunk i
-// holds tile bytes [16*(lane + 64 i), +16) wherever those lie inside the
-// tile.  DW: every tile of
-// the batch starts 4-byte aligned and has a size divisible by 4 (16-byte
-// loads at 4-byte alignment); otherwise bytes are gathered one by one.
+// KiB, always issuing NP loads (NP KiB cover the tile) so that the wait
+// counts stay static.  DW: every tile of the batch starts 4-byte aligned and
+// has a size divisible by 4; register chunk i holds tile bytes
+// [16*(lane + 64 i), +16) wherever those lie inside the tile (chunks past the
+// tile end re-read its last 16 bytes).  Otherwise chunk i holds the bytes
+// from 16*(lane + 64 i) on counted from the tile start rounded down to 4
+// bytes (staged as is, the tile then starts at byte tile_shift of the
+// staging area): 16-byte loads at 4-byte alignment wherever the chunk lies
+// inside the tensor's tile bytes, bytes one by one where it would leave them
+// (the tensor's first and last chunks), anything for chunks past the tile.
 template <bool DW, int NP>
 __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, int lane,
                                               u32x4 (&pf)[NP]) {
@@ -210,7 +214,23 @@ __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, i
 #pragma unroll
     for (int i = 0; i < NP; i++) {
         const uint32_t off = 16u * (lane + 64u * i);
-        if constexpr (DW) {
+        if constexpr (!DW) {
+            const uintptr_t s0 = (uintptr_t)B.tiles[ti];
+            const uintptr_t e0 = s0 + (size_t)(B.start[ti + 1] - B.start[ti]) * tb;  // >= s0 + 515
+            const uintptr_t ts = (uintptr_t)src;
+            const uintptr_t a = (ts & ~(uintptr_t)3) + off;
+            if (a >= s0 && a + 16 <= e0) {
+                pf[i] = *(g_u32x4 *)a;
+            } else if (a < ts + tb) {
+                uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll 1
+                for (int b = 0; b < 16; b++)
+                    if (a + b >= s0 && a + b < ts + tb) d[b >> 2] |= (uint32_t)((g_u8 *)(a + b))[0] << (8 * (b & 3));
+                pf[i] = u32x4{d[0], d[1], d[2], d[3]};
+            } else {
+                pf[i] = *(g_u32x4 *)((e0 - 16) & ~(uintptr_t)3);  // not used
+            }
+        } else {
             // A chunk reaching past the tile end is read at tb - 16 (tiles
             // are >= 515 bytes) and shifted down by s dwords so that byte
             // off lands first; dwords beyond the tile end are don't-care.
@@ -221,14 +241,16 @@ __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, i
             const uint32_t d1 = s == 0 ? v[1] : s == 1 ? v[2] : v[3];
             const uint32_t d2 = s == 0 ? v[2] : v[3];
             pf[i] = u32x4{d0, d1, d2, v[3]};
-        } else {
-            uint32_t d[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int b = 0; b < 16; b++)
-                if (off + b < tb) d[b >> 2] |= (uint32_t)src[off + b] << (8 * (b & 3));
-            pf[i] = u32x4{d[0], d[1], d[2], d[3]};
         }
     }
+}
+
+// Byte offset of global tile gt's first byte in the staging area that
+// prefetch_tile<false> fills (its address mod 4); 0 for DW.
+template <bool DW>
+__device__ __forceinline__ uint32_t tile_shift(const TileBatch &B, uint32_t ti, uint32_t t) {
+    if constexpr (DW) return 0u;
+    return (uint32_t)(((uintptr_t)B.tiles[ti] + (size_t)t * B.tb[ti]) & 3u);
 }
 
 // One tile from its bytes in LDS (`pay`): steps 1-8 of the data flow above,
@@ -538,7 +560,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
         prefetch_tile<DW, NP>(B, has_next ? gt + stride : gt, lane, pf);
         wave_sync();
 
-        tile_body<DT, false>(B, ti, t, pay, V, wbase, mtab, lane, one, n4, [&]() {
+        tile_body<DT, false>(B, ti, t, pay + tile_shift<DW>(B, ti, t), V, wbase, mtab, lane, one, n4, [&]() {
             // stage the next tile's bytes (the current ones are no longer needed)
 #pragma unroll
             for (int i = 0; i < NP; i++)
@@ -1026,7 +1048,9 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         B.vo_bytes = ((vbytes > obytes ? vbytes : obytes) + 15u) & ~15u;
         uint32_t max_tb = 0;
         for (uint32_t j = 0; j < B.n; j++) max_tb = B.tb[j] > max_tb ? B.tb[j] : max_tb;
-        const int np = max_tb <= 2048u ? 2 : 3;  // KiB of tile bytes prefetched per wave
+        // KiB of tile bytes prefetched per wave: the tile, up to 3 bytes of
+        // alignment before it and the V build's 2-byte reads past its end
+        const int np = max_tb + 8u <= 2048u ? 2 : 3;
         B.wave_lds = B.vo_bytes + 16u * 64u * (uint32_t)np;
         const uint32_t lds = kSharedBytes + B.wave_lds * kWaves;
         // workgroups per CU: what the registers allow, then the LDS
