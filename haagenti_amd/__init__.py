@@ -110,6 +110,8 @@ _sig("hh_hctt_decode_lz4_batch_noalloc", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _v
 NOALLOC_SCRATCH_BYTES = 64 << 20
 _sig("hh_hctt_decode_lz4_fused", _i32, [_vp, _vp, _sz, _vp, _vp, _u32, _vp, C.POINTER(HcttTensor), _u32, _u32,
                                         _i32, _vp])
+_sig("hh_hctt_decode_lz4_fused_tpb", _i32, [_vp, _vp, _sz, _vp, _vp, _u32, _vp, C.POINTER(HcttTensor), _u32,
+                                            C.POINTER(_u32), _i32, _vp])
 FUSED_BLOCK_BYTES = 16352
 
 
@@ -214,7 +216,7 @@ EXPORTS = [
     "hh_lz4_max_compressed_size", "hh_dequant_int4", "hh_quantize_int4",
     "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
     "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_decode_lz4_batch", "hh_hctt_decode_lz4_batch_noalloc",
-    "hh_hctt_decode_lz4_fused",
+    "hh_hctt_decode_lz4_fused", "hh_hctt_decode_lz4_fused_tpb",
     "hh_hctt_encode",
     "hh_hct_read_header", "hh_hct_decompress_all",
     "hh_xxh3_64", "hh_xxh3_64_batch", "hh_hct_read_header_v2", "hh_hct_decompress_all_validated",
@@ -408,12 +410,18 @@ class HipContext:
         """LZ4 blocks of whole tiles and their tiles in one launch, the tile
         bytes kept in LDS (hh_hctt_decode_lz4_fused); tensors are (rows,
         cols, k, d_out[, d_status]), tensor i's blocks the next
-        ceil(tiles_i / tiles_per_block) of the block tables.  Returns the
-        status code."""
+        ceil(tiles_i / tiles_per_block) of the block tables; tiles_per_block
+        is one count for every tensor or a sequence of one per tensor
+        (hh_hctt_decode_lz4_fused_tpb).  Returns the status code."""
         arr = (HcttTensor * max(len(tensors), 1))()
         for i, t in enumerate(tensors):
             st = t[4] if len(t) > 4 else None
             arr[i] = HcttTensor(None, 0, int(t[0]), int(t[1]), int(t[2]), _addr(t[3]), _addr(st))
+        if isinstance(tiles_per_block, (list, tuple)):
+            tpb = (_u32 * max(len(tiles_per_block), 1))(*[int(x) for x in tiles_per_block])
+            return _lib.hh_hctt_decode_lz4_fused_tpb(
+                self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), int(nblocks),
+                _addr(d_status), arr, len(tensors), tpb, int(dtype), stream)
         return _lib.hh_hctt_decode_lz4_fused(
             self._p, _addr(d_in), int(in_total), _addr(d_in_off), _addr(d_in_len), int(nblocks), _addr(d_status),
             arr, len(tensors), int(tiles_per_block), int(dtype), stream)

@@ -314,21 +314,23 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
     return hh_hctt_decode_batch(ctx, tensors, ntensors, out_dtype, stream);
 }
 
-int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
-                                 const uint32_t *d_in_len, uint32_t nblocks, hh_block_status *d_status,
-                                 const hh_hctt_tensor *tensors, uint32_t ntensors, uint32_t tiles_per_block,
-                                 int32_t out_dtype, void *stream) {
-    if (!ctx || (!tensors && ntensors) || tiles_per_block == 0) return HH_ERR_INVALID_ARGUMENT;
+int32_t hh_hctt_decode_lz4_fused_tpb(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                     const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,
+                                     hh_block_status *d_status, const hh_hctt_tensor *tensors, uint32_t ntensors,
+                                     const uint32_t *tiles_per_block, int32_t out_dtype, void *stream) {
+    if (!ctx || (!tensors && ntensors) || (!tiles_per_block && ntensors)) return HH_ERR_INVALID_ARGUMENT;
     if (out_dtype != HH_F32 && out_dtype != HH_F16 && out_dtype != HH_BF16) return HH_ERR_UNSUPPORTED;
     uint64_t need = 0, total = 0;
     for (uint32_t i = 0; i < ntensors; i++) {
         const hh_hctt_tensor &T = tensors[i];
+        const uint32_t tpb = tiles_per_block[i];
+        if (tpb == 0) return HH_ERR_INVALID_ARGUMENT;
         if (T.rows % 64 || T.cols % 64 || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
         const uint64_t nt = (uint64_t)(T.rows / 64) * (T.cols / 64);
         if (nt == 0) continue;
         if (!T.d_out || ((uintptr_t)T.d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
-        if ((uint64_t)tiles_per_block * hh_hctt_tile_bytes(T.k) > hh::fused_block_max()) return HH_ERR_UNSUPPORTED;
-        need += (nt + tiles_per_block - 1) / tiles_per_block;
+        if ((uint64_t)tpb * hh_hctt_tile_bytes(T.k) > hh::fused_block_max()) return HH_ERR_UNSUPPORTED;
+        need += (nt + tpb - 1) / tpb;
         total += nt;
     }
     if (need != nblocks) return HH_ERR_INVALID_ARGUMENT;
@@ -337,9 +339,19 @@ int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in
     if (!d_in || !d_in_off || !d_in_len || !d_status) return HH_ERR_INVALID_ARGUMENT;
     hh::DeviceGuard guard(ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
-    return from_hip(hh::launch_hctt_lz4_fused(tensors, ntensors, tiles_per_block, d_in, in_total, d_in_off, d_in_len,
-                                              d_status, out_dtype, ctx->d_basis, ctx->num_cus,
+    return from_hip(hh::launch_hctt_lz4_fused(tensors, ntensors, tiles_per_block, d_in, in_total, d_in_off,
+                                              d_in_len, d_status, out_dtype, ctx->d_basis, ctx->num_cus,
                                               pick_stream(ctx, stream)));
+}
+
+int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
+                                 const uint32_t *d_in_len, uint32_t nblocks, hh_block_status *d_status,
+                                 const hh_hctt_tensor *tensors, uint32_t ntensors, uint32_t tiles_per_block,
+                                 int32_t out_dtype, void *stream) {
+    if (!ctx || (!tensors && ntensors) || tiles_per_block == 0) return HH_ERR_INVALID_ARGUMENT;
+    std::vector<uint32_t> tpb(ntensors, tiles_per_block);
+    return hh_hctt_decode_lz4_fused_tpb(ctx, d_in, in_total, d_in_off, d_in_len, nblocks, d_status, tensors,
+                                        ntensors, tpb.data(), out_dtype, stream);
 }
 
 int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len, uint32_t rows,

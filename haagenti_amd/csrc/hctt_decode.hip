@@ -575,15 +575,15 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_deco
 // One persistent workgroup per CU (G of them) takes the launch's blocks g,
 // g + G, g + 2 G, ... (its slots 0, 1, 2, ...) and all their tiles (each
 // block holds whole tiles of one tensor: block j of tensor i tiles
-// [j tpb, j tpb + tpb) of it, the last block the rest).  Every wave of the
+// [j tpb_i, j tpb_i + tpb_i) of it, the last block the rest).  Every wave of the
 // workgroup does both kinds of work, claimed from two LDS counters:
 //   next_block  the slots' blocks are decoded in order, each by the wave
 //               that claims it, with the LDS-ring decoder (lz4_ring.hpp, the
 //               whole output kept in LDS: at most kFusedMax bytes) into a
 //               ring of nbuf block buffers (slot q into buffer q mod nbuf);
 //   next_tile   the slots' tiles are decoded in order (tile slot v: tile
-//               v mod tpb of slot v / tpb, skipped past a short block's
-//               tiles), each by the wave that claims it, straight from the
+//               v mod T of slot v / T, T the largest tpb_i, skipped past a
+//               block's tiles), each by the wave that claims it, straight from the
 //               block buffer with tile_body (the whole output tile parked in
 //               LDS, then stored).
 // A wave first claims the next block if its buffer is free (compare and
@@ -647,7 +647,8 @@ struct FusedBlocks {
     hh_block_status *status;
     uint32_t blk_base;                    // global number of this launch's block 0
     uint32_t blk_start[kMaxTensors + 1];  // first block of each tensor, launch-relative
-    uint32_t tpb;                         // tiles per block
+    uint32_t tpb[kMaxTensors];            // tiles per block of each tensor
+    uint32_t tpb_max;
     uint32_t nbuf;                        // block buffers
     uint32_t buf_off;                     // LDS byte offset of the buffers
 };
@@ -741,8 +742,8 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
         ti = 0;
         while (ti + 1 < B.n && lb >= F.blk_start[ti + 1]) ti++;
-        t0 = (lb - F.blk_start[ti]) * F.tpb;
-        nt = min(F.tpb, B.start[ti + 1] - B.start[ti] - t0);
+        t0 = (lb - F.blk_start[ti]) * F.tpb[ti];
+        nt = min(F.tpb[ti], B.start[ti + 1] - B.start[ti] - t0);
     };
     // The workgroup's blocks: launch blocks g, g + G, g + 2 G, ... (G
     // workgroups), its q-th block lb(q) = g + q G, all of whose tiles it
@@ -895,7 +896,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
 
     const float one = Bk.one;
     const int32_t n4 = (int32_t)(int8_t)Bk.neg4;
-    const uint32_t tpb = F.tpb;
+    const uint32_t tpb = Fk.tpb_max;
     bool aborted = false;
     for (;;) {
         // the next block, when its buffer is free
@@ -910,7 +911,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             }
         }
         // else the next tile: slot v / tpb, tile v % tpb of its block (slots
-        // past a short block's tiles are skipped)
+        // past the block's tiles are skipped)
         const int ln = opaque_lane();
         uint32_t v = 0;
         if (ln == 0)
@@ -1100,7 +1101,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
 }
 
 
-hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint32_t tpb, const uint8_t *d_in,
+hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
                                  hipStream_t s) {
@@ -1116,7 +1117,6 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
         F.in_len = d_in_len;
         F.status = d_status;
         F.blk_base = blk;
-        F.tpb = tpb;
         uint32_t max_k = 0, total = 0, nb = 0;
         for (; i < n && B.n < (uint32_t)kMaxTensors; i++) {
             const hh_hctt_tensor &T = tensors[i];
@@ -1131,8 +1131,10 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint
             B.k[j] = T.k;
             B.tb[j] = (uint32_t)hh_hctt_tile_bytes(T.k);
             F.blk_start[j] = nb;
+            F.tpb[j] = tpb[i];
+            F.tpb_max = tpb[i] > F.tpb_max ? tpb[i] : F.tpb_max;
             total += nt;
-            nb += (nt + tpb - 1) / tpb;
+            nb += (nt + tpb[i] - 1) / tpb[i];
             max_k = T.k > max_k ? T.k : max_k;
         }
         if (B.n == 0) continue;

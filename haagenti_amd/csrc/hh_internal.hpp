@@ -246,9 +246,9 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
                               const void *d_basis, int num_cus, hipStream_t s);
 // LZ4 blocks of whole tiles decoded and their tiles decoded from LDS in one
 // launch per 8 tensors (hctt_decode.hip; validated by the caller: tensor i's
-// blocks are the next ceil(ntiles_i / tpb) of d_in_off / d_in_len, each
-// tpb * tile bytes <= fused_block_max()).
-hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, uint32_t tpb, const uint8_t *d_in,
+// blocks are the next ceil(ntiles_i / tpb[i]) of d_in_off / d_in_len, each
+// tpb[i] * tile bytes <= fused_block_max()).
+hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
                                  hipStream_t s);

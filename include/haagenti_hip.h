@@ -235,6 +235,16 @@ int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in
                                  hh_block_status *d_status, const hh_hctt_tensor *tensors, uint32_t ntensors,
                                  uint32_t tiles_per_block, int32_t out_dtype, void *stream);
 
+/* hh_hctt_decode_lz4_fused with tiles_per_block[i] tiles per LZ4 block of
+ * tensor i: each tensor written by its own HctWriter whose block size
+ * (HctWriter::with_block_size, haagenti-hct/src/tensor.rs:544-547; chunks of
+ * it compressed one by one, :556-561) is a whole number of that tensor's
+ * tiles, e.g. floor(16384 / tile bytes) tiles in a layer of mixed k. */
+int32_t hh_hctt_decode_lz4_fused_tpb(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                     const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,
+                                     hh_block_status *d_status, const hh_hctt_tensor *tensors, uint32_t ntensors,
+                                     const uint32_t *tiles_per_block, int32_t out_dtype, void *stream);
+
 /* Size of the tile-byte array hh_hctt_decode_lz4_batch_noalloc uses: 64 MiB
  * (a Llama-3-8B layer's tiles at 30 % retention take 64,110,592 bytes). */
 #define HH_NOALLOC_SCRATCH_BYTES (64ull << 20)

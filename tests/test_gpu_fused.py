@@ -289,3 +289,31 @@ def test_fewer_tiles_than_workgroups():
     fo, st, fs, bo, codes, bs = both_paths(L, Hm.BF16, 2)
     assert (st["code"] == 0).all()
     assert_same(T, Hm.BF16, fo, fs, bo, bs)
+
+
+def test_per_tensor_tiles_per_block():
+    # every tensor cut into blocks of floor(16352 / its tile bytes) whole
+    # tiles (one writer per tensor with a whole-tile block size), retention
+    # 0.18-0.42: the sparse tensor's blocks are a few hundred short LZ4
+    # sequences each (4-byte matches thousands of bytes back); then the same
+    # layer with a truncated block of the sparse tensor
+    Hm = H()
+    T = G.torch()
+    shapes = [("a", 512, 1024), ("b", 256, 1536), ("c", 1024, 512), ("d", 384, 640)]
+    ks = [Hm.hctt_retain_count(r) for r in (0.18, 0.42, 0.25, 0.33)]
+    tpb = [Hm.FUSED_BLOCK_BYTES // Hm.hctt_tile_bytes(k) for k in ks]
+    assert len(set(tpb)) == 4
+    L = LU.encode_layer(Hm, shapes, ks, seed=71, block_bytes=Hm.FUSED_BLOCK_BYTES)
+    fo, st, fs, bo, codes, bs = both_paths(L, Hm.F32, tpb)
+    assert (st["code"] == 0).all() and (codes == 0).all()
+    assert all((s.cpu().numpy() == 0).all() for s in fs)
+    assert_same(T, Hm.F32, fo, fs, bo, bs)
+    check_against_oracle(L, fo)
+    bad = 3
+    lens = L["in_len"].copy()
+    lens[bad] //= 2
+    fo, st, fs, bo, codes, bs = both_paths(L, Hm.BF16, tpb, lens=lens)
+    assert st["code"][bad] != 0 and codes[bad] == st["code"][bad]
+    assert (np.delete(st["code"], bad) == 0).all()
+    assert_same(T, Hm.BF16, fo, fs, bo, bs)
+    assert (fs[0].cpu().numpy()[bad * tpb[0]:(bad + 1) * tpb[0]] == Hm.CORRUPTED_DATA).all()

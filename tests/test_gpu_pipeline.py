@@ -217,3 +217,51 @@ def test_pipeline_pageable_and_in_place_staging_and_errors():
     assert ei.value.block == bad
     pipe.finish()                                            # nothing pending any more
     pipe.close()
+
+
+def test_pipeline_blocks_across_tile_boundaries():
+    # each tensor written with HctWriter's default block size (16 KiB chunks
+    # of its tile bytes, tiles cut between blocks: tensor.rs:556-561): the
+    # LZ4 output lands in the scratch at block offsets inside tiles
+    Hm, Pm = H(), P()
+    T = G.torch()
+    shapes = [("a", 256, 512), ("b", 512, 256)]
+    ks = [Hm.hctt_retain_count(0.3), Hm.hctt_retain_count(0.22)]
+    rng = np.random.default_rng(91)
+    comp = Hm.Lz4Compressor()
+    parts, in_off, in_len, out_off, out_cap, tens = [], [], [], [], [], []
+    pos = spos = 0
+    for (name, r, c), k in zip(shapes, ks):
+        tiles = Hm.hctt_encode((rng.standard_normal((r, c), dtype=np.float32) * np.float32(0.02)), k)
+        assert tiles.size % 16384 != 0 and 16384 % Hm.hctt_tile_bytes(k) != 0
+        for s in range(0, tiles.size, 16384):
+            chunk = tiles[s:s + 16384]
+            cb = comp.compress(chunk.tobytes())
+            parts.append(cb)
+            in_off.append(pos)
+            in_len.append(len(cb))
+            out_off.append(spos + s)
+            out_cap.append(chunk.size)
+            pos += len(cb)
+        tens.append(dict(name=name, rows=r, cols=c, k=k, tiles=tiles))
+        spos += tiles.size
+    blob = np.frombuffer(b"".join(parts), np.uint8)
+    cfg = Pm.default_config()
+    cfg.staging_buffer_size = 1 << 20
+    cfg.tile_scratch_size = 1 << 20
+    cfg.max_blocks = 64
+    pipe = Pm.DecompressionPipeline(G.ctx(), None, cfg)
+    outs = [T.empty(t["rows"] * t["cols"], dtype=T.float32, device="cuda") for t in tens]
+    tst = [T.full(((t["rows"] // 64) * (t["cols"] // 64),), -1, dtype=T.int32, device="cuda") for t in tens]
+    desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o, s) for t, o, s in zip(tens, outs, tst)]
+    tk = pipe.submit(blob.copy(), np.array(in_off, np.uint64), np.array(in_len, np.uint32),
+                     np.array(out_off, np.uint64), np.array(out_cap, np.uint32), tensors=desc, dtype=Hm.F32)
+    pipe.wait(tk)
+    for t, o, s in zip(tens, outs, tst):
+        assert (s.cpu().numpy() == 0).all()
+        rc, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+        assert rc == O.OK
+        got = o.cpu().numpy().reshape(t["rows"], t["cols"])
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.abs(got - ref).max() <= TOL * rms
+    pipe.close()
