@@ -185,6 +185,26 @@ uint16_t f32_to_f16_rne(float f) {
     return (uint16_t)(sign | r);
 }
 
+// Whether hct3_decode_eo takes a decode (its conditions, checked here so
+// that the dense path's scratch is not sized for nothing).
+bool eo_candidate(const std::vector<Layer> &layers, uint32_t rows, uint32_t cols, int32_t dtype,
+                  const void *d_out) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(d_out);
+    return !layers.empty() && layers.size() <= 16 && rows % 512 == 0 && cols % 512 == 0 &&
+           (a & (dtype == HH_F32 ? 15u : 7u)) == 0;
+}
+
+// hct3_decode_eo over the layers of a container whose bytes are at h_base
+// on the host and d_base on the device.
+int32_t decode_eo(hh_context *ctx, const std::vector<Layer> &layers, const uint8_t *h_base, const uint8_t *d_base,
+                  uint32_t rows, uint32_t cols, int32_t dtype, void *d_out, uint8_t *d_stage, hipStream_t s) {
+    std::vector<hh::Hct3Frag> fr;
+    for (const Layer &L : layers)
+        fr.push_back(hh::Hct3Frag{d_base + (L.bitmap - h_base),
+                                  d_base + (reinterpret_cast<const uint8_t *>(L.coef) - h_base), L.ncoef});
+    return hh::hct3_decode_eo(ctx, fr.data(), (uint32_t)fr.size(), rows, cols, dtype, d_out, d_stage, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -226,13 +246,26 @@ int32_t hh_hct3_decompress(hh_context *ctx, const uint8_t *data, size_t len, con
     for (const Layer &L : layers) mc = std::max(mc, L.ncoef);
     hh::DeviceGuard guard(ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (eo_candidate(layers, rows, cols, out_dtype, d_out)) {
+        // the container copied whole to the device, then decoded in place
+        const size_t st = stage_bytes(total, 0, 0);
+        rc = ensure_scratch(ctx, st + align16(len));
+        if (rc != HH_OK) return rc;
+        uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
+        uint8_t *d_data = base + st;
+        hipError_t e = hipMemcpyAsync(d_data, data, len, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return from_hip(e);
+        rc = decode_eo(ctx, layers, data, d_data, rows, cols, out_dtype, d_out, base, s);
+        if (rc != HH_OK) return rc;
+        return from_hip(hipStreamSynchronize(s));
+    }
     const size_t mat = align16((size_t)total * sizeof(float));
     rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, mc, 0));
     if (rc != HH_OK) return rc;
     uint8_t *base = reinterpret_cast<uint8_t *>(ctx->d_scratch);
     float *d_dense = reinterpret_cast<float *>(base);
     float *d_tmp = reinterpret_cast<float *>(base + mat);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     rc = scatter_layers(layers, total, 0, d_dense, base + 2 * mat, s);
     if (rc == HH_OK) rc = inverse_to(ctx, d_dense, d_tmp, rows, cols, out_dtype, d_out, s, true);
     if (rc != HH_OK) return rc;
@@ -257,6 +290,12 @@ int32_t hh_hct3_decompress_device(hh_context *ctx, const uint8_t *h_data, const 
     if (!d_out) return HH_ERR_INVALID_ARGUMENT;
     hh::DeviceGuard guard(ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
+    if (eo_candidate(layers, rows, cols, out_dtype, d_out)) {
+        rc = ensure_scratch(ctx, stage_bytes(total, 0, 0));
+        if (rc != HH_OK) return rc;
+        return decode_eo(ctx, layers, h_data, d_data, rows, cols, out_dtype, d_out,
+                         reinterpret_cast<uint8_t *>(ctx->d_scratch), reinterpret_cast<hipStream_t>(stream));
+    }
     const size_t mat = align16((size_t)total * sizeof(float));
     rc = ensure_scratch(ctx, 2 * mat + stage_bytes(total, 0, 0));
     if (rc != HH_OK) return rc;

@@ -157,6 +157,127 @@ __global__ __launch_bounds__(256) void hct3_scatter_kernel(const uint64_t *__res
     }
 }
 
+// hct3_scatter_kernel's output written as the first product's operand
+// plane of the even / odd split inverse DCT (dct2d_eo): element (r, c) of
+// the h x w matrix, times scale[0] (a power of two), as f16 at r w + c / 2
+// for even c and r w + w / 2 + c / 2 for odd c.  The values are f16, so the
+// plane holds them exactly (barring f16 range limits at the scale chosen).
+__global__ __launch_bounds__(256) void hct3_scatter_plane_kernel(const uint64_t *__restrict__ bits,
+                                                                 uint64_t nbits,
+                                                                 const uint32_t *__restrict__ block_pref,
+                                                                 const uint8_t *__restrict__ coef, uint32_t ncoef,
+                                                                 uint32_t w, const float *__restrict__ scale,
+                                                                 _Float16 *__restrict__ plane, int first) {
+    __shared__ uint64_t W[kWordsPerBlock];
+    __shared__ uint32_t P[kWordsPerBlock];
+    __shared__ uint32_t s[4];
+    const uint64_t w0 = (uint64_t)blockIdx.x * kWordsPerBlock;
+    const uint64_t wd = w0 + threadIdx.x;
+    const uint64_t m = word_mask(wd, nbits);
+    const uint64_t b = m ? bits[wd] & m : 0ull;
+    uint32_t total;
+    const uint32_t excl = block_excl_sum((uint32_t)__popcll(b), s, &total);
+    W[threadIdx.x] = b;
+    P[threadIdx.x] = block_pref[blockIdx.x] + excl;
+    __syncthreads();
+    const float sc = *scale;
+    const uint32_t half = w / 2;
+    const uint64_t e0 = w0 * 64 + threadIdx.x;
+    // this thread's first element as (row, column); each step advances 256
+    // columns (w >= 512: at most one row wrap per step)
+    uint64_t r = e0 / w;
+    uint32_t c = (uint32_t)(e0 - r * w);
+    if (((uintptr_t)coef & 1u) == 0 && ncoef > 0) {
+        // 2-byte aligned values: eight elements' values loaded together
+        // (an element without a value loads value 0 and discards it)
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(coef);
+        for (uint32_t j0 = 0; j0 < 64; j0 += 8) {
+            uint32_t x[8];
+            bool hv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t el = threadIdx.x + kWordsPerBlock * (j0 + k);
+                const uint64_t bw = W[el >> 6];
+                const uint32_t bit = el & 63u;
+                const uint32_t rk = P[el >> 6] + (uint32_t)__popcll(bw & ((1ull << bit) - 1ull));
+                hv[k] = ((bw >> bit) & 1ull) && rk < ncoef;  // bits past nbits are clear
+                x[k] = h[hv[k] ? rk : 0u];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint64_t e = w0 * 64 + threadIdx.x + kWordsPerBlock * (j0 + k);
+                if (e < nbits && (first || hv[k])) {
+                    const _Float16 v = hv[k] ? (_Float16)(f16_bits_to_f32(x[k]) * sc) : (_Float16)0.0f;
+                    plane[r * w + ((c & 1u) ? half + (c >> 1) : (c >> 1))] = v;
+                }
+                c += kWordsPerBlock;
+                if (c >= w) {
+                    c -= w;
+                    r++;
+                }
+            }
+        }
+        return;
+    }
+    for (uint32_t j = 0; j < 64; j++) {
+        const uint32_t el = threadIdx.x + kWordsPerBlock * j;
+        const uint64_t e = w0 * 64 + el;
+        if (e >= nbits) break;
+        const uint64_t bw = W[el >> 6];
+        const uint32_t bit = el & 63u;
+        bool have = false;
+        _Float16 v = (_Float16)0.0f;
+        if ((bw >> bit) & 1ull) {
+            const uint32_t rk = P[el >> 6] + (uint32_t)__popcll(bw & ((1ull << bit) - 1ull));
+            if (rk < ncoef) {
+                const uint8_t *q = coef + 2ull * rk;
+                v = (_Float16)(f16_bits_to_f32((uint32_t)q[0] | ((uint32_t)q[1] << 8)) * sc);
+                have = true;
+            }
+        }
+        const uint64_t o = r * w + ((c & 1u) ? half + (c >> 1) : (c >> 1));
+        if (first || have) plane[o] = v;
+        c += kWordsPerBlock;
+        if (c >= w) {
+            c -= w;
+            r++;
+        }
+    }
+}
+
+// Per-block max |v| of n f16 values at any byte address (a grid-stride
+// range per block) into partial[blockIdx.x]; 16-bit loads when the values
+// are 2-byte aligned, bytes otherwise.
+__global__ __launch_bounds__(256) void amax_f16_kernel(const uint8_t *__restrict__ v, uint32_t n,
+                                                       float *__restrict__ partial) {
+    __shared__ float sm[256];
+    float mx = 0.0f;
+    if (((uintptr_t)v & 1u) == 0) {
+        // eight independent loads in flight per thread
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(v);
+        const uint32_t st = gridDim.x * 256;
+        uint32_t i = blockIdx.x * 256 + threadIdx.x;
+        for (; (uint64_t)i + 7ull * st < n; i += 8 * st) {
+            uint32_t x[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) x[k] = h[i + k * st];
+#pragma unroll
+            for (int k = 0; k < 8; k++) mx = fmaxf(mx, fabsf(f16_bits_to_f32(x[k])));
+        }
+        for (; i < n; i += st) mx = fmaxf(mx, fabsf(f16_bits_to_f32(h[i])));
+    } else {
+        for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+            mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)v[2ull * i] | ((uint32_t)v[2ull * i + 1] << 8))));
+    }
+    sm[threadIdx.x] = mx;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) sm[threadIdx.x] = fmaxf(sm[threadIdx.x], sm[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = sm[0];
+}
+
 // 64-bit words of a bitmap held at any byte address (nbytes bytes; the last
 // word is zero-padded).
 __global__ __launch_bounds__(256) void pack_bits_kernel(const uint8_t *__restrict__ src, uint64_t nbytes,
@@ -328,47 +449,54 @@ static int32_t split_scratch(hh_context *ctx, size_t need, hipStream_t s) {
 // planes with their columns in even / odd order), then a butterfly pass.
 //   P  = butterfly(split(B_w)^T (C 2^e)^T)     (w x h, as even / odd planes)
 //   X  = 2^-e butterfly(split(B_h)^T P^T)      (h x w)
-static int32_t dct2d_eo(hh_context *ctx, const float *d_in, float *d_out, uint32_t h, uint32_t w, hipStream_t s,
-                        bool f16_exact, int32_t cvt_dtype, void *cvt_out, bool *converted) {
-    const uint16_t *wh, *wl, *hh_, *hl;
-    int32_t rc = planes_for(ctx, w, 2, s, &wh, &wl);
+// dct2d_eo's scratch: block maxima, the constants {0, 1, 2^e, 2^-e}, the
+// input's planes, the stacked E / O products (f32), the intermediate's
+// planes; and the basis planes.
+struct EoScratch {
+    float *partial, *consts;
+    uint16_t *in_hi, *in_lo, *mid_hi, *mid_lo;
+    float *y;
+    const uint16_t *wh, *wl, *hh, *hl;
+};
+constexpr uint32_t kEoPartials = 4096;  // block maxima: 256 per fragment in hct3_decode_eo
+
+static int32_t eo_scratch(hh_context *ctx, uint32_t h, uint32_t w, bool f16_exact, hipStream_t s, EoScratch &S) {
+    int32_t rc = planes_for(ctx, w, 2, s, &S.wh, &S.wl);
     if (rc != HH_OK) return rc;
-    rc = planes_for(ctx, h, 2, s, &hh_, &hl);
+    rc = planes_for(ctx, h, 2, s, &S.hh, &S.hl);
     if (rc != HH_OK) return rc;
-    if (h == w) {
-        wh = hh_;
-        wl = hl;
+    if (h == w) {  // the second lookup may have replaced the first's slot
+        S.wh = S.hh;
+        S.wl = S.hl;
     }
-    const uint32_t np = 1024;
     const uint64_t total = (uint64_t)h * w;
-    // scratch: maxima and constants, the input's planes, the stacked E / O
-    // products (f32), the intermediate's planes
-    const size_t off_in = ((np + 4) * sizeof(float) + 255) & ~(size_t)255;
+    const size_t off_in = ((kEoPartials + 4) * sizeof(float) + 255) & ~(size_t)255;
     const size_t off_y = off_in + ((total * (f16_exact ? 2 : 4) + 255) & ~(uint64_t)255);
     const size_t off_mid = off_y + total * 4;
     rc = split_scratch(ctx, off_mid + total * 4, s);
     if (rc != HH_OK) return rc;
     uint8_t *sp = reinterpret_cast<uint8_t *>(ctx->d_split);
-    float *partial = reinterpret_cast<float *>(sp);
-    float *consts = partial + np;
-    uint16_t *in_hi = reinterpret_cast<uint16_t *>(sp + off_in);
-    uint16_t *in_lo = f16_exact ? nullptr : in_hi + total;
-    float *y = reinterpret_cast<float *>(sp + off_y);
-    uint16_t *mid_hi = reinterpret_cast<uint16_t *>(sp + off_mid);
-    uint16_t *mid_lo = mid_hi + total;
-    hipLaunchKernelGGL(amax_kernel, dim3(np), dim3(256), 0, s, d_in, total, partial);
-    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, partial, np, w, consts);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return from_hip(e);
-    e = launch_operand_planes_eo(d_in, h, w, w, consts + 2, in_hi, in_lo, s);
-    if (e != hipSuccess) return from_hip(e);
+    S.partial = reinterpret_cast<float *>(sp);
+    S.consts = S.partial + kEoPartials;
+    S.in_hi = reinterpret_cast<uint16_t *>(sp + off_in);
+    S.in_lo = f16_exact ? nullptr : S.in_hi + total;
+    S.y = reinterpret_cast<float *>(sp + off_y);
+    S.mid_hi = reinterpret_cast<uint16_t *>(sp + off_mid);
+    S.mid_lo = S.mid_hi + total;
+    return HH_OK;
+}
+
+// The two half-depth products and butterflies of dct2d_eo, from the input's
+// planes (C 2^e in even / odd column order) and the constants in S.
+static int32_t eo_products(const EoScratch &S, float *d_out, uint32_t h, uint32_t w, hipStream_t s,
+                           int32_t cvt_dtype, void *cvt_out, bool *converted) {
     DctGemm g1;
-    g1.a_hi = wh;
-    g1.a_lo = wl;
-    g1.b_hi = in_hi;
-    g1.b_lo = in_lo;
+    g1.a_hi = S.wh;
+    g1.a_lo = S.wl;
+    g1.b_hi = S.in_hi;
+    g1.b_lo = S.in_lo;
     g1.out_scale = nullptr;
-    g1.d = y;
+    g1.d = S.y;
     g1.ldd = h;
     g1.d_dtype = HH_F32;
     g1.d_planes = false;
@@ -379,16 +507,16 @@ static int32_t dct2d_eo(hh_context *ctx, const float *d_in, float *d_out, uint32
     g1.ldb = w;
     g1.m_split = w / 2;
     g1.b_koff = w / 2;
-    e = launch_dct_gemm(g1, s);
-    if (e == hipSuccess) e = launch_dct_butterfly(y, w / 2, h, true, nullptr, HH_F32, mid_hi, 0, s);
+    hipError_t e = launch_dct_gemm(g1, s);
+    if (e == hipSuccess) e = launch_dct_butterfly(S.y, w / 2, h, true, nullptr, HH_F32, S.mid_hi, 0, s);
     if (e != hipSuccess) return from_hip(e);
     DctGemm g2;
-    g2.a_hi = hh_;
-    g2.a_lo = hl;
-    g2.b_hi = mid_hi;
-    g2.b_lo = mid_lo;
+    g2.a_hi = S.hh;
+    g2.a_lo = S.hl;
+    g2.b_hi = S.mid_hi;
+    g2.b_lo = S.mid_lo;
     g2.out_scale = nullptr;
-    g2.d = y;
+    g2.d = S.y;
     g2.ldd = w;
     g2.d_dtype = HH_F32;
     g2.d_planes = false;
@@ -402,11 +530,63 @@ static int32_t dct2d_eo(hh_context *ctx, const float *d_in, float *d_out, uint32
     e = launch_dct_gemm(g2, s);
     const bool cvt = cvt_out != nullptr;
     if (e == hipSuccess)
-        e = launch_dct_butterfly(y, h / 2, w, false, consts + 3, cvt ? cvt_dtype : HH_F32, cvt ? cvt_out : d_out,
-                                 w, s);
+        e = launch_dct_butterfly(S.y, h / 2, w, false, S.consts + 3, cvt ? cvt_dtype : HH_F32,
+                                 cvt ? cvt_out : d_out, w, s);
     if (e != hipSuccess) return from_hip(e);
     if (converted) *converted = cvt;
     return HH_OK;
+}
+
+static int32_t dct2d_eo(hh_context *ctx, const float *d_in, float *d_out, uint32_t h, uint32_t w, hipStream_t s,
+                        bool f16_exact, int32_t cvt_dtype, void *cvt_out, bool *converted) {
+    EoScratch S;
+    int32_t rc = eo_scratch(ctx, h, w, f16_exact, s, S);
+    if (rc != HH_OK) return rc;
+    const uint64_t total = (uint64_t)h * w;
+    hipLaunchKernelGGL(amax_kernel, dim3(kEoPartials), dim3(256), 0, s, d_in, total, S.partial);
+    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, S.partial, kEoPartials, w, S.consts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e);
+    e = launch_operand_planes_eo(d_in, h, w, w, S.consts + 2, S.in_hi, S.in_lo, s);
+    if (e != hipSuccess) return from_hip(e);
+    return eo_products(S, d_out, h, w, s, cvt_dtype, cvt_out, converted);
+}
+
+int32_t hct3_decode_eo(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, uint32_t h, uint32_t w,
+                       int32_t dtype, void *d_out, uint8_t *d_stage, hipStream_t s) {
+    const uintptr_t out_addr = (uintptr_t)d_out;
+    if (h % 512u || w % 512u || nfrags == 0 || nfrags > kEoPartials / 256u ||
+        (out_addr & (dtype == HH_F32 ? 15u : 7u)))
+        return HH_ERR_UNSUPPORTED;
+    EoScratch S;
+    int32_t rc = eo_scratch(ctx, h, w, true, s, S);
+    if (rc != HH_OK) return rc;
+    // the scale from the largest coefficient of any fragment (at least the
+    // largest of the matrix the fragments make)
+    for (uint32_t i = 0; i < nfrags; i++)
+        hipLaunchKernelGGL(amax_f16_kernel, dim3(256), dim3(256), 0, s, frags[i].coef, frags[i].ncoef,
+                           S.partial + 256u * i);
+    hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, S.partial, 256u * nfrags, w, S.consts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e);
+    const uint64_t total = (uint64_t)h * w;
+    const uint32_t nwords = blocks_for(total, 64);
+    const uint32_t nblk = blocks_for(nwords, kWordsPerBlock);
+    uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
+    uint64_t *d_bits = reinterpret_cast<uint64_t *>(d_stage + ((hct3_block_sums_bytes(total) + 15u) & ~(size_t)15));
+    for (uint32_t i = 0; i < nfrags; i++) {
+        e = launch_pack_bits(frags[i].bitmap, (total + 7) / 8, d_bits, s);
+        if (e != hipSuccess) return from_hip(e);
+        hipLaunchKernelGGL(hct3_count_kernel, dim3(nblk), dim3(256), 0, s, d_bits, total, d_sums);
+        hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(1024), 0, s, d_sums, nblk);
+        hipLaunchKernelGGL(hct3_scatter_plane_kernel, dim3(nblk), dim3(256), 0, s, d_bits, total, d_sums,
+                           frags[i].coef, frags[i].ncoef, w, S.consts + 2,
+                           reinterpret_cast<_Float16 *>(S.in_hi), i == 0 ? 1 : 0);
+        e = hipGetLastError();
+        if (e != hipSuccess) return from_hip(e);
+    }
+    return eo_products(S, reinterpret_cast<float *>(d_out), h, w, s, dtype == HH_F32 ? HH_F32 : dtype,
+                       dtype == HH_F32 ? nullptr : d_out, nullptr);
 }
 
 int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tmp, float *d_out,

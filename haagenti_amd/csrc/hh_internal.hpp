@@ -181,6 +181,22 @@ size_t hct3_block_sums_bytes(uint64_t nbits);
 // Bitmap bytes at any device address -> zero-padded 64-bit words.
 hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_words, hipStream_t s);
 hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_out, hipStream_t s);
+// One HCT3 fragment in device memory: its bitmap bytes and its f16
+// coefficient values (both at any byte address).
+struct Hct3Frag {
+    const uint8_t *bitmap;
+    const uint8_t *coef;
+    uint32_t ncoef;
+};
+// The h x w HCT3 decode straight to d_out (dtype): the fragments' values,
+// scaled by a power of two from the largest of them, scattered in order
+// into the operand plane of the even / odd split inverse DCT, then its two
+// products.  d_stage holds hct3_block_sums_bytes(h w) rounded up to 16 plus
+// the bitmap words.  HH_ERR_UNSUPPORTED (nothing enqueued) unless h and w
+// are multiples of 512, d_out is aligned (16 bytes f32, 8 bytes 16-bit) and
+// there are 1..16 fragments.
+int32_t hct3_decode_eo(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, uint32_t h, uint32_t w,
+                       int32_t dtype, void *d_out, uint8_t *d_stage, hipStream_t s);
 // One split-f16 MFMA product D = s_out * A Bt^T (dct_gemm.hip).  A (M x K)
 // and Bt (N x K) are f16 hi / lo planes, row-major with k contiguous,
 // dct_planes_rows(rows) x dct_planes_cols(K) with zeros past the matrix;

@@ -192,6 +192,68 @@ def test_decompress_even_odd_split_vs_oracle_and_16bit():
     assert np.array_equal(h16, G.f16_bits(got))
 
 
+def _direct_vs_dense(data, shape):
+    # the direct plane scatter (host-staged and device-resident entries)
+    # against the oracle and against the dense route (hh_hct3_coefficients,
+    # then hh_idct_2d); returns the f32 output and the two differences
+    T = G.torch()
+    total = shape[0] * shape[1]
+    rc, ref = O.hct3_decode(data, shape)
+    assert rc == O.OK
+    got = dec().decompress_to_gpu(data, shape, stream=G.stream()).cpu().numpy()
+    out = T.empty(total, dtype=T.float32, device="cuda")
+    dec().decompress_device(data, G.dev(np.frombuffer(data, np.uint8)), shape, out, stream=G.stream())
+    G.sync()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), got.view(np.uint32))
+    coef = dec().reconstruct_coefficients_gpu(data, total, stream=G.stream())
+    x = T.empty(total, dtype=T.float32, device="cuda")
+    G.ctx().idct_2d(coef, shape[0], shape[1], x, stream=G.stream())
+    G.sync()
+    e_ref, e_dense = rel_err(got, ref), rel_err(got, x.cpu().numpy())
+    print(f"shape {shape}: max|gpu - oracle| = {e_ref:.2e}, max|direct - dense| = {e_dense:.2e} x RMS")
+    return got, e_ref, e_dense
+
+
+def test_decompress_direct_plane_scatter_matches_dense_route():
+    # sides that are multiples of 512: the fragments' values are scattered
+    # straight into the split transform's operand plane, scaled by a power of
+    # two from the largest value of any fragment; with the largest value in
+    # the final matrix that is the dense route's scale
+    Hm = H()
+    T = G.torch()
+    rng = np.random.default_rng(2048)
+    shape = (512, 1024)
+    total = 512 * 1024
+    bm2, v2, _ = random_fragment(rng, total, 0.02)
+    data = container([random_fragment(rng, total, 0.2), random_fragment(rng, total, 0.05),
+                      (bm2, v2[: v2.size // 2], None)])    # the third runs out of values
+    got, e_ref, e_dense = _direct_vs_dense(data, shape)
+    assert e_ref <= 1e-5 and e_dense <= 1e-6
+    b16 = dec().decompress_to_gpu(data, shape, dtype=Hm.BF16).view(T.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(b16, G.bf16_bits(got))
+
+
+def test_decompress_direct_plane_scatter_overwritten_maximum():
+    # the second fragment overwrites part of the first, including its largest
+    # value (400, against values of ~0.05): the scale comes from a value the
+    # final matrix no longer holds (2^11 smaller than the dense route's), and
+    # the error stays at the 1e-6 level
+    rng = np.random.default_rng(4096)
+    shape = (1024, 512)
+    total = 1024 * 512
+    bm0, v0, _ = random_fragment(rng, total, 0.2)
+    bits0 = np.unpackbits(np.frombuffer(bm0, np.uint8), bitorder="little")[:total].astype(bool)
+    v0 = v0.copy()
+    v0[0] = np.float16(400.0)
+    bits1 = rng.random(total) < 0.05
+    bits1[int(np.flatnonzero(bits0)[0])] = True
+    v1 = rng.normal(0, 0.05, int(bits1.sum())).astype(np.float16)
+    bm1 = np.packbits(bits1.astype(np.uint8), bitorder="little").tobytes()
+    data = container([(bm0, v0, None), (bm1, v1, None)])
+    _, e_ref, e_dense = _direct_vs_dense(data, shape)
+    assert e_ref <= 1e-5 and e_dense <= 1e-5
+
+
 def test_idct_single_coefficient_closed_form():
     # C = e_k e_l^T  ->  X[i][j] = B_h[k][i] B_w[l][j]
     T = G.torch()
