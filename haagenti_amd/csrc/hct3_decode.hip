@@ -33,7 +33,6 @@ namespace hh {
 namespace {
 
 constexpr int kWordsPerBlock = 256;
-constexpr uint64_t kElemsPerBlock = 64ull * kWordsPerBlock;
 
 __device__ __forceinline__ uint64_t word_mask(uint64_t w, uint64_t nbits) {
     const uint64_t lo = 64ull * w;

@@ -159,11 +159,10 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
 constexpr int kMaxTensors = 8;
-constexpr int kMaxPrefetch = 3;  // 16-byte loads per lane: tiles up to 3 KiB (k <= 4096)
 // Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs with
 // at most 2 KiB of tile bytes prefetched (168 registers, no spills; the LDS
 // also fits 3 workgroups per CU), else 2.
-constexpr int kWavesPerSimd(int dt, bool dw, int np) { return dt != HH_F32 && np == 2 ? 3 : 2; }
+constexpr int kWavesPerSimd(int dt, int np) { return dt != HH_F32 && np == 2 ? 3 : 2; }
 struct TileBatch {
     const uint8_t *tiles[kMaxTensors];
     void *out[kMaxTensors];
@@ -513,13 +512,11 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
 }
 
 template <int DT, bool DW, int NP>
-__global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, DW, NP)) void hctt_decode_kernel(TileBatch Bk,
+__global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_kernel(TileBatch Bk,
                                                                    const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int h = lane >> 5;
-    const int l32 = lane & 31;
     u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
     for (int i = threadIdx.x; i < (int)(sizeof(TileBatch) / 4); i += kThreads)
         reinterpret_cast<uint32_t *>(smem + kBatchOff)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
@@ -1055,7 +1052,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         B.wave_lds = B.vo_bytes + 16u * 64u * (uint32_t)np;
         const uint32_t lds = kSharedBytes + B.wave_lds * kWaves;
         // workgroups per CU: what the registers allow, then the LDS
-        uint32_t per_cu = (uint32_t)kWavesPerSimd(dtype, all_dw, np);
+        uint32_t per_cu = (uint32_t)kWavesPerSimd(dtype, np);
         if (per_cu > (160u * 1024u) / lds) per_cu = (160u * 1024u) / lds;
         if (per_cu == 0) per_cu = 1;
         uint32_t grid = (uint32_t)(num_cus > 0 ? num_cus : 256) * per_cu;
