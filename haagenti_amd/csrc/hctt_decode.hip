@@ -43,6 +43,7 @@
 //      by the workgroup;
 //   5. the output block is parked in LDS (reusing V's space) and written as
 //      coalesced 16-byte row segments.
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 
@@ -618,9 +619,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
 // before a claimed tile of slot i or later); a tile's wave waits for its
 // block's bytes, whose decoder waits only on lower slots; every such chain
 // descends to a slot whose buffer is free.  Every wait is bounded all the
-// same (kSpinLimit polls); one that runs out (not expected) raises the
-// workgroup's abort word, every wave then leaves, and the block record of
-// the block waited on reports HH_ERR_DEVICE.
+// same (kSpinLimit polls, or HH_FUSED_SPIN_LIMIT from the environment, which
+// tests set small to run this path); one that runs out raises the
+// workgroup's abort word, every wave then leaves, and every block record of
+// the workgroup reports HH_ERR_DEVICE (written by the last wave to leave).
 //
 // The input stage holds 8 KiB of a block's compressed bytes (a 16 KiB block
 // is staged in two or three batches of loads): it fits a wave's tile area,
@@ -648,11 +650,12 @@ struct FusedBlocks {
     uint32_t tpb_max;
     uint32_t nbuf;                        // block buffers
     uint32_t buf_off;                     // LDS byte offset of the buffers
+    uint32_t spin_limit;                  // polls before a wait gives up
 };
 
 // Workgroup LDS layout after the shared part: [block descriptor][state[8]
-// (8 bytes each), done[8], abort, next_block, next_tile, finished, the
-// complete and failed bitmaps][wave areas][block buffers].
+// (8 bytes each), done[8], abort, next_block, next_tile, finished, left,
+// the complete and failed bitmaps][wave areas][block buffers].
 constexpr uint32_t kFusedFOff = kSharedBytes;
 constexpr uint32_t kFusedFlagsOff = kFusedFOff + ((sizeof(FusedBlocks) + 15u) & ~15u);
 constexpr uint32_t kFusedStateOff = kFusedFlagsOff;
@@ -661,7 +664,8 @@ constexpr uint32_t kFusedAbortOff = kFusedDoneOff + 4 * kFusedMaxBufs;
 constexpr uint32_t kFusedNextBlockOff = kFusedAbortOff + 4;
 constexpr uint32_t kFusedNextTileOff = kFusedNextBlockOff + 4;
 constexpr uint32_t kFusedFinishedOff = kFusedNextTileOff + 4;
-constexpr uint32_t kFusedFinalOff = kFusedFinishedOff + 4;
+constexpr uint32_t kFusedLeftOff = kFusedFinishedOff + 4;
+constexpr uint32_t kFusedFinalOff = kFusedLeftOff + 4;
 constexpr uint32_t kFusedFailOff = kFusedFinalOff + kFusedMaxRange / 8;
 constexpr uint32_t kFusedFlagWords = (kFusedFailOff + kFusedMaxRange / 8 - kFusedFlagsOff) / 4;
 constexpr uint32_t kFusedWaveOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
@@ -694,14 +698,14 @@ __device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__bui
 // holds (true, the value in v), or the abort word is raised or the poll
 // limit runs out (false; the latter raises it).
 template <typename T, typename Pred>
-__device__ __forceinline__ bool fused_poll(uint32_t w, int lane, T &v, Pred &&ok) {
+__device__ __forceinline__ bool fused_poll(uint32_t w, int lane, uint32_t limit, T &v, Pred &&ok) {
     for (uint32_t it = 0;; it++) {
         v = uniform(lds_load_acq(w, T{}));
         if (ok(v)) return true;
         const uint32_t ab = uniform(
             __hip_atomic_load((lds_word *)(size_t)kFusedAbortOff, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         if (ab != 0) return false;
-        if (it == kSpinLimit) {
+        if (it >= limit) {
             if (lane == 0)
                 __hip_atomic_store((lds_word *)(size_t)kFusedAbortOff, 1u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -752,15 +756,31 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // bit q of a bitmap: LDS word address and mask
     auto bit_w = [&](uint32_t base, uint32_t q) { return base + 4u * (q >> 5); };
     auto bit_m = [&](uint32_t q) { return 1u << (q & 31u); };
-    auto report = [&](uint32_t q, int ln) {  // a wait ran out
-        if (ln == 0) {
-            hh_block_status st;
-            st.code = HH_ERR_DEVICE;
-            st.detail = HH_CORRUPT_NONE;
-            st.position = 0;
-            st.required = 0;
-            st.written = 0;
-            ((hh_block_status *)Fk.status)[Fk.blk_base + lb_of(q)] = st;
+    // Every wave leaves through here: its stores complete, it counts itself
+    // out, and the last one out, if a wait gave up (the abort word), writes
+    // HH_ERR_DEVICE into every block record of the workgroup (any of its
+    // tiles may be undecoded); the other waves' records are complete by then,
+    // so none overwrites it.
+    auto leave = [&]() {
+        const int l = opaque_lane();
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        uint32_t prev = 0;
+        if (l == 0)
+            prev = __hip_atomic_fetch_add((lds_word *)(size_t)kFusedLeftOff, 1u, __ATOMIC_ACQ_REL,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP);
+        prev = uniform(prev);
+        const uint32_t ab = uniform(
+            __hip_atomic_load((lds_word *)(size_t)kFusedAbortOff, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (prev + 1u == nw && ab != 0u) {
+            for (uint32_t q = (uint32_t)l; q < Q; q += 64u) {
+                hh_block_status st;
+                st.code = HH_ERR_DEVICE;
+                st.detail = HH_CORRUPT_NONE;
+                st.position = 0;
+                st.required = 0;
+                st.written = 0;
+                ((hh_block_status *)Fk.status)[Fk.blk_base + lb_of(q)] = st;
+            }
         }
     };
     // this wave's LDS area: a tile's V table and output park, or the input
@@ -804,11 +824,10 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             uint32_t pti, pt0, pnt, v;
             uint64_t sv;
             locate(lb_of(q - nbuf), pti, pt0, pnt);
-            if (!fused_poll(state_w(x), ln, sv, [&](uint64_t s) { return (uint32_t)(s >> 32) == q - nbuf + 1u; }) ||
-                !fused_poll(done_w(x), ln, v, [&](uint32_t c) { return c == pnt; })) {
-                report(q, ln);
+            if (!fused_poll(state_w(x), ln, Fk.spin_limit, sv,
+                            [&](uint64_t s) { return (uint32_t)(s >> 32) == q - nbuf + 1u; }) ||
+                !fused_poll(done_w(x), ln, Fk.spin_limit, v, [&](uint32_t c) { return c == pnt; }))
                 return false;
-            }
         }
         const uint64_t stamp = (uint64_t)(q + 1u) << 32;
         if (ln == 0) {
@@ -935,10 +954,9 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         const uint32_t tb = B.tb[ti];
         const uint32_t need = (off + 1u) * tb;
         uint64_t sv;
-        if (!fused_poll(state_w(x), ln2, sv, [&](uint64_t s) {
+        if (!fused_poll(state_w(x), ln2, Fk.spin_limit, sv, [&](uint64_t s) {
                 return (uint32_t)(s >> 32) == q + 1u && (uint32_t)s >= need;  // the tile's bytes are there
             })) {
-            report(q, ln2);
             aborted = true;
             break;
         }
@@ -951,7 +969,10 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
         });
     }
-    if (aborted) return;
+    if (aborted) {
+        leave();
+        return;
+    }
     // this wave's tile stores are complete: count it finished
     const int ln = opaque_lane();
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -962,21 +983,25 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     bool any_failed = false;
     for (uint32_t q = 0; q < Q; q++) {
         uint32_t w;
-        if (!fused_poll(bit_w(kFusedFinalOff, q), ln, w, [&](uint32_t b) { return (b & bit_m(q)) != 0u; })) {
-            report(q, ln);
+        if (!fused_poll(bit_w(kFusedFinalOff, q), ln, Fk.spin_limit, w,
+                        [&](uint32_t b) { return (b & bit_m(q)) != 0u; })) {
+            leave();
             return;
         }
         const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, q), __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
         any_failed = any_failed || (f & bit_m(q)) != 0u;
     }
-    if (!any_failed) return;
+    if (!any_failed) {
+        leave();
+        return;
+    }
     // rewrite the failed blocks' tiles (tile j of a block by wave j mod nw)
     // once every wave's own stores are complete
     {
         uint32_t c;
-        if (!fused_poll(kFusedFinishedOff, ln, c, [&](uint32_t n) { return n == nw; })) {
-            report(0, ln);
+        if (!fused_poll(kFusedFinishedOff, ln, Fk.spin_limit, c, [&](uint32_t n) { return n == nw; })) {
+            leave();
             return;
         }
     }
@@ -1003,6 +1028,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 ((int32_t HH_GLOBAL *)B.status[bti])[t] = HH_ERR_CORRUPTED_DATA;
         }
     }
+    leave();
 }
 
 }  // namespace
@@ -1158,6 +1184,11 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
         if (nbuf > kFusedMaxBufs) nbuf = kFusedMaxBufs;
         F.nbuf = nbuf;
         F.buf_off = kFusedWaveOff + nw * B.wave_lds;
+        F.spin_limit = kSpinLimit;
+        if (const char *lim = std::getenv("HH_FUSED_SPIN_LIMIT")) {
+            const unsigned long v = std::strtoul(lim, nullptr, 10);
+            if (v >= 1 && v <= kSpinLimit) F.spin_limit = (uint32_t)v;
+        }
         const uint32_t lds = F.buf_off + nbuf * kFusedBuf;
         const uint32_t threads = 64u * nw;
         // workgroup g takes blocks g, g + grid, ...: at most kFusedMaxRange

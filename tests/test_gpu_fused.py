@@ -190,6 +190,13 @@ def test_argument_errors():
     assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], 14) == Hm.UNSUPPORTED
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(100, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], 2) == Hm.OK
+    # the per-tensor entry (hh_hctt_decode_lz4_fused_tpb): a zero count, a
+    # block over HH_FUSED_BLOCK_BYTES, a block total that does not match
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], [0]) == Hm.INVALID_ARGUMENT
+    assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], [14]) == Hm.UNSUPPORTED
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o), (64, 64, k, o)], [2, 1]) == \
+        Hm.INVALID_ARGUMENT
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], [2]) == Hm.OK
 
 
 def both_paths(L, dtype, tpb, blob=None, lens=None):
@@ -317,3 +324,28 @@ def test_per_tensor_tiles_per_block():
     assert (np.delete(st["code"], bad) == 0).all()
     assert_same(T, Hm.BF16, fo, fs, bo, bs)
     assert (fs[0].cpu().numpy()[bad * tpb[0]:(bad + 1) * tpb[0]] == Hm.CORRUPTED_DATA).all()
+
+
+def test_bounded_waits_give_up_cleanly(monkeypatch):
+    # every wait of the fused kernel gives up after HH_FUSED_SPIN_LIMIT polls
+    # (normally 2^24; here 1, so the waits at the start of each workgroup's
+    # run, before its first block's bytes are decoded, run out): the waves
+    # leave through the workgroup's abort word, the records of the blocks
+    # waited on report HH_ERR_DEVICE (the others keep what the buffer held),
+    # the kernel ends, and the next call decodes normally
+    Hm = H()
+    k = Hm.hctt_retain_count(0.3)
+    tpb = 13
+    L = encode_fixed(Hm, [("a", 1024, 1024), ("b", 512, 2048)], [k, k], seed=81, tpb=tpb)
+    monkeypatch.setenv("HH_FUSED_SPIN_LIMIT", "1")
+    _, st, _ = fused(L, Hm.F32, tpb)
+    codes = st["code"]
+    print(f"[fused] spin limit 1: {int((codes == Hm.DEVICE).sum())} of {codes.size} block records HH_ERR_DEVICE",
+          flush=True)
+    assert set(np.unique(codes).tolist()) <= {Hm.OK, Hm.DEVICE}
+    assert (codes == Hm.DEVICE).any()
+    monkeypatch.delenv("HH_FUSED_SPIN_LIMIT")
+    fo, st, fs = fused(L, Hm.F32, tpb)
+    assert (st["code"] == 0).all()
+    assert all((s.cpu().numpy() == 0).all() for s in fs)
+    check_against_oracle(L, fo)
