@@ -226,9 +226,9 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
  * bytes); the tile bytes a block does not produce (all of a failed block's)
  * read as zeros, so those tiles report HH_ERR_CORRUPTED_DATA with zero
  * output.  Asynchronous on the stream.  One persistent workgroup per CU
- * takes a run of tiles: each of its waves in turn decodes the run's next
- * block into an LDS block buffer (when one is free) or the run's next tile
- * from the buffers. */
+ * takes every G-th block (G workgroups) and its tiles: each of its waves in
+ * turn decodes the next of those blocks into an LDS block buffer (when one
+ * is free) or the next of their tiles from the buffers. */
 #define HH_FUSED_BLOCK_BYTES 16352u
 int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total,
                                  const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,

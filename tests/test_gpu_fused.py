@@ -242,7 +242,8 @@ def test_many_tensors_small_blocks_f16():
 
 def test_large_retention_tiles():
     # k = 4096 (2,816-byte tiles, 5 per block) and k = 3000 (7 per block):
-    # fewer consumer waves fit the LDS next to the block buffers
+    # fewer waves fit the LDS next to the block buffers (a wave's area holds
+    # a table of k entries)
     Hm = H()
     T = G.torch()
     for k, shape in ((4096, ("a", 320, 256)), (3000, ("b", 256, 448))):
@@ -254,10 +255,11 @@ def test_large_retention_tiles():
         check_against_oracle(L, fo)
 
 
-def test_failed_blocks_at_run_boundaries():
-    # 188 blocks of two tiles over up to 256 workgroups: nearly every block is
-    # shared by two workgroups' runs; ten corrupted blocks poison all of
-    # their tiles in both, exactly as the two-launch path does
+def test_failed_blocks_one_per_workgroup():
+    # 188 blocks of two tiles over up to 256 workgroups: one block per
+    # workgroup, whose waves then mostly wait on that block's decoder; ten
+    # corrupted blocks poison all of their tiles, exactly as the two-launch
+    # path does
     Hm = H()
     T = G.torch()
     shapes = [("a", 1024, 512), ("b", 512, 1024), ("c", 768, 640)]
