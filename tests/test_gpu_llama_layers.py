@@ -11,7 +11,9 @@ idct_2d, crates/haagenti-core/src/dct.rs:311-337):
     the round-to-nearest-even of the f32 decode for every tensor;
   * a Llama-70B layer (q,o 8192x8192; k,v 1024x8192; gate,up 28672x8192;
     down 8192x28672) with a seeded retention per tensor drawn from
-    U[0.10, 0.50], all seven tensors (seven different k) in one launch.
+    U[0.10, 0.50], all seven tensors (seven different k) in one launch; the
+    same layer through the fused launch (hh_hctt_decode_lz4_fused_tpb, 10-17
+    tiles per block by tensor) bit-identical to it.
 """
 import numpy as np
 import pytest
@@ -53,6 +55,34 @@ def decode(L, dtype):
     G.sync()
     codes = status.cpu().numpy().view(np.int32)[0::8]
     return outs, codes, scratch, tst
+
+
+def decode_fused(L, dtype):
+    """The layer through one hh_hctt_decode_lz4_fused_tpb launch (tensor
+    i's blocks hold block_bytes // tile_bytes_i tiles); returns the device
+    outputs, the LZ4 status codes and the tile statuses."""
+    Hm = H()
+    T = G.torch()
+    d_in = G.dev(L["blob"])
+    in_off, in_len = G.dev(L["in_off"]), G.dev(L["in_len"])
+    n = L["in_off"].size
+    status = T.zeros(n * 32, dtype=T.uint8, device="cuda")
+    tdt = {Hm.F32: T.float32, Hm.BF16: T.bfloat16, Hm.F16: T.float16}[dtype]
+    outs, tst, desc, tpb = [], [], [], []
+    for t in L["tensors"]:
+        o = T.empty(t["rows"] * t["cols"], dtype=tdt, device="cuda")
+        s = T.full(((t["rows"] // 64) * (t["cols"] // 64),), -1, dtype=T.int32, device="cuda")
+        outs.append(o)
+        tst.append(s)
+        desc.append((t["rows"], t["cols"], t["k"], o, s))
+        tpb.append(max(1, 16384 // Hm.hctt_tile_bytes(t["k"])))
+    print(f"[layer] fused: {len(desc)} tensors, {n} LZ4 blocks, tiles per block {tpb}", flush=True)
+    rc = G.ctx().hctt_decode_lz4_fused(d_in, d_in.numel(), in_off, in_len, n, status, desc, tpb, dtype=dtype,
+                                       stream=G.stream())
+    assert rc == Hm.OK
+    G.sync()
+    codes = status.cpu().numpy().view(np.int32)[0::8]
+    return outs, codes, tst
 
 
 def check_against_oracle(L, outs):
@@ -121,3 +151,10 @@ def test_llama70b_layer_mixed_retention_matches_oracle():
     assert all((s.cpu().numpy() == 0).all() for s in tst)
     del scratch
     check_against_oracle(L, outs)
+    # the fused launch: the same bits, with no tile bytes in HBM
+    T = G.torch()
+    fo, fcodes, ftst = decode_fused(L, Hm.F32)
+    assert (fcodes == 0).all()
+    assert all((s.cpu().numpy() == 0).all() for s in ftst)
+    for t, a, b in zip(L["tensors"], outs, fo):
+        assert T.equal(a.view(T.int32), b.view(T.int32)), t["name"]
