@@ -271,7 +271,7 @@ int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_
 // ---------------------------------------------------------------- HCT-T
 
 static int32_t check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
-    if (T.rows % 64 || T.cols % 64 || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
+    if (T.rows % 64 || T.cols % 64 || T.cols > (1u << 24) || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
     const size_t nt = (size_t)(T.rows / 64) * (T.cols / 64);
     *ntiles = nt;
     if (nt == 0) return HH_OK;
@@ -325,7 +325,7 @@ int32_t hh_hctt_decode_lz4_fused_tpb(hh_context *ctx, const uint8_t *d_in, size_
         const hh_hctt_tensor &T = tensors[i];
         const uint32_t tpb = tiles_per_block[i];
         if (tpb == 0) return HH_ERR_INVALID_ARGUMENT;
-        if (T.rows % 64 || T.cols % 64 || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
+        if (T.rows % 64 || T.cols % 64 || T.cols > (1u << 24) || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
         const uint64_t nt = (uint64_t)(T.rows / 64) * (T.cols / 64);
         if (nt == 0) continue;
         if (!T.d_out || ((uintptr_t)T.d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;

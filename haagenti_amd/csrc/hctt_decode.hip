@@ -78,6 +78,14 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A wave-uniform value (read from LDS, say) moved to scalar registers, so
+// that addresses built from it are scalar bases.
+__device__ __forceinline__ uint64_t uniform(uint64_t v) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
 __device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
                                                   __builtin_bit_cast(half8, b), c, 0, 0, 0);
@@ -181,6 +189,15 @@ struct TileBatch {
     int32_t neg4;
 };
 
+// The tensor holding batch tile gt (wave-uniform), searched with the
+// descriptor's values in scalar registers.
+__device__ __forceinline__ uint32_t tensor_of(const TileBatch &B, uint32_t gt) {
+    const uint32_t n = uniform(B.n);
+    uint32_t ti = 0;
+    while (ti + 1 < n && gt >= uniform(B.start[ti + 1])) ti++;
+    return ti;
+}
+
 // Workgroup LDS layout: [zero word][batch descriptor][M fragment table][per-wave areas].
 // The zero word sits at LDS address 0, so a gathered address masked to 0
 // reads zeros.  The descriptor is copied from the kernel arguments once:
@@ -207,16 +224,28 @@ constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 template <bool DW, int NP>
 __device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, int lane,
                                               u32x4 (&pf)[NP]) {
-    uint32_t ti = 0;
-    while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
-    const uint32_t tb = B.tb[ti];
-    g_u8 *src = (g_u8 *)B.tiles[ti] + (size_t)(gt - B.start[ti]) * tb;
+    const uint32_t ti = tensor_of(B, gt);
+    const uint32_t tb = uniform(B.tb[ti]), st = uniform(B.start[ti]), sn = uniform(B.start[ti + 1]);
+    const uint64_t s0 = uniform((uint64_t)(uintptr_t)B.tiles[ti]);
+    g_u8 *src = (g_u8 *)(uintptr_t)s0 + (size_t)(gt - st) * tb;
+    {
+        // every chunk inside the tensor's tile bytes (all but its first and
+        // last tiles, usually): scalar base + 32-bit lane offset, no
+        // per-lane checks.  The chunks hold what both forms below hold
+        // inside the tile; past its end, don't-care bytes.
+        const uint64_t e0 = s0 + (uint64_t)(sn - st) * tb;
+        const uint64_t a0 = (uint64_t)(uintptr_t)src & ~(uint64_t)3;
+        if (a0 >= s0 && a0 + 1024u * NP <= e0) {
+#pragma unroll
+            for (int i = 0; i < NP; i++) pf[i] = *(g_u32x4 *)((g_u8 *)(uintptr_t)a0 + 16u * (lane + 64u * i));
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < NP; i++) {
         const uint32_t off = 16u * (lane + 64u * i);
         if constexpr (!DW) {
-            const uintptr_t s0 = (uintptr_t)B.tiles[ti];
-            const uintptr_t e0 = s0 + (size_t)(B.start[ti + 1] - B.start[ti]) * tb;  // >= s0 + 515
+            const uintptr_t e0 = (uintptr_t)s0 + (size_t)(sn - st) * tb;  // >= s0 + 515
             const uintptr_t ts = (uintptr_t)src;
             const uintptr_t a = (ts & ~(uintptr_t)3) + off;
             if (a >= s0 && a + 16 <= e0) {
@@ -264,7 +293,7 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                                           int32_t n4, Hook &&consumed) {
     const int h = lane >> 5;
     const int l32 = lane & 31;
-    const uint32_t k = B.k[ti], cols = B.cols[ti];
+    const uint32_t k = uniform(B.k[ti]), cols = uniform(B.cols[ti]);
     const uint32_t nsc = (k + 31) >> 5;
     const uint32_t nib_off = 512 + 2 * nsc;
 
@@ -420,15 +449,22 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     const uint32_t i_lo = wbase + (uint32_t)l32 * pitch;
     const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * pitch;
     constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
-    const uint32_t tpr = B.tiles_per_row[ti];
+    const uint32_t tpr = uniform(B.tiles_per_row[ti]);
     const uint32_t tr = t / tpr, tc = t % tpr;
     const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
+    // the tile's first output byte and the row pitch, in scalar registers:
+    // a store addresses scalar base + 32-bit lane offset (no 64-bit vector
+    // arithmetic per store)
+    uint8_t HH_GLOBAL *const otile =
+        (uint8_t HH_GLOBAL *)uniform((uint64_t)(uintptr_t)((uint8_t HH_GLOBAL *)B.out[ti] + esz * base));
+    const uint32_t opitch = uniform(cols * esz);
     // row stores of columns [c0, c0 + ncols) from the park (16 bytes per lane)
     auto store = [&](uint32_t c0, auto ncolc) {
         constexpr uint32_t ncols = decltype(ncolc)::value;
         constexpr uint32_t per_row = ncols * esz / 16;  // lanes per row
         constexpr uint32_t rows_per = 64 / per_row;     // rows per instruction
         const uint32_t rsub = (uint32_t)lane / per_row, csub = (uint32_t)lane % per_row;
+        const uint32_t loff = rsub * opitch + esz * c0 + 16 * csub;  // < 16 rows: fits 32 bits
 #pragma unroll
         for (uint32_t it = 0; it < 64 / rows_per; it++) {
             const uint32_t row = rows_per * it + rsub;
@@ -441,8 +477,7 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                 const u32x2 lo = *(lds_u32x2 *)(size_t)a0, hi = *(lds_u32x2 *)(size_t)(a0 + 8);
                 v = u32x4{lo[0], lo[1], hi[0], hi[1]};
             }
-            uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[ti] + esz * (base + (size_t)row * cols + c0);
-            *(u32x4 HH_GLOBAL *)(o + 16 * csub) = v;
+            *(u32x4 HH_GLOBAL *)(otile + (size_t)(rows_per * it) * opitch + loff) = v;
         }
     };
 #pragma unroll
@@ -517,7 +552,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
                                                                    const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = (int)uniform((uint32_t)threadIdx.x >> 6);  // in a scalar register
     u32x4 *mtab = reinterpret_cast<u32x4 *>(smem + kMTabOff);
     for (int i = threadIdx.x; i < (int)(sizeof(TileBatch) / 4); i += kThreads)
         reinterpret_cast<uint32_t *>(smem + kBatchOff)[i] = reinterpret_cast<const uint32_t *>(&Bk)[i];
@@ -546,9 +581,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
             *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
     }
     for (; gt < ntiles; gt += stride) {
-        uint32_t ti = 0;
-        while (ti + 1 < B.n && gt >= B.start[ti + 1]) ti++;
-        const uint32_t t = gt - B.start[ti];
+        const uint32_t ti = tensor_of(B, gt);
+        const uint32_t t = gt - uniform(B.start[ti]);
 
         // This tile's bytes are staged in LDS.  Fetch the next tile now; it is
         // staged at the end of this iteration, long after the loads landed
@@ -688,11 +722,6 @@ __device__ __forceinline__ uint64_t lds_load_acq(uint32_t a, uint64_t) {
 __device__ __forceinline__ uint32_t lds_load_acq(uint32_t a, uint32_t) {
     return __hip_atomic_load((lds_word *)(size_t)a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ uint64_t uniform(uint64_t v) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
-           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-}
-__device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 
 // Polls the LDS word (32 or 64 bits, by T) at LDS address w until ok(value)
 // holds (true, the value in v), or the abort word is raised or the poll

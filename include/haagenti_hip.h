@@ -170,7 +170,8 @@ uint32_t hh_hctt_retain_count(float rho);
  * 741-745) -> 2-D inverse DCT (haagenti-core/src/dct.rs:311-337), on MFMA.
  * d_tile_status (optional, one int32 per tile) receives HH_OK or
  * HH_ERR_CORRUPTED_DATA (bitmap popcount != k; that tile is written as
- * zeros).  Output row-major rows x cols of out_dtype.
+ * zeros).  Output row-major rows x cols of out_dtype; rows and cols are
+ * multiples of 64, cols at most 2^24 (else HH_ERR_INVALID_ARGUMENT).
  * Replaces GpuDctContext::idct_2d_gpu (crates/haagenti-cuda/src/dct_gpu.rs:1163)
  * and GpuDecompressor::decompress_to_gpu (decompress.rs:183-203). */
 int32_t hh_hctt_decode(hh_context *ctx, const uint8_t *d_tiles, size_t tiles_len,
