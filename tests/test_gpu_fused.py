@@ -189,6 +189,7 @@ def test_argument_errors():
     assert G.ctx().hctt_decode_lz4_fused(*args, 3, st, [(128, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
     assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], 14) == Hm.UNSUPPORTED
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(100, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
+    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(64, (1 << 24) + 64, k, o)], 2) == Hm.INVALID_ARGUMENT
     assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], 2) == Hm.OK
     # the per-tensor entry (hh_hctt_decode_lz4_fused_tpb): a zero count, a
     # block over HH_FUSED_BLOCK_BYTES, a block total that does not match

@@ -116,6 +116,22 @@ def test_corrupted_bitmap_tile_reports_and_zeroes():
     assert np.abs(got[ok] - good[ok]).max() <= TOL * rms
 
 
+def test_shape_limits_are_argument_errors():
+    """rows / cols not multiples of 64, or cols above 2^24 (the stores'
+    32-bit row offsets), are rejected before any launch."""
+    import haagenti_amd as Hm
+    T = G.torch()
+    k = 1024
+    tiles = G.dev(_encode(64, 64, k, seed=3))
+    o = T.empty(64 * 64, dtype=T.float32, device="cuda")
+    for rows, cols in ((64, 100), (100, 64), (64, (1 << 24) + 64)):
+        with pytest.raises(Hm.HaagentiError) as e:
+            G.ctx().hctt_decode(tiles, tiles.numel(), rows, cols, k, o)
+        assert e.value.code == Hm.INVALID_ARGUMENT, (rows, cols)
+    G.ctx().hctt_decode(tiles, tiles.numel(), 64, 64, k, o)
+    G.sync()
+
+
 def test_config3_8192x8192_vs_oracle():
     # 16,384 tiles, top 25% (k = 1024), f32 output against the oracle, plus
     # Parseval per tile (orthonormal IDCT preserves energy).
