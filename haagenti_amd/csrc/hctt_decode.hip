@@ -770,10 +770,12 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
 
     // block lb -> tensor, first tile, tile count
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
+        const uint32_t n = uniform(B.n);
         ti = 0;
-        while (ti + 1 < B.n && lb >= F.blk_start[ti + 1]) ti++;
-        t0 = (lb - F.blk_start[ti]) * F.tpb[ti];
-        nt = min(F.tpb[ti], B.start[ti + 1] - B.start[ti] - t0);
+        while (ti + 1 < n && lb >= uniform(F.blk_start[ti + 1])) ti++;
+        const uint32_t tpb_i = uniform(F.tpb[ti]);
+        t0 = (lb - uniform(F.blk_start[ti])) * tpb_i;
+        nt = min(tpb_i, uniform(B.start[ti + 1]) - uniform(B.start[ti]) - t0);
     };
     // The workgroup's blocks: launch blocks g, g + G, g + 2 G, ... (G
     // workgroups), its q-th block lb(q) = g + q G, all of whose tiles it
@@ -866,7 +868,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         const uint32_t lb = lb_of(q);
         uint32_t ti, t0, nt;
         locate(lb, ti, t0, nt);
-        const uint32_t tb = B.tb[ti];
+        const uint32_t tb = uniform(B.tb[ti]);
         const uint32_t cap = nt * tb;
         uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
         const uint32_t gb = Fk.blk_base + lb;
@@ -980,7 +982,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         if (aborted) break;
         const int ln2 = opaque_lane();
         const uint32_t x = q % nbuf;
-        const uint32_t tb = B.tb[ti];
+        const uint32_t tb = uniform(B.tb[ti]);
         const uint32_t need = (off + 1u) * tb;
         uint64_t sv;
         if (!fused_poll(state_w(x), ln2, Fk.spin_limit, sv, [&](uint64_t s) {
