@@ -287,7 +287,10 @@ __device__ __forceinline__ uint32_t tile_shift(const TileBatch &B, uint32_t ti, 
 // same area as a pointer).  `consumed` runs once the tile's bytes are no
 // longer read: right after the V table is built (HALF), or just before the
 // output stores (whole-tile park; EARLY: right after the V table there too).
-template <int DT, bool HALF, bool EARLY = false, typename Hook>
+// PRIO raises the wave's issue priority over the two products (the tile
+// kernel, where every wave decodes tiles; not the fused kernel, whose LZ4
+// waves would then starve).
+template <int DT, bool HALF, bool EARLY = false, bool PRIO = false, typename Hook>
 __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint32_t t, const uint8_t *pay,
                                           uint32_t *V, uint32_t wbase, const u32x4 *mtab, int lane, float one,
                                           int32_t n4, Hook &&consumed) {
@@ -363,6 +366,10 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     //    acc[upar][vpar][n] = sum_v C[2m + upar][v] M[v][n], v of parity vpar,
     //    n < 32.  Then S[u][n] = E + O and S[u][63 - n] = E - O.
     floatx16 acc[2][2];
+    // PRIO: the wave issues at raised priority from here to its last MFMA
+    // (the second column block's output stage), so that the matrix cores are
+    // fed while the other waves' gathers, splits and stores fill the VALU
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int up = 0; up < 2; up++) {
         const uint64_t b64 = ok ? bits_r[up] : 0ull;
@@ -505,6 +512,8 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                 x2[up] = mfma(slo, mh, x2[up]);
             }
         }
+        if constexpr (PRIO)
+            if (jb == 1) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             float va[4], vc[4];  // rows i and 63 - i, columns ascending
@@ -592,7 +601,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
         prefetch_tile<DW, NP>(B, has_next ? gt + stride : gt, lane, pf);
         wave_sync();
 
-        tile_body<DT, false>(B, ti, t, pay + tile_shift<DW>(B, ti, t), V, wbase, mtab, lane, one, n4, [&]() {
+        tile_body<DT, false, false, true>(B, ti, t, pay + tile_shift<DW>(B, ti, t), V, wbase, mtab, lane, one, n4, [&]() {
             // stage the next tile's bytes (the current ones are no longer needed)
 #pragma unroll
             for (int i = 0; i < NP; i++)
