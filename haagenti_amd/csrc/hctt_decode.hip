@@ -189,12 +189,15 @@ struct TileBatch {
     int32_t neg4;
 };
 
-// The tensor holding batch tile gt (wave-uniform), searched with the
-// descriptor's values in scalar registers.
+// The tensor holding batch tile gt (wave-uniform): the count of tensor
+// starts after the first at or below gt (the starts ascend).  The loads are
+// independent, so they overlap instead of taking one LDS round trip per
+// tensor passed.
 __device__ __forceinline__ uint32_t tensor_of(const TileBatch &B, uint32_t gt) {
     const uint32_t n = uniform(B.n);
     uint32_t ti = 0;
-    while (ti + 1 < n && gt >= uniform(B.start[ti + 1])) ti++;
+#pragma unroll
+    for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += (j < n && gt >= uniform(B.start[j])) ? 1u : 0u;
     return ti;
 }
 
@@ -779,9 +782,12 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
 
     // block lb -> tensor, first tile, tile count
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
+        // the count of tensor first blocks after the first at or below lb
+        // (independent loads, as in tensor_of)
         const uint32_t n = uniform(B.n);
         ti = 0;
-        while (ti + 1 < n && lb >= uniform(F.blk_start[ti + 1])) ti++;
+#pragma unroll
+        for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += (j < n && lb >= uniform(F.blk_start[j])) ? 1u : 0u;
         const uint32_t tpb_i = uniform(F.tpb[ti]);
         t0 = (lb - uniform(F.blk_start[ti])) * tpb_i;
         nt = min(tpb_i, uniform(B.start[ti + 1]) - uniform(B.start[ti]) - t0);
