@@ -187,6 +187,18 @@ __device__ __forceinline__ uint64_t ld64(const uint8_t *p, const uint8_t *lo, co
     return (uint64_t)x | ((uint64_t)y << 32);
 }
 
+// Eight input bytes at abase + off + sh (abase 4-byte aligned and
+// wave-uniform, off a multiple of 4, sh = the input's address mod 4), when
+// every byte read lies inside the buffer: scalar base plus a 32-bit lane
+// offset, no per-lane checks.
+__device__ __forceinline__ uint64_t ld64_in(const uint8_t *abase, uint32_t off, uint32_t sh) {
+    uint32_t w[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) w[k] = *reinterpret_cast<const uint32_t *>(abase + off + 4 * k);
+    const uint32_t x = __builtin_amdgcn_alignbyte(w[1], w[0], sh), y = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
+    return (uint64_t)x | ((uint64_t)y << 32);
+}
+
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
     const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
     return (uint64_t)lo | ((uint64_t)hi << 32);
@@ -201,7 +213,8 @@ __global__ __launch_bounds__(64 * kWaves) void xxh3_batch_kernel(const uint8_t *
     for (int i = threadIdx.x; i < 192; i += blockDim.x) sec[i] = d_secret[i];
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const uint32_t b = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    // wave-uniform (scalar): the block's offset, length and base follow
+    const uint32_t b = blockIdx.x * kWaves + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (b >= n) return;
     const uint64_t o = off[b];
     const uint32_t L = len[b];
@@ -239,8 +252,16 @@ __global__ __launch_bounds__(64 * kWaves) void xxh3_batch_kernel(const uint8_t *
     for (uint32_t blk = 0; blk < nb; blk++) {
         uint64_t n0 = 0, n1 = 0;
         if (blk + 1 < nb) {  // next block's words, loaded before this one is reduced
-            n0 = ld64(in + 1024 * (blk + 1) + 64 * s + 8 * i, lo, hi);
-            n1 = ld64(in + 1024 * (blk + 1) + 64 * (s + 8) + 8 * i, lo, hi);
+            const uint8_t *nbk = in + 1024 * (size_t)(blk + 1);
+            const uint8_t *ab = (const uint8_t *)((uintptr_t)nbk & ~(uintptr_t)3);
+            if (ab >= lo && ab + 1024 + 12 <= hi) {  // the block's words inside the buffer
+                const uint32_t sh = (uint32_t)((uintptr_t)nbk & 3u);
+                n0 = ld64_in(ab, 64u * s + 8u * i, sh);
+                n1 = ld64_in(ab, 64u * (s + 8) + 8u * i, sh);
+            } else {
+                n0 = ld64(nbk + 64 * s + 8 * i, lo, hi);
+                n1 = ld64(nbk + 64 * (s + 8) + 8 * i, lo, hi);
+            }
         }
         const uint64_t x0 = v0 ^ k0, x1 = v1 ^ k1;
         const uint64_t prod = (x0 & 0xffffffffull) * (x0 >> 32) + (x1 & 0xffffffffull) * (x1 >> 32);
