@@ -164,6 +164,18 @@ class Timed:
         return float(t.min()), float(np.median(t)), float(t.max())
 
 
+LZ4_KERNEL_NAMES = {"auto": "lz4_ring_kernel<4096, 4096>", "seq": "lz4_seq_kernel<4096, 4096>", "seq8": "lz4_seq_kernel<8192, 2048>",
+                    "ring4": "lz4_ring_kernel<4096, 4096>", "ring8": "lz4_ring_kernel<8192, 2048>",
+                    "ring16": "lz4_ring_kernel<16384, 3072>", "ring32": "lz4_ring_kernel<32768, 4096>",
+                    "window": "lz4_batch_kernel"}
+
+
+def new_ctx(H, args):
+    ctx = H.HipContext(0)
+    ctx.set_lz4_decoder(args.lz4_decoder)
+    return ctx
+
+
 def warm(step, args):
     """Untimed steps right before the timed region: the checks before it
     leave the GPU idle and its clocks fall back."""
@@ -262,7 +274,7 @@ def wl_llama3_8b_layer(args, torch, H, O):
         f"{layers_host[0]['blob'].size / 1e6:.1f} MB compressed, "
         f"{layers_host[0]['scratch_bytes'] / 1e6:.1f} MB tile bytes per layer")
 
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     tabs = [dict(in_off=devtab(torch, L["in_off"]), in_len=devtab(torch, L["in_len"]),
@@ -395,7 +407,7 @@ def wl_int4(args, torch, H, O):
     rng = np.random.default_rng(1)
     w = rng.normal(0, 0.02, n).astype(np.float32)
     q = H.quantize_int4(w)
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     dq = torch.from_numpy(q.copy()).cuda()
@@ -464,7 +476,7 @@ def wl_lz4(args, torch, H, O):
     srcs, pick, blob, in_off, in_len = config2_blocks(H)
     out_off = np.arange(nb, dtype=np.uint64) * 65536
     out_cap = np.full(nb, 65536, np.uint32)
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     d_in = torch.from_numpy(blob.copy()).cuda()
@@ -512,7 +524,7 @@ def wl_lz4(args, torch, H, O):
                 "synthetic (64 distinct seeded blocks, seeded coin per block)",
                 {"blocks": nb, "block_bytes": 65536, "in_bytes": int(blob.size),
                  "launches_per_step": launches},
-                roofline("lz4-256mib", "lz4_ring_kernel<4096, 4096>", blob.size + out_b, per), cpu,
+                roofline("lz4-256mib", LZ4_KERNEL_NAMES[args.lz4_decoder], blob.size + out_b, per), cpu,
                 {"bit_exact": exact})
 
 
@@ -525,7 +537,7 @@ def wl_idct(args, torch, H, O):
     tiles = H.hctt_encode(w, k)
     del w
     log(f"encoded 8192x8192 in {time.time() - t0:.1f}s ({tiles.size} tile bytes)")
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     dt = torch.from_numpy(tiles).cuda()
@@ -591,7 +603,7 @@ def wl_hct3(args, torch, H, O):
     HBM, bf16 output."""
     import struct
     n = 4096
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     g = torch.Generator(device="cuda")
@@ -693,7 +705,7 @@ def wl_stream(args, torch, H, O):
     L = encode_layer(H, L70B, ks, 70, args.lz4_block)
     log(f"encoded one 70B layer in {time.time() - t0:.1f}s: {L['blob'].size / 1e6:.1f} MB "
         f"compressed, {L['scratch_bytes'] / 1e6:.1f} MB tile bytes; k = {ks}")
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     nin = int(L["blob"].size)
     nb = int(L["in_off"].size)
     cfg = P.default_config()
@@ -827,7 +839,9 @@ def wl_stream(args, torch, H, O):
                 "source": file_info["source"] if file_info else "pinned host memory (hh_pinned_alloc)",
                 "value_is": "decode-only (events around LZ4 + tile decode on the pipeline's compute stream)",
                 "runtime": "hh_pipeline_* (copy stream + compute stream, 2 staging slots)"},
-               roofline("llama70b-stream", "lz4_ring_kernel + hctt_decode_kernel<bf16>",
+               roofline("llama70b-stream",
+                        LZ4_KERNEL_NAMES["seq" if args.lz4_decoder == "auto" else args.lz4_decoder].split("<")[0]
+                        + " + hctt_decode_kernel<bf16>",
                         L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
                cpu,
                {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
@@ -848,7 +862,7 @@ def wl_copy(args, torch, H, O):
     a = torch.empty(n, dtype=torch.uint8, device="cuda")
     b = torch.empty(n, dtype=torch.uint8, device="cuda")
     a.fill_(1)
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     launches = 10
@@ -879,7 +893,7 @@ def wl_copy(args, torch, H, O):
 def wl_xxh3(args, torch, H, O):
     nb = 4096
     srcs, pick, blob, in_off, in_len = config2_blocks(H)
-    ctx = H.HipContext(0)
+    ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     d_in = torch.from_numpy(blob.copy()).cuda()
@@ -947,6 +961,8 @@ def main():
     ap.add_argument("--path", choices=["fused", "two-launch"], default="fused",
                     help="llama3-8b-layer: one fused LZ4 + tile launch per layer (hh_hctt_decode_lz4_fused) "
                          "or the LZ4 and tile launches through a scratch buffer (hh_hctt_decode_lz4_batch)")
+    ap.add_argument("--lz4-decoder", default="auto", choices=sorted(LZ4_KERNEL_NAMES),
+                    help="LZ4 block decoder of the batched LZ4 launches (the context's HH_OPT_LZ4_DECODER)")
     ap.add_argument("--lz4-block", type=int, default=16384,
                     help="LZ4 block size in bytes before rounding down to whole tiles "
                          "(the reference HctWriter default is 16 KiB)")

@@ -44,6 +44,10 @@ CORRUPT_BITMAP_COUNT = 3
 
 F32, F16, BF16 = 0, 1, 2
 
+# hh_context_set_option options and LZ4 decoders (diagnostics and tests)
+OPT_LZ4_DECODER, OPT_FUSED_POLL_LIMIT = 1, 2
+LZ4_DECODERS = {"auto": 0, "seq": 1, "seq8": 2, "ring4": 3, "ring8": 4, "ring16": 5, "ring32": 6, "window": 7}
+
 
 class BlockStatus(C.Structure):
     _fields_ = [("code", C.c_int32), ("detail", C.c_int32), ("position", C.c_uint64),
@@ -83,6 +87,7 @@ _sig("hh_context_create", _i32, [_i32, C.POINTER(_vp)])
 _sig("hh_context_destroy", None, [_vp])
 _sig("hh_context_stream", _vp, [_vp])
 _sig("hh_context_synchronize", _i32, [_vp])
+_sig("hh_context_set_option", _i32, [_vp, _i32, C.c_int64])
 _sig("hh_lz4_decompress_batch", _i32, [_vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp])
 _sig("hh_lz4_decompress_to", _i32, [_vp, _vp, _sz, _vp, _sz, C.POINTER(_sz), C.POINTER(BlockStatus)])
 _sig("hh_lz4_compress_block", _i32, [_vp, _sz, _vp, _sz, C.POINTER(_sz)])
@@ -212,7 +217,7 @@ _sig("hh_hbm_copy", _i32, [_vp, _vp, _vp, C.c_uint64, _vp])
 EXPORTS = [
     "hh_status_category", "hh_status_is_recoverable", "hh_version", "hh_device_count",
     "hh_context_create", "hh_context_destroy", "hh_context_stream", "hh_context_synchronize",
-    "hh_lz4_decompress_batch", "hh_lz4_decompress_to", "hh_lz4_compress_block",
+    "hh_context_set_option", "hh_lz4_decompress_batch", "hh_lz4_decompress_to", "hh_lz4_compress_block",
     "hh_lz4_max_compressed_size", "hh_dequant_int4", "hh_quantize_int4",
     "hh_int4_compressed_size", "hh_hctt_tile_bytes", "hh_hctt_retain_count",
     "hh_hctt_decode", "hh_hctt_decode_batch", "hh_hctt_decode_lz4_batch", "hh_hctt_decode_lz4_batch_noalloc",
@@ -344,6 +349,14 @@ class HipContext:
 
     def synchronize(self):
         _check(_lib.hh_context_synchronize(self._p))
+
+    def set_option(self, option, value):
+        """hh_context_set_option: OPT_LZ4_DECODER (a value of LZ4_DECODERS) or
+        OPT_FUSED_POLL_LIMIT (polls per wait of the fused decode, 0 = default)."""
+        _check(_lib.hh_context_set_option(self._p, int(option), int(value)), "hh_context_set_option")
+
+    def set_lz4_decoder(self, name):
+        self.set_option(OPT_LZ4_DECODER, LZ4_DECODERS[name])
 
     def close(self):
         if getattr(self, "_p", None):

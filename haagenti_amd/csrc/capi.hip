@@ -177,6 +177,21 @@ int32_t hh_context_synchronize(hh_context *ctx) {
     return from_hip(hipStreamSynchronize(ctx->stream));
 }
 
+int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    switch (option) {
+        case HH_OPT_LZ4_DECODER:
+            if (value < HH_LZ4_AUTO || value > HH_LZ4_WINDOW) return HH_ERR_INVALID_ARGUMENT;
+            ctx->lz4_decoder = (int32_t)value;
+            return HH_OK;
+        case HH_OPT_FUSED_POLL_LIMIT:
+            if (value < 0 || value > (1 << 24)) return HH_ERR_INVALID_ARGUMENT;
+            ctx->fused_poll_limit = (uint32_t)value;
+            return HH_OK;
+        default: return HH_ERR_INVALID_ARGUMENT;
+    }
+}
+
 // ---------------------------------------------------------------- LZ4
 
 int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
@@ -193,7 +208,7 @@ int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_
     // the caller's output buffer has no stated size: its block table is trusted
     const hh::Lz4Batch B = {d_in,      in_total,  d_in_off, d_in_len, d_out, ~0ull,
                             d_out_off, d_out_cap, nblocks,  d_status};
-    return from_hip(hh::launch_lz4_batch(B, pick_stream(ctx, stream)));
+    return from_hip(hh::launch_lz4_batch(B, hh::lz4_decoder_for(ctx, HH_LZ4_RING4), pick_stream(ctx, stream)));
 }
 
 int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, uint8_t *out,
@@ -230,7 +245,7 @@ int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, 
                             reinterpret_cast<uint32_t *>(base + 56),
                             1,
                             reinterpret_cast<hh_block_status *>(base)};
-    e = hh::launch_lz4_batch(B, s);
+    e = hh::launch_lz4_batch(B, hh::lz4_decoder_for(ctx, HH_LZ4_RING4), s);
     if (e != hipSuccess) return from_hip(e);
     hh_block_status st;
     e = hipMemcpyAsync(&st, base, sizeof(st), hipMemcpyDeviceToHost, s);
@@ -341,7 +356,7 @@ int32_t hh_hctt_decode_lz4_fused_tpb(hh_context *ctx, const uint8_t *d_in, size_
     if (guard.status() != hipSuccess) return from_hip(guard.status());
     return from_hip(hh::launch_hctt_lz4_fused(tensors, ntensors, tiles_per_block, d_in, in_total, d_in_off,
                                               d_in_len, d_status, out_dtype, ctx->d_basis, ctx->num_cus,
-                                              pick_stream(ctx, stream)));
+                                              ctx->fused_poll_limit, pick_stream(ctx, stream)));
 }
 
 int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,
@@ -501,7 +516,7 @@ int32_t hct_blocks(hh_context *ctx, const uint8_t *h_file, const uint8_t *d_file
                 he = hipMemcpyAsync(d_cap, expect.data(), 4 * (size_t)md, hipMemcpyHostToDevice, s);
             const hh::Lz4Batch B = {d_file,    file_len, d_in_off, d_in_len, dst, direct ? out_cap : nominal,
                                     d_out_off, d_cap,    md,       d_st};
-            if (he == hipSuccess) he = hh::launch_lz4_batch(B, s);
+            if (he == hipSuccess) he = hh::launch_lz4_batch(B, hh::lz4_decoder_for(ctx, HH_LZ4_RING4), s);
             if (he == hipSuccess)
                 he = hipMemcpyAsync(st.data(), d_st, 32 * (size_t)md, hipMemcpyDeviceToHost, s);
         }

@@ -665,7 +665,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
 // before a claimed tile of slot i or later); a tile's wave waits for its
 // block's bytes, whose decoder waits only on lower slots; every such chain
 // descends to a slot whose buffer is free.  Every wait is bounded all the
-// same (kSpinLimit polls, or HH_FUSED_SPIN_LIMIT from the environment, which
+// same (kSpinLimit polls, or the context's HH_OPT_FUSED_POLL_LIMIT, which
 // tests set small to run this path); one that runs out raises the
 // workgroup's abort word, every wave then leaves, and every block record of
 // the workgroup reports HH_ERR_DEVICE (written by the last wave to leave).
@@ -1173,7 +1173,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
 hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
-                                 hipStream_t s) {
+                                 uint32_t poll_limit, hipStream_t s) {
     uint32_t blk = 0;  // global block number of the next tensor's first block
     for (uint32_t i = 0; i < n;) {
         TileBatch B;
@@ -1230,11 +1230,7 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
         if (nbuf > kFusedMaxBufs) nbuf = kFusedMaxBufs;
         F.nbuf = nbuf;
         F.buf_off = kFusedWaveOff + nw * B.wave_lds;
-        F.spin_limit = kSpinLimit;
-        if (const char *lim = std::getenv("HH_FUSED_SPIN_LIMIT")) {
-            const unsigned long v = std::strtoul(lim, nullptr, 10);
-            if (v >= 1 && v <= kSpinLimit) F.spin_limit = (uint32_t)v;
-        }
+        F.spin_limit = poll_limit >= 1 && poll_limit <= kSpinLimit ? poll_limit : kSpinLimit;
         const uint32_t lds = F.buf_off + nbuf * kFusedBuf;
         const uint32_t threads = 64u * nw;
         // workgroup g takes blocks g, g + grid, ...: at most kFusedMaxRange

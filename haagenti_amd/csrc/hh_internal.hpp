@@ -38,6 +38,10 @@ struct hh_context {
     // at context creation (capi_noalloc.hip), and the lookup's result.
     uint8_t *noalloc_scratch = nullptr;
     hipError_t noalloc_status = hipErrorNotInitialized;
+    // hh_context_set_option settings: the LZ4 decoder (hh_lz4_decoder) and
+    // the poll limit of the fused decode's waits (0: the default)
+    int32_t lz4_decoder = HH_LZ4_AUTO;
+    uint32_t fused_poll_limit = 0;
 };
 
 namespace hh {
@@ -154,11 +158,16 @@ struct Lz4Batch {
     hh_block_status *status;
 };
 
-// Batched LZ4: dispatches to the LDS-ring decoder (lz4_ring.hip) or, when
-// the environment sets HH_LZ4_KERNEL=window, to the register-window decoder
-// (lz4_decode.hip).  The ring is 4 KiB with a 4 KiB input stage;
-// HH_LZ4_KERNEL=ring8 / ring16 / ring32 select an 8 / 16 / 32 KiB ring.
-hipError_t launch_lz4_batch(const Lz4Batch &B, hipStream_t s);
+// Batched LZ4 with the decoder `decoder` (hh_lz4_decoder; HH_LZ4_AUTO is
+// resolved by the caller): the sequence-batched decoder (lz4_seq.hip), the
+// one-sequence-at-a-time LDS ring decoder (lz4_ring.hip) or the
+// register-window decoder (lz4_decode.hip).
+hipError_t launch_lz4_batch(const Lz4Batch &B, int32_t decoder, hipStream_t s);
+// The context's decoder for an entry point whose default is `dflt`.
+inline int32_t lz4_decoder_for(const hh_context *ctx, int32_t dflt) {
+    return ctx->lz4_decoder == HH_LZ4_AUTO ? dflt : ctx->lz4_decoder;
+}
+hipError_t launch_lz4_seq(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s);
 hipError_t launch_lz4_ring(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s);
 
 hipError_t launch_xxh3_batch(const uint8_t *d_data, size_t data_len, const uint64_t *d_off,
@@ -264,10 +273,11 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
 // launch per 8 tensors (hctt_decode.hip; validated by the caller: tensor i's
 // blocks are the next ceil(ntiles_i / tpb[i]) of d_in_off / d_in_len, each
 // tpb[i] * tile bytes <= fused_block_max()).
+// poll_limit: polls before a wait gives up (0: the default 2^24).
 hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
-                                 hipStream_t s);
+                                 uint32_t poll_limit, hipStream_t s);
 uint32_t fused_block_max();
 
 }  // namespace hh

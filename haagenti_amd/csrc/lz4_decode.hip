@@ -351,15 +351,17 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(Lz4Batch B) {
 
 }  // namespace
 
-hipError_t launch_lz4_batch(const Lz4Batch &B, hipStream_t s) {
+hipError_t launch_lz4_batch(const Lz4Batch &B, int32_t decoder, hipStream_t s) {
     if (B.nblocks == 0) return hipSuccess;
-    const char *k = std::getenv("HH_LZ4_KERNEL");
-    if (k == nullptr || std::strcmp(k, "window") != 0) {
-        uint32_t kib = 4u;
-        if (k != nullptr && std::strcmp(k, "ring8") == 0) kib = 8u;
-        if (k != nullptr && std::strcmp(k, "ring16") == 0) kib = 16u;
-        if (k != nullptr && std::strcmp(k, "ring32") == 0) kib = 32u;
-        return launch_lz4_ring(B, kib, s);
+    switch (decoder) {
+        case HH_LZ4_AUTO:
+        case HH_LZ4_SEQ: return launch_lz4_seq(B, 4u, s);
+        case HH_LZ4_SEQ8: return launch_lz4_seq(B, 8u, s);
+        case HH_LZ4_RING4: return launch_lz4_ring(B, 4u, s);
+        case HH_LZ4_RING8: return launch_lz4_ring(B, 8u, s);
+        case HH_LZ4_RING16: return launch_lz4_ring(B, 16u, s);
+        case HH_LZ4_RING32: return launch_lz4_ring(B, 32u, s);
+        default: break;
     }
     const uint32_t grid = (B.nblocks + kWaves - 1) / kWaves;
     hipLaunchKernelGGL(lz4_batch_kernel, dim3(grid), dim3(kThreads), 0, s, B);

@@ -1,0 +1,84 @@
+// Batched raw-LZ4 block decoder: one wavefront per block, sequences parsed
+// in batches and copied lane-parallel (the decoder is in lz4_seq.hpp).
+#include "lz4_seq.hpp"
+
+namespace hh {
+namespace {
+
+template <uint32_t R, uint32_t S>
+__global__ __launch_bounds__(64) void lz4_seq_kernel(Lz4Batch B) {
+    using D = seq::SeqDec<R, S, false>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    if (b >= B.nblocks) return;
+
+    int32_t code = HH_OK, detail = HH_CORRUPT_NONE;
+    uint64_t pos = 0, req = 0;
+
+    const uint64_t ioff = B.in_off[b];
+    const uint32_t ilen = B.in_len[b];
+    const uint64_t oofs = B.out_off[b];
+    const uint32_t ocap = B.out_cap[b];
+    const bool out_ok = oofs <= B.out_total && (uint64_t)ocap <= B.out_total - oofs;
+    uint8_t *out = B.out + oofs;
+    D d;
+    seq::lds8 *lds = (seq::lds8 *)smem;
+    d.ring = lds;
+    d.tab = reinterpret_cast<seq::lds32 *>(lds + R);
+    d.stage = lds + R + D::kTabLds + D::kSFront;
+    d.gbuf = B.in;
+    d.gsz = B.in_total;
+    d.ioff = ioff;
+    d.a0 = (uint32_t)((uintptr_t)out & 15u);
+    d.obase = out - d.a0;
+    d.cap = ocap;
+    d.sb = 0;
+    d.at_end = false;
+    d.op = 0;
+    d.fl = 0;
+    d.lane = lane;
+
+    if (ioff > B.in_total || (uint64_t)ilen > B.in_total - ioff || !out_ok) {
+        code = HH_ERR_INVALID_ARGUMENT;
+    } else {
+        seq::decode_block(d, ilen, code, detail, pos, req);
+        if (code == HH_OK) d.flush(true);
+    }
+    // a failed block's output reads as zeros (the reference returns no output)
+    if (code != HH_OK && out_ok) {
+        __asm__ __volatile__("" ::: "memory");
+        wave_zero_fill(out, d.cap, lane);
+    }
+    if (lane == 0) {
+        hh_block_status st;
+        st.code = code;
+        st.detail = detail;
+        st.position = pos;
+        st.required = req;
+        st.written = code == HH_OK ? d.op : 0;
+        B.status[b] = st;
+    }
+}
+
+template <uint32_t R, uint32_t S>
+hipError_t launch_seq(const Lz4Batch &B, hipStream_t s) {
+    constexpr uint32_t lds = seq::SeqDec<R, S, false>::kLds;
+    hipError_t e = hipFuncSetAttribute((const void *)lz4_seq_kernel<R, S>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((lz4_seq_kernel<R, S>), dim3(B.nblocks), dim3(64), lds, s, B);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_lz4_seq(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s) {
+    if (B.nblocks == 0) return hipSuccess;
+    switch (ring_kib) {
+        case 8: return launch_seq<8192, 2048>(B, s);
+        default: return launch_seq<4096, 4096>(B, s);
+    }
+}
+
+}  // namespace hh

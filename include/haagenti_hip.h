@@ -95,6 +95,30 @@ void hh_context_destroy(hh_context *ctx);
 void *hh_context_stream(hh_context *ctx);
 int32_t hh_context_synchronize(hh_context *ctx);
 
+/* Context settings for diagnostics and tests; no counterpart in the
+ * reference (whose GPU contexts have no tunables).  HH_OPT_LZ4_DECODER
+ * selects the LZ4 block decoder of every batched LZ4 launch made through the
+ * context (hh_lz4_decoder).  The default, HH_LZ4_AUTO, takes the
+ * one-sequence ring decoder (4 KiB ring) for hh_lz4_decompress_batch and the
+ * layer entries, whose blocks carry few long runs, and the sequence-batched
+ * decoder for hh_pipeline_submit, whose streamed layers of low retention
+ * carry many short ones.  HH_OPT_FUSED_POLL_LIMIT bounds every wait of
+ * the fused layer decode to that many polls (1 .. 2^24; 0 restores 2^24),
+ * so a test can drive the path taken when a wait runs out.  Returns
+ * HH_ERR_INVALID_ARGUMENT for an unknown option or value. */
+typedef enum hh_option { HH_OPT_LZ4_DECODER = 1, HH_OPT_FUSED_POLL_LIMIT = 2 } hh_option;
+typedef enum hh_lz4_decoder {
+    HH_LZ4_AUTO = 0,   /* per entry point, as above */
+    HH_LZ4_SEQ = 1,    /* sequences parsed in batches, copies lane-parallel; 4 KiB ring */
+    HH_LZ4_SEQ8 = 2,   /* the same with an 8 KiB ring */
+    HH_LZ4_RING4 = 3,  /* one sequence at a time through a 4 KiB LDS ring */
+    HH_LZ4_RING8 = 4,
+    HH_LZ4_RING16 = 5,
+    HH_LZ4_RING32 = 6,
+    HH_LZ4_WINDOW = 7  /* one sequence at a time, global -> global */
+} hh_lz4_decoder;
+int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value);
+
 /* Streaming device-to-device copy of `bytes` bytes (non-overlapping ranges):
  * no counterpart in the reference; it is the bandwidth calibration of this
  * library's measurements (the rate a kernel that reads and writes every byte

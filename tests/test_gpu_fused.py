@@ -329,8 +329,8 @@ def test_per_tensor_tiles_per_block():
     assert (fs[0].cpu().numpy()[bad * tpb[0]:(bad + 1) * tpb[0]] == Hm.CORRUPTED_DATA).all()
 
 
-def test_bounded_waits_give_up_cleanly(monkeypatch):
-    # every wait of the fused kernel gives up after HH_FUSED_SPIN_LIMIT polls
+def test_bounded_waits_give_up_cleanly():
+    # every wait of the fused kernel gives up after the context's poll limit
     # (normally 2^24; here 1, so the waits at the start of each workgroup's
     # run, before its first block's bytes are decoded, run out): the waves
     # leave through the workgroup's abort word, the records of the blocks
@@ -340,14 +340,16 @@ def test_bounded_waits_give_up_cleanly(monkeypatch):
     k = Hm.hctt_retain_count(0.3)
     tpb = 13
     L = encode_fixed(Hm, [("a", 1024, 1024), ("b", 512, 2048)], [k, k], seed=81, tpb=tpb)
-    monkeypatch.setenv("HH_FUSED_SPIN_LIMIT", "1")
-    _, st, _ = fused(L, Hm.F32, tpb)
+    G.ctx().set_option(Hm.OPT_FUSED_POLL_LIMIT, 1)
+    try:
+        _, st, _ = fused(L, Hm.F32, tpb)
+    finally:
+        G.ctx().set_option(Hm.OPT_FUSED_POLL_LIMIT, 0)
     codes = st["code"]
     print(f"[fused] spin limit 1: {int((codes == Hm.DEVICE).sum())} of {codes.size} block records HH_ERR_DEVICE",
           flush=True)
     assert set(np.unique(codes).tolist()) <= {Hm.OK, Hm.DEVICE}
     assert (codes == Hm.DEVICE).any()
-    monkeypatch.delenv("HH_FUSED_SPIN_LIMIT")
     fo, st, fs = fused(L, Hm.F32, tpb)
     assert (st["code"] == 0).all()
     assert all((s.cpu().numpy() == 0).all() for s in fs)

@@ -9,16 +9,19 @@ import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
 
-# Every test runs on each decoder the batched entry point can dispatch to:
-# the LDS-ring decoder with its 4 (default), 8, 16 and 32 KiB rings, and the
-# register-window decoder.
-KERNELS = ["ring4", "ring8", "ring16", "ring32", "window"]
+# Every test runs on each decoder the batched entry point can dispatch to
+# (the context's HH_OPT_LZ4_DECODER): the sequence-batched decoder with its
+# 4 and 8 KiB rings, the one-sequence LDS-ring decoder with its 4 (the
+# entry point's default), 8, 16 and 32 KiB rings, and the register-window
+# decoder.
+KERNELS = ["seq", "seq8", "ring4", "ring8", "ring16", "ring32", "window"]
 
 
 @pytest.fixture(autouse=True, params=KERNELS)
-def lz4_kernel(request, monkeypatch):
-    monkeypatch.setenv("HH_LZ4_KERNEL", request.param)
-    return request.param
+def lz4_kernel(request):
+    G.ctx().set_lz4_decoder(request.param)
+    yield request.param
+    G.ctx().set_lz4_decoder("auto")
 
 
 def gpu_batch(streams, caps, in_pad=0, out_pad=0, in_align=0, out_align=0):
