@@ -285,7 +285,7 @@ int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_
 
 // ---------------------------------------------------------------- HCT-T
 
-static int32_t check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
+int32_t hh::check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
     if (T.rows % 64 || T.cols % 64 || T.cols > (1u << 24) || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
     const size_t nt = (size_t)(T.rows / 64) * (T.cols / 64);
     *ntiles = nt;
@@ -303,7 +303,7 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
     size_t total = 0;
     for (uint32_t i = 0; i < n; i++) {
         size_t nt = 0;
-        int32_t rc = check_hctt_tensor(tensors[i], &nt);
+        int32_t rc = hh::check_hctt_tensor(tensors[i], &nt);
         if (rc != HH_OK) return rc;
         total += nt;
     }

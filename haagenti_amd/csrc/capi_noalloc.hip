@@ -73,6 +73,20 @@ int32_t hh_hctt_decode_lz4_batch_noalloc(hh_context *ctx, const uint8_t *d_in, s
     if (guard.status() != hipSuccess) return hh::from_hip(guard.status());
     if (ctx->noalloc_status != hipSuccess) return hh::from_hip(ctx->noalloc_status);
     uint8_t *base = ctx->noalloc_scratch;
+    // every tensor is checked before anything is enqueued
+    {
+        uint64_t off = 0, ntiles = 0;
+        for (uint32_t i = 0; i < ntensors; i++) {
+            hh_hctt_tensor t = tensors[i];
+            t.d_tiles = base + off;
+            size_t nt = 0;
+            const int32_t rc = hh::check_hctt_tensor(t, &nt);
+            if (rc != HH_OK) return rc;
+            off += t.tiles_len;
+            ntiles += nt;
+        }
+        if (ntiles > 0xffffffffull) return HH_ERR_UNSUPPORTED;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (nblocks) {
         // blocks writing outside the packed tile bytes are reported, not run

@@ -46,6 +46,10 @@ struct hh_context {
 
 namespace hh {
 
+// Checks of one tensor of the tile decode (capi.hip): rows and cols
+// multiples of 64 (cols at most 2^24), 1 <= k <= 4096, tile bytes for every
+// tile, d_tiles set and d_out 16-byte aligned; *ntiles its tile count.
+int32_t check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles);
 // hipError_t -> hh_status; grows ctx->d_scratch to at least `bytes`
 // (capi.hip).
 int32_t from_hip(hipError_t e);

@@ -496,13 +496,22 @@ int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, co
         lz4_out = p->d_tiles;
         lz4_cap = p->d_tiles ? p->cfg.tile_scratch_size : 0;
     }
-    uint64_t tiles_total = 0, out_bytes = 0;
+    uint64_t tiles_total = 0, out_bytes = 0, ntiles_total = 0;
     for (uint32_t i = 0; i < ntensors; i++) {
         if (tensors[i].d_tiles != nullptr) return HH_ERR_INVALID_ARGUMENT;
         if (tensors[i].tiles_len > lz4_cap - tiles_total) return HH_ERR_BUFFER_TOO_SMALL;
+        // the tile decode's own checks, made before anything is enqueued
+        // (its d_tiles points into the LZ4 output once enqueued)
+        hh_hctt_tensor t = tensors[i];
+        t.d_tiles = lz4_out ? lz4_out + tiles_total : nullptr;
+        size_t nt = 0;
+        const int32_t trc = hh::check_hctt_tensor(t, &nt);
+        if (trc != HH_OK) return trc;
+        ntiles_total += nt;
         tiles_total += tensors[i].tiles_len;
         out_bytes += (uint64_t)tensors[i].rows * tensors[i].cols * elem_bytes(out_dtype);
     }
+    if (ntiles_total > 0xffffffffull) return HH_ERR_UNSUPPORTED;
     if (nblocks && !lz4_out) return HH_ERR_INVALID_ARGUMENT;
     hh::DeviceGuard guard(p->ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());

@@ -143,6 +143,9 @@ class DecompressionPipeline:
         _check(_lib.hh_pipeline_create(ctx.handle, pool.handle if pool is not None else None, C.byref(cfg),
                                        C.byref(p)), "hh_pipeline_create")
         self._p, self.ctx, self.config, self._pool = p, ctx, cfg, pool
+        # host arrays of submitted units, kept alive until the unit is waited
+        # for: page-locked input is copied to the device from where it lies
+        self._inflight = {}
 
     @property
     def streams(self):
@@ -178,6 +181,7 @@ class DecompressionPipeline:
                                        il.ctypes.data, oo.ctypes.data, oc.ctypes.data, n, _addr(lz4_out),
                                        int(lz4_out_cap), arr, len(tensors), int(dtype), ev, C.byref(tk)),
                "hh_pipeline_submit")
+        self._inflight[tk.value] = data
         return tk.value
 
     def wait(self, ticket):
@@ -186,6 +190,8 @@ class DecompressionPipeline:
         block failed."""
         st, fb = BlockStatus(), C.c_int64(-1)
         rc = _lib.hh_pipeline_wait(self._p, int(ticket), C.byref(st), C.byref(fb))
+        for t in [t for t in self._inflight if t <= int(ticket)]:
+            del self._inflight[t]   # units complete in order
         if rc != OK:
             e = HaagentiError(rc, f"unit {ticket} block {fb.value}", st)
             e.block = fb.value
@@ -203,6 +209,7 @@ class DecompressionPipeline:
         """DecompressionPipeline::finish (pipeline.rs:262-269)."""
         st, fb, ft = BlockStatus(), C.c_int64(-1), C.c_uint64(0)
         rc = _lib.hh_pipeline_finish(self._p, C.byref(st), C.byref(fb), C.byref(ft))
+        self._inflight.clear()
         if rc != OK:
             e = HaagentiError(rc, f"unit {ft.value} block {fb.value}", st)
             e.block, e.ticket = fb.value, ft.value

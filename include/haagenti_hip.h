@@ -385,7 +385,16 @@ int32_t hh_pipeline_next_staging(hh_pipeline *p, uint8_t **h_ptr, size_t *cap);
  * hh_hctt_decode_batch does.  after_event (a hipEvent_t, or NULL) delays
  * the decode until it completes (e.g. the consumer of the tensors' output
  * slot is done with it).  The host blocks only while the staging slot's
- * previous unit completes.  *ticket names the unit. */
+ * previous unit completes.  *ticket names the unit.
+ * Lifetime of h_data: pageable memory is copied into the slot's staging
+ * buffer before the call returns, so the caller may reuse it at once.
+ * Page-locked memory (hh_pinned_alloc, hipHostMalloc, a pinned torch
+ * tensor) is copied to the device from where it lies, with no host copy:
+ * it must stay allocated and unchanged until the unit has been waited for
+ * (hh_pipeline_wait / hh_pipeline_finish) or its stream event passed
+ * (hh_pipeline_stream_wait).  Every tensor is checked (shape, k, tile
+ * bytes, output alignment) before anything is enqueued; an invalid one
+ * fails the call with nothing enqueued. */
 int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, const uint64_t *h_in_off,
                            const uint32_t *h_in_len, const uint64_t *h_out_off, const uint32_t *h_out_cap,
                            uint32_t nblocks, uint8_t *d_lz4_out, uint64_t lz4_out_cap,

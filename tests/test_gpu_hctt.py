@@ -148,3 +148,33 @@ def test_config3_8192x8192_vs_oracle():
     e_out = (got.astype(np.float64) ** 2).reshape(128, 64, 128, 64).sum(axis=(1, 3))
     e_ref = (ref.astype(np.float64) ** 2).reshape(128, 64, 128, 64).sum(axis=(1, 3))
     assert np.abs(e_out - e_ref).max() <= 1e-4 * e_ref.max()
+
+
+def test_tile_with_infinite_scale_matches_the_oracle():
+    # A constant tile of 1e5 has a DC coefficient of 6.4e6, so its first
+    # 32-block's scale max/7 truncates to an infinite f16
+    # (quantization.rs:136-163); the reference then dequantizes that block
+    # to inf (7 x inf) and nan (0 x inf, its other coefficients) and its
+    # inverse DCT spreads nan over the tile.  The GPU decode must agree:
+    # the same tile status and the same non-finite pattern, with the finite
+    # tiles around it within tolerance.
+    import haagenti_amd as H
+    rows, cols, k = 128, 128, 1228
+    rng = np.random.default_rng(71)
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    w[0:64, 64:128] = 1e5
+    tiles = H.hctt_encode(w, k)
+    tb = O.hctt_tile_bytes(k)
+    scales = np.frombuffer(bytes(tiles[tb + 512:tb + 514]), np.uint16)
+    assert scales[0] == 0x7C00  # +inf
+    rc, ref = O.hctt_decode_tensor(tiles, rows, cols, k)
+    assert rc == O.OK
+    got, st = decode_gpu(tiles, rows, cols, k, status=True)
+    assert (st == 0).all()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    rms = np.sqrt((ref[fin].astype(np.float64) ** 2).mean())
+    assert np.abs(got[fin] - ref[fin]).max() <= TOL * rms
+    assert not fin[0:64, 64:128].any()   # the oracle's tile is all nan

@@ -216,6 +216,23 @@ def test_pipeline_pageable_and_in_place_staging_and_errors():
         pipe.finish()
     assert ei.value.block == bad
     pipe.finish()                                            # nothing pending any more
+    # an invalid tensor (rows not a multiple of 64) fails the submit before
+    # anything is enqueued; the slot is reused by the next unit as if the
+    # call had not happened
+    outs = [T.full((r * c,), 3.0, dtype=T.float32, device="cuda") for _, r, c in shapes]
+    desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o) for t, o in zip(L["tensors"], outs)]
+    bad_desc = list(desc)
+    bad_desc[1] = (L["tensors"][1]["tiles"].size, 65, 256, 410, outs[1])
+    with pytest.raises(Hm.HaagentiError) as ei:
+        pipe.submit(L["blob"].copy(), *_layer_tables(L), tensors=bad_desc, dtype=Hm.F32)
+    assert ei.value.code == Hm.INVALID_ARGUMENT
+    G.sync()
+    assert all((o.cpu().numpy() == 3.0).all() for o in outs)   # nothing ran
+    tk5 = pipe.submit(L["blob"].copy(), *_layer_tables(L), tensors=desc, dtype=Hm.F32)
+    pipe.wait(tk5)
+    for o, t, ref in zip(outs, L["tensors"], refs):
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.abs(o.cpu().numpy().reshape(t["rows"], t["cols"]) - ref).max() <= TOL * rms
     pipe.close()
 
 

@@ -110,3 +110,35 @@ def test_noalloc_rejects_oversized_and_misplaced_inputs():
     inside = (L["out_off"] + L["out_cap"]) <= t0["tiles"].size
     assert inside.any() and (~inside).any()
     assert (codes[inside] == Hm.OK).all() and (codes[~inside] == Hm.INVALID_ARGUMENT).all()
+
+
+def test_noalloc_call_allocates_no_device_memory():
+    # The entry point's defining property: a call, even the first on a
+    # fresh context, leaves the device's free memory unchanged (kernels are
+    # loaded first through the shared context; loading code objects is the
+    # runtime's, once per process).
+    Hm = H()
+    T = G.torch()
+    L = small_layer(Hm, seed=34)
+    d_in, d_off, d_len, d_oo, d_oc = tables(L)
+    n = L["in_off"].size
+    outs = [T.empty(t["rows"] * t["cols"], dtype=T.float32, device="cuda") for t in L["tensors"]]
+    desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o) for t, o in zip(L["tensors"], outs)]
+    status = T.zeros(n * 32, dtype=T.uint8, device="cuda")
+    assert G.ctx().hctt_decode_lz4_batch_noalloc(d_in, d_in.numel(), d_off, d_len, d_oo, d_oc, n, status, desc,
+                                                 dtype=Hm.F32, stream=G.stream()) == Hm.OK
+    G.sync()
+    ctx = Hm.HipContext(0)
+    try:
+        G.sync()
+        free0 = T.cuda.mem_get_info()[0]
+        rc = ctx.hctt_decode_lz4_batch_noalloc(d_in, d_in.numel(), d_off, d_len, d_oo, d_oc, n, status, desc,
+                                               dtype=Hm.F32, stream=G.stream())
+        G.sync()
+        free1 = T.cuda.mem_get_info()[0]
+        print(f"[noalloc] free device memory before {free0} after {free1}", flush=True)
+        assert rc == Hm.OK
+        assert free1 == free0
+        assert (status.cpu().numpy().view(np.int32)[0::8] == 0).all()
+    finally:
+        ctx.close()
