@@ -89,6 +89,18 @@ void build_basis_table(void *buf) {
 
 }  // namespace hh
 
+namespace hh {
+int32_t check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
+    if (T.rows % 64 || T.cols % 64 || T.cols > (1u << 24) || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
+    const size_t nt = (size_t)(T.rows / 64) * (T.cols / 64);
+    *ntiles = nt;
+    if (nt == 0) return HH_OK;
+    if (T.tiles_len < nt * hh_hctt_tile_bytes(T.k)) return HH_ERR_UNEXPECTED_EOF;
+    if (!T.d_tiles || !T.d_out || ((uintptr_t)T.d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
+    return HH_OK;
+}
+}  // namespace hh
+
 extern "C" {
 
 const char *hh_status_category(int32_t code) {
@@ -194,10 +206,10 @@ int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value) {
 
 // ---------------------------------------------------------------- LZ4
 
-int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
-                                const uint64_t *d_in_off, const uint32_t *d_in_len, uint8_t *d_out,
-                                const uint64_t *d_out_off, const uint32_t *d_out_cap,
-                                uint32_t nblocks, hh_block_status *d_status, void *stream) {
+static int32_t lz4_batch_with(hh_context *ctx, int32_t decoder, const uint8_t *d_in, size_t in_total,
+                              const uint64_t *d_in_off, const uint32_t *d_in_len, uint8_t *d_out,
+                              const uint64_t *d_out_off, const uint32_t *d_out_cap, uint32_t nblocks,
+                              hh_block_status *d_status, void *stream) {
     if (!ctx) return HH_ERR_INVALID_ARGUMENT;
     if (nblocks == 0) return HH_OK;
     if (!d_in || !d_in_off || !d_in_len || !d_out || !d_out_off || !d_out_cap || !d_status)
@@ -208,7 +220,16 @@ int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_
     // the caller's output buffer has no stated size: its block table is trusted
     const hh::Lz4Batch B = {d_in,      in_total,  d_in_off, d_in_len, d_out, ~0ull,
                             d_out_off, d_out_cap, nblocks,  d_status};
-    return from_hip(hh::launch_lz4_batch(B, hh::lz4_decoder_for(ctx, HH_LZ4_RING4), pick_stream(ctx, stream)));
+    return from_hip(hh::launch_lz4_batch(B, decoder, pick_stream(ctx, stream)));
+}
+
+int32_t hh_lz4_decompress_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
+                                const uint64_t *d_in_off, const uint32_t *d_in_len, uint8_t *d_out,
+                                const uint64_t *d_out_off, const uint32_t *d_out_cap,
+                                uint32_t nblocks, hh_block_status *d_status, void *stream) {
+    if (!ctx) return HH_ERR_INVALID_ARGUMENT;
+    return lz4_batch_with(ctx, hh::lz4_decoder_for(ctx, HH_LZ4_RING4), d_in, in_total, d_in_off, d_in_len, d_out,
+                          d_out_off, d_out_cap, nblocks, d_status, stream);
 }
 
 int32_t hh_lz4_decompress_to(hh_context *ctx, const uint8_t *in, size_t in_len, uint8_t *out,
@@ -285,16 +306,6 @@ int32_t hh_dequant_int4(hh_context *ctx, const uint8_t *d_q, size_t q_len, size_
 
 // ---------------------------------------------------------------- HCT-T
 
-int32_t hh::check_hctt_tensor(const hh_hctt_tensor &T, size_t *ntiles) {
-    if (T.rows % 64 || T.cols % 64 || T.cols > (1u << 24) || T.k < 1 || T.k > 4096) return HH_ERR_INVALID_ARGUMENT;
-    const size_t nt = (size_t)(T.rows / 64) * (T.cols / 64);
-    *ntiles = nt;
-    if (nt == 0) return HH_OK;
-    if (T.tiles_len < nt * hh_hctt_tile_bytes(T.k)) return HH_ERR_UNEXPECTED_EOF;
-    if (!T.d_tiles || !T.d_out || ((uintptr_t)T.d_out & 15u)) return HH_ERR_INVALID_ARGUMENT;
-    return HH_OK;
-}
-
 int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uint32_t n,
                              int32_t out_dtype, void *stream) {
     if (!ctx || (!tensors && n)) return HH_ERR_INVALID_ARGUMENT;
@@ -323,8 +334,9 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
                                  void *stream) {
     // both launches on the caller's stream: the tile decode reads the
     // scratch after every block has been written
-    int32_t rc = hh_lz4_decompress_batch(ctx, d_in, in_total, d_in_off, d_in_len, d_scratch, d_out_off, d_out_cap,
-                                         nblocks, d_status, stream);
+    if (!ctx || (!tensors && ntensors)) return HH_ERR_INVALID_ARGUMENT;
+    int32_t rc = lz4_batch_with(ctx, hh::lz4_decoder_for_tiles(ctx, tensors, ntensors), d_in, in_total, d_in_off,
+                                d_in_len, d_scratch, d_out_off, d_out_cap, nblocks, d_status, stream);
     if (rc != HH_OK) return rc;
     return hh_hctt_decode_batch(ctx, tensors, ntensors, out_dtype, stream);
 }
@@ -356,7 +368,9 @@ int32_t hh_hctt_decode_lz4_fused_tpb(hh_context *ctx, const uint8_t *d_in, size_
     if (guard.status() != hipSuccess) return from_hip(guard.status());
     return from_hip(hh::launch_hctt_lz4_fused(tensors, ntensors, tiles_per_block, d_in, in_total, d_in_off,
                                               d_in_len, d_status, out_dtype, ctx->d_basis, ctx->num_cus,
-                                              ctx->fused_poll_limit, pick_stream(ctx, stream)));
+                                              ctx->fused_poll_limit,
+                                              hh::lz4_decoder_for_tiles(ctx, tensors, ntensors) == HH_LZ4_SEQ,
+                                              pick_stream(ctx, stream)));
 }
 
 int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total, const uint64_t *d_in_off,

@@ -49,6 +49,7 @@
 
 #include "hh_internal.hpp"
 #include "lz4_ring.hpp"
+#include "lz4_seq.hpp"
 
 namespace hh {
 namespace {
@@ -675,9 +676,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
 // which leaves the rest of the LDS to three block buffers.
 constexpr uint32_t kFusedStageData = 8 * 1024;
 using FusedRing = ring::RingDec<16384, kFusedStageData, true>;
+using FusedSeq = seq::SeqDec<16384, kFusedStageData, true>;
 constexpr uint32_t kFusedMax = 16384 - 32;
 constexpr uint32_t kFusedBuf = 16384;  // a block buffer: the decoder's ring
-constexpr uint32_t kFusedStage = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;  // a decoder's input stage
+// a decoder's input stage (the sequence-batched decoder's run table after it)
+constexpr uint32_t kFusedStageRing = FusedRing::kSFront + kFusedStageData + FusedRing::kSPad;
+constexpr uint32_t kFusedStageSeq = FusedSeq::kStageLds + FusedSeq::kTabLds;
+constexpr uint32_t kFusedStage = kFusedStageRing > kFusedStageSeq ? kFusedStageRing : kFusedStageSeq;
+static_assert(FusedRing::kSFront == FusedSeq::kSFront, "both decoders' stages start at the same offset");
 constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's budget
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
@@ -756,7 +762,9 @@ __device__ __forceinline__ bool fused_poll(uint32_t w, int lane, uint32_t limit,
     }
 }
 
-template <int DT>
+// SEQ: the blocks are decoded by the sequence-batched decoder
+// (lz4_seq.hpp) instead of the one-sequence ring decoder (lz4_ring.hpp).
+template <int DT, bool SEQ>
 __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(TileBatch Bk, FusedBlocks Fk,
                                                                               const u32x4 *__restrict__ basis) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -804,9 +812,10 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     auto bit_m = [&](uint32_t q) { return 1u << (q & 31u); };
     // Every wave leaves through here: its stores complete, it counts itself
     // out, and the last one out, if a wait gave up (the abort word), writes
-    // HH_ERR_DEVICE into every block record of the workgroup (any of its
-    // tiles may be undecoded); the other waves' records are complete by then,
-    // so none overwrites it.
+    // HH_ERR_DEVICE into every block record and every tile status of the
+    // workgroup's blocks (any of its tiles may be undecoded); the other
+    // waves' records and statuses are complete by then, so none overwrites
+    // it.
     auto leave = [&]() {
         const int l = opaque_lane();
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -826,6 +835,13 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 st.required = 0;
                 st.written = 0;
                 ((hh_block_status *)Fk.status)[Fk.blk_base + lb_of(q)] = st;
+            }
+            for (uint32_t q = 0; q < Q; q++) {
+                uint32_t ti, t0, nt;
+                locate(lb_of(q), ti, t0, nt);
+                int32_t *ts = B.status[ti];
+                if (ts != nullptr)
+                    for (uint32_t j = (uint32_t)l; j < nt; j += 64u) ts[t0 + j] = HH_ERR_DEVICE;
             }
         }
     };
@@ -891,9 +907,18 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         uint64_t pos = 0, req = 0;
         const uint64_t ioff = Fk.in_off[gb];
         const uint32_t ilen = Fk.in_len[gb];
-        FusedRing d;
-        d.ring = rbuf;
-        d.stage = stage;
+        using Dec = typename std::conditional<SEQ, FusedSeq, FusedRing>::type;
+        Dec d;
+        if constexpr (SEQ) {
+            d.ring = (seq::lds8 *)(size_t)(Fk.buf_off + x * kFusedBuf);
+            d.stage = (seq::lds8 *)(size_t)(wbase + FusedSeq::kSFront);
+            d.tab = (seq::lds32 *)(size_t)(wbase + FusedSeq::kStageLds);
+        } else {
+            d.ring = rbuf;
+            d.stage = stage;
+            d.wso = ring::kNoWin;
+            d.w = 0;
+        }
         d.gbuf = Fk.in;
         d.gsz = Fk.in_total;
         d.ioff = ioff;
@@ -902,8 +927,6 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         d.cap = cap;
         d.sb = 0;
         d.at_end = false;
-        d.wso = ring::kNoWin;
-        d.w = 0;
         d.op = 0;
         d.fl = 0;
         d.lane = ln;
@@ -924,7 +947,10 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         if (ioff > Fk.in_total || (uint64_t)ilen > Fk.in_total - ioff) {
             code = HH_ERR_INVALID_ARGUMENT;
         } else {
-            ring::parse_block(d, ilen, code, detail, pos, req, false, publish);
+            if constexpr (SEQ)
+                seq::decode_block(d, ilen, code, detail, pos, req, false, publish);
+            else
+                ring::parse_block(d, ilen, code, detail, pos, req, false, publish);
         }
         // a complete block: the bytes it did not produce read as zeros; a
         // failed one: zeros from its first tile not released (released
@@ -1173,7 +1199,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
 hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
-                                 uint32_t poll_limit, hipStream_t s) {
+                                 uint32_t poll_limit, bool seq_decoder, hipStream_t s) {
     uint32_t blk = 0;  // global block number of the next tensor's first block
     for (uint32_t i = 0; i < n;) {
         TileBatch B;
@@ -1240,18 +1266,27 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
         if ((nb + grid - 1) / grid > kFusedMaxRange) grid = (nb + kFusedMaxRange - 1) / kFusedMaxRange;
         const u32x4 *basis = reinterpret_cast<const u32x4 *>(d_basis);
         hipError_t e = hipSuccess;
-#define HH_LAUNCH_FUSED(DTV)                                                                                \
+#define HH_LAUNCH_FUSED(DTV, SQ)                                                                            \
     do {                                                                                                    \
-        e = hipFuncSetAttribute((const void *)hctt_lz4_fused_kernel<DTV>,                                   \
+        e = hipFuncSetAttribute((const void *)hctt_lz4_fused_kernel<DTV, SQ>,                               \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
         if (e != hipSuccess) return e;                                                                      \
-        hipLaunchKernelGGL((hctt_lz4_fused_kernel<DTV>), dim3(grid), dim3(threads), lds, s, B, F, basis);       \
+        hipLaunchKernelGGL((hctt_lz4_fused_kernel<DTV, SQ>), dim3(grid), dim3(threads), lds, s, B, F, basis);   \
     } while (0)
-        switch (dtype) {
-            case HH_F32: HH_LAUNCH_FUSED(HH_F32); break;
-            case HH_F16: HH_LAUNCH_FUSED(HH_F16); break;
-            case HH_BF16: HH_LAUNCH_FUSED(HH_BF16); break;
-            default: return hipErrorInvalidValue;
+        if (seq_decoder) {
+            switch (dtype) {
+                case HH_F32: HH_LAUNCH_FUSED(HH_F32, true); break;
+                case HH_F16: HH_LAUNCH_FUSED(HH_F16, true); break;
+                case HH_BF16: HH_LAUNCH_FUSED(HH_BF16, true); break;
+                default: return hipErrorInvalidValue;
+            }
+        } else {
+            switch (dtype) {
+                case HH_F32: HH_LAUNCH_FUSED(HH_F32, false); break;
+                case HH_F16: HH_LAUNCH_FUSED(HH_F16, false); break;
+                case HH_BF16: HH_LAUNCH_FUSED(HH_BF16, false); break;
+                default: return hipErrorInvalidValue;
+            }
         }
 #undef HH_LAUNCH_FUSED
         e = hipGetLastError();

@@ -171,6 +171,16 @@ hipError_t launch_lz4_batch(const Lz4Batch &B, int32_t decoder, hipStream_t s);
 inline int32_t lz4_decoder_for(const hh_context *ctx, int32_t dflt) {
     return ctx->lz4_decoder == HH_LZ4_AUTO ? dflt : ctx->lz4_decoder;
 }
+// The automatic decoder of a launch whose LZ4 blocks hold the tiles of
+// these tensors: tiles of retention below 25 % (k < 1024) compress into
+// blocks of many short LZ4 sequences (runs of the sparse bitmaps), which the
+// sequence-batched decoder copies many at a time; denser tiles leave a few
+// long runs per block, which the one-sequence ring decoder copies faster.
+inline int32_t lz4_decoder_for_tiles(const hh_context *ctx, const hh_hctt_tensor *tensors, uint32_t n) {
+    bool sparse = false;
+    for (uint32_t i = 0; i < n; i++) sparse = sparse || tensors[i].k < 1024u;
+    return lz4_decoder_for(ctx, sparse ? HH_LZ4_SEQ : HH_LZ4_RING4);
+}
 hipError_t launch_lz4_seq(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s);
 hipError_t launch_lz4_ring(const Lz4Batch &B, uint32_t ring_kib, hipStream_t s);
 
@@ -277,11 +287,13 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
 // launch per 8 tensors (hctt_decode.hip; validated by the caller: tensor i's
 // blocks are the next ceil(ntiles_i / tpb[i]) of d_in_off / d_in_len, each
 // tpb[i] * tile bytes <= fused_block_max()).
-// poll_limit: polls before a wait gives up (0: the default 2^24).
+// poll_limit: polls before a wait gives up (0: the default 2^24);
+// seq_decoder: blocks decoded by the sequence-batched decoder (else the
+// one-sequence ring decoder).
 hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, const uint32_t *tpb, const uint8_t *d_in,
                                  uint64_t in_total, const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  hh_block_status *d_status, int dtype, const void *d_basis, int num_cus,
-                                 uint32_t poll_limit, hipStream_t s);
+                                 uint32_t poll_limit, bool seq_decoder, hipStream_t s);
 uint32_t fused_block_max();
 
 }  // namespace hh

@@ -193,9 +193,12 @@ struct SeqDec {
             *reinterpret_cast<ldsx4 *>(stage + 16 * (lane + 64 * i)) = v[i];
         wave_sync();
     }
-    // Starts the load of the stage after the current one.
+    // Starts the load of the stage after the current one.  Not in LDS mode,
+    // whose caller runs other waves beside this one to hide the loads (and
+    // needs the registers).
+    static constexpr bool kPrefetch = !LDS;
     __device__ __forceinline__ void prefetch() {
-        pf_on = !at_end;
+        pf_on = kPrefetch && !at_end;
         if (pf_on) {
             pf = sb + S - 64u;
             load_stage(pf, pv);
@@ -204,12 +207,19 @@ struct SeqDec {
     // Makes the stage hold input position x: from the prefetched stage when
     // it holds x with at least 1 KiB after it, else loaded now.
     __device__ __forceinline__ void restage(uint32_t x) {
-        if (!(pf_on && x - pf <= S - 1024u)) {
-            pf = x - (uint32_t)((uintptr_t)(gbuf + ioff + x) & 15u);
-            load_stage(pf, pv);
+        if constexpr (kPrefetch) {
+            if (!(pf_on && x - pf <= S - 1024u)) {
+                pf = x - (uint32_t)((uintptr_t)(gbuf + ioff + x) & 15u);
+                load_stage(pf, pv);
+            }
+            put_stage(pf, pv);
+            prefetch();
+        } else {
+            const uint32_t s0 = x - (uint32_t)((uintptr_t)(gbuf + ioff + x) & 15u);
+            u32x4 v[S / 1024];
+            load_stage(s0, v);
+            put_stage(s0, v);
         }
-        put_stage(pf, pv);
-        prefetch();
     }
     // [x, x + 8) is in the stage (or the stage reaches the end of the buffer)
     __device__ __forceinline__ bool in_stage8(uint32_t x) const { return at_end || x - sb <= S - 8; }

@@ -570,7 +570,7 @@ int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, co
                                 reinterpret_cast<const uint32_t *>(t + 20 * (size_t)nblocks),
                                 nblocks,
                                 s.d_status};
-        e = hh::launch_lz4_batch(B, hh::lz4_decoder_for(p->ctx, HH_LZ4_SEQ), p->compute);
+        e = hh::launch_lz4_batch(B, hh::lz4_decoder_for_tiles(p->ctx, tensors, ntensors), p->compute);
         if (e != hipSuccess) return from_hip(e);
     }
     hh_hctt_tensor local[8];

@@ -98,11 +98,14 @@ int32_t hh_context_synchronize(hh_context *ctx);
 /* Context settings for diagnostics and tests; no counterpart in the
  * reference (whose GPU contexts have no tunables).  HH_OPT_LZ4_DECODER
  * selects the LZ4 block decoder of every batched LZ4 launch made through the
- * context (hh_lz4_decoder).  The default, HH_LZ4_AUTO, takes the
- * one-sequence ring decoder (4 KiB ring) for hh_lz4_decompress_batch and the
- * layer entries, whose blocks carry few long runs, and the sequence-batched
- * decoder for hh_pipeline_submit, whose streamed layers of low retention
- * carry many short ones.  HH_OPT_FUSED_POLL_LIMIT bounds every wait of
+ * context (hh_lz4_decoder), and the block decoder of the fused layer entries
+ * (HH_LZ4_SEQ or one of the ring decoders, which decode there into LDS).
+ * The default, HH_LZ4_AUTO, takes the one-sequence ring decoder (4 KiB
+ * ring) for hh_lz4_decompress_batch, and for the layer entries (two-launch,
+ * fused, no-alloc, hh_pipeline_submit) the sequence-batched decoder when a
+ * tensor of the call has k < 1024 (retention below 25 %: its tiles compress
+ * into blocks of many short LZ4 sequences) and the ring decoder otherwise
+ * (denser tiles leave a few long runs per block).  HH_OPT_FUSED_POLL_LIMIT bounds every wait of
  * the fused layer decode to that many polls (1 .. 2^24; 0 restores 2^24),
  * so a test can drive the path taken when a wait runs out.  Returns
  * HH_ERR_INVALID_ARGUMENT for an unknown option or value. */
@@ -253,7 +256,11 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
  * output.  Asynchronous on the stream.  One persistent workgroup per CU
  * takes every G-th block (G workgroups) and its tiles: each of its waves in
  * turn decodes the next of those blocks into an LDS block buffer (when one
- * is free) or the next of their tiles from the buffers. */
+ * is free) or the next of their tiles from the buffers.  Every wait between
+ * the waves is bounded (HH_OPT_FUSED_POLL_LIMIT polls); when one runs out,
+ * every block record and every tile status of that workgroup's blocks
+ * report HH_ERR_DEVICE and those tiles' outputs are unspecified (the
+ * kernel still ends; the next call decodes normally). */
 #define HH_FUSED_BLOCK_BYTES 16352u
 int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total,
                                  const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,

@@ -22,6 +22,16 @@ from test_gpu_llama_layers import check_against_oracle, decode
 pytestmark = pytest.mark.gpu
 
 
+# Every test runs with each block decoder the fused kernel can use (the
+# context's HH_OPT_LZ4_DECODER): the one-sequence ring decoder (the fused
+# entry's default) and the sequence-batched decoder.
+@pytest.fixture(autouse=True, params=["ring4", "seq"])
+def lz4_decoder(request):
+    G.ctx().set_lz4_decoder(request.param)
+    yield request.param
+    G.ctx().set_lz4_decoder("auto")
+
+
 def H():
     import haagenti_amd as h
     return h
@@ -331,18 +341,20 @@ def test_per_tensor_tiles_per_block():
 
 def test_bounded_waits_give_up_cleanly():
     # every wait of the fused kernel gives up after the context's poll limit
-    # (normally 2^24; here 1, so the waits at the start of each workgroup's
-    # run, before its first block's bytes are decoded, run out): the waves
-    # leave through the workgroup's abort word, the records of the blocks
-    # waited on report HH_ERR_DEVICE (the others keep what the buffer held),
-    # the kernel ends, and the next call decodes normally
+    # (normally 2^24; here 1, so the waits at the start of a workgroup's run,
+    # before its first block's bytes are decoded, run out): the waves leave
+    # through the workgroup's abort word, and every block record and tile
+    # status of a workgroup that gave up reports HH_ERR_DEVICE (workgroup g
+    # of G holds blocks g, g + G, ...; a workgroup that never waited long
+    # enough decodes as usual); the kernel ends, and the next call decodes
+    # normally
     Hm = H()
     k = Hm.hctt_retain_count(0.3)
     tpb = 13
     L = encode_fixed(Hm, [("a", 1024, 1024), ("b", 512, 2048)], [k, k], seed=81, tpb=tpb)
     G.ctx().set_option(Hm.OPT_FUSED_POLL_LIMIT, 1)
     try:
-        _, st, _ = fused(L, Hm.F32, tpb)
+        _, st, fs = fused(L, Hm.F32, tpb)
     finally:
         G.ctx().set_option(Hm.OPT_FUSED_POLL_LIMIT, 0)
     codes = st["code"]
@@ -350,6 +362,20 @@ def test_bounded_waits_give_up_cleanly():
           flush=True)
     assert set(np.unique(codes).tolist()) <= {Hm.OK, Hm.DEVICE}
     assert (codes == Hm.DEVICE).any()
+    nb = codes.size
+    grid = min(G.torch().cuda.get_device_properties(0).multi_processor_count, nb)
+    for g in range(grid):
+        assert len(set(codes[g::grid].tolist())) == 1   # a workgroup's blocks all alike
+    # each block's tiles report what its record reports
+    blk = 0
+    for t, s in zip(L["tensors"], fs):
+        s = s.cpu().numpy()
+        ntiles = (t["rows"] // 64) * (t["cols"] // 64)
+        for j in range(0, ntiles, tpb):
+            want = Hm.DEVICE if codes[blk] == Hm.DEVICE else 0
+            assert (s[j:j + tpb] == want).all()
+            blk += 1
+    assert blk == nb
     fo, st, fs = fused(L, Hm.F32, tpb)
     assert (st["code"] == 0).all()
     assert all((s.cpu().numpy() == 0).all() for s in fs)
