@@ -767,6 +767,44 @@ void hho_idct_2d(const float *in, float *out, size_t width, size_t height) {
     free(co);
 }
 
+/* hho_idct_2d on nthreads threads: the same 1-D transforms (columns
+ * first, then rows), each independent, so the result is bit-identical. */
+typedef struct {
+    const float *in;
+    float *tmp, *out;
+    size_t w, h, nchunk;
+    int pass;
+} idct2_mt_ctx;
+
+static void idct2_mt_task(void *vctx, size_t c) {
+    idct2_mt_ctx *t = (idct2_mt_ctx *)vctx;
+    if (t->pass == 0) {
+        const size_t x0 = c * t->w / t->nchunk, x1 = (c + 1) * t->w / t->nchunk;
+        float *cb = (float *)malloc(sizeof(float) * t->h);
+        float *co = (float *)malloc(sizeof(float) * t->h);
+        for (size_t x = x0; x < x1; x++) {
+            for (size_t y = 0; y < t->h; y++) cb[y] = t->in[y * t->w + x];
+            hho_idct_1d(cb, co, t->h);
+            for (size_t y = 0; y < t->h; y++) t->tmp[y * t->w + x] = co[y];
+        }
+        free(cb);
+        free(co);
+    } else {
+        const size_t y0 = c * t->h / t->nchunk, y1 = (c + 1) * t->h / t->nchunk;
+        for (size_t y = y0; y < y1; y++) hho_idct_1d(t->tmp + y * t->w, t->out + y * t->w, t->w);
+    }
+}
+
+void hho_idct_2d_mt(const float *in, float *out, size_t width, size_t height, int nthreads) {
+    idct2_mt_ctx t = {in, (float *)malloc(sizeof(float) * width * height), out, width, height, 0, 0};
+    t.nchunk = 256;
+    t.pass = 0;
+    hho_parallel_for(t.nchunk, nthreads, idct2_mt_task, &t);
+    t.pass = 1;
+    hho_parallel_for(t.nchunk, nthreads, idct2_mt_task, &t);
+    free(t.tmp);
+}
+
 /* :342-361 */
 void hho_dct_1d_f64(const double *in, double *out, size_t n) {
     if (n == 0) return;

@@ -104,6 +104,8 @@ void hho_idct_1d(const float *in, float *out, size_t n);       /* :154-259 */
 void hho_idct_1d_direct(const float *in, float *out, size_t n);/* :263-277 */
 void hho_dct_2d(const float *in, float *out, size_t width, size_t height);  /* :282-308 */
 void hho_idct_2d(const float *in, float *out, size_t width, size_t height); /* :311-337 */
+/* hho_idct_2d on nthreads threads (0: all cores), bit-identical. */
+void hho_idct_2d_mt(const float *in, float *out, size_t width, size_t height, int nthreads);
 void hho_dct_1d_f64(const double *in, double *out, size_t n);  /* :342-361 */
 void hho_idct_1d_f64(const double *in, double *out, size_t n); /* :364-383 */
 void hho_dct_2d_f64(const double *in, double *out, size_t w, size_t h);  /* :386-412 */

@@ -108,6 +108,8 @@ def lib():
         L.hho_f32_to_f16_rne.argtypes = [C.c_float]
         L.hho_hct3_coefficients.restype = C.c_int
         L.hho_hct3_coefficients.argtypes = [u8p, sz, sz, f32p]
+        L.hho_idct_2d_mt.restype = None
+        L.hho_idct_2d_mt.argtypes = [f32p, f32p, sz, sz, C.c_int]
         L.hho_hct3_decode.restype = C.c_int
         L.hho_hct3_decode.argtypes = [u8p, sz, u8p, sz, f32p]
         L.hho_spectral_encode_from_dct.restype = sz
@@ -262,6 +264,14 @@ def idct_2d(x):
 
 def dct_2d_f64(x):
     return _call2d("hho_dct_2d_f64", x, np.float64)
+
+
+def idct_2d_mt(x, nthreads=0):
+    """idct_2d on all host threads (bit-identical to idct_2d)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().hho_idct_2d_mt(_p(x), _p(out), x.shape[1], x.shape[0], int(nthreads))
+    return out
 
 
 def idct_2d_f64(x):

@@ -386,3 +386,37 @@ def test_decompress_batch_pipelined_matches_decompress():
     for (c, shp), o in zip(items, outs):
         assert rel_err(o, dec().decompress(c, shp)) <= 1e-5
         assert rel_err(o, O.hct3_decode(c, shp)[1]) <= TOL
+
+
+def _real_size(rows, cols, seed):
+    # one fragment at the turbo pipeline's 20 % retention: the GPU decode
+    # (direct plane scatter + even / odd split products at these sizes)
+    # against the oracle's bit-exact scatter and f32 idct_2d (the same 1-D
+    # transforms as hct3_decode, run on every host thread)
+    rng = np.random.default_rng(seed)
+    total = rows * cols
+    data = container([random_fragment(rng, total, 0.2)])
+    print(f"[hct3] {rows} x {cols}: {len(data)} container bytes", flush=True)
+    got = dec().decompress_to_gpu(data, (rows, cols), stream=G.stream()).cpu().numpy()
+    rc, coef = O.hct3_coefficients(data, total)
+    assert rc == O.OK
+    ref = O.idct_2d_mt(coef.reshape(rows, cols)).ravel()
+    del coef
+    err = rel_err(got, ref)
+    print(f"[hct3] {rows} x {cols}: max|gpu - oracle| = {err:.2e} x RMS", flush=True)
+    assert err <= TOL
+    return data, got
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192)])
+def test_decompress_real_sizes_vs_oracle(rows, cols):
+    data, got = _real_size(rows, cols, seed=rows // 64)
+    if rows == 8192:
+        T = G.torch()
+        b16 = dec().decompress_to_gpu(data, (rows, cols), dtype=H().BF16).view(T.int16).cpu().numpy()
+        assert np.array_equal(b16.view(np.uint16), G.bf16_bits(got))
+
+
+def test_decompress_llama70b_mlp_tensor_vs_oracle():
+    # a 28672 x 8192 tensor (the Llama-70B gate / up projection's shape)
+    _real_size(28672, 8192, seed=28672)
