@@ -1,9 +1,13 @@
 // Streaming device copy: the HBM bandwidth calibration of the measurements
 // (the rate a kernel that reads and writes each byte once can reach, and the
-// scale of the FETCH_SIZE / WRITE_SIZE counters).  Each thread of a
-// grid-stride loop moves four 16-byte chunks per iteration, all four loads
-// issued before the stores; the bytes before the first 16-aligned source
-// address and after the last whole chunk are copied one by one.
+// scale of the FETCH_SIZE / WRITE_SIZE counters).  Each workgroup copies one
+// contiguous 16 KiB piece: each of its 256 threads moves four 16-byte chunks
+// (a wave's 1 KiB apart), all four non-temporal loads issued before the
+// stores.  Contiguous pieces per workgroup keep each wave's accesses in few
+// DRAM pages; a grid-stride loop over the whole buffer (each thread's chunks
+// a grid apart) measured 20-30 % slower.  The bytes before the first
+// 16-aligned source address and after the last whole chunk are copied one by
+// one.
 #include "hh_internal.hpp"
 
 namespace hh {
@@ -15,16 +19,18 @@ constexpr int kUnroll = 4;
 
 __global__ __launch_bounds__(kThreads) void copy16_kernel(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst,
                                                           uint64_t n16) {
-    const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-    uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
-        u32x4 v[kUnroll];
+    const uint64_t base = (uint64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    u32x4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = __builtin_nontemporal_load(src + i + u * stride);
-#pragma unroll
-        for (int u = 0; u < kUnroll; u++) __builtin_nontemporal_store(v[u], dst + i + u * stride);
+    for (int u = 0; u < kUnroll; u++) {
+        const uint64_t j = base + (uint64_t)u * kThreads;
+        if (j < n16) v[u] = __builtin_nontemporal_load(src + j);
     }
-    for (; i < n16; i += stride) dst[i] = src[i];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const uint64_t j = base + (uint64_t)u * kThreads;
+        if (j < n16) __builtin_nontemporal_store(v[u], dst + j);
+    }
 }
 
 __global__ void copy_bytes_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, uint64_t n) {
@@ -53,13 +59,17 @@ int32_t hh_hbm_copy(hh_context *ctx, void *d_dst, const void *d_src, uint64_t by
     if (head)
         hipLaunchKernelGGL(hh::copy_bytes_kernel, dim3((uint32_t)((head + 255) / 256)), dim3(256), 0, s, s8, d8,
                            head);
-    if (n16) {
-        const uint32_t cus = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
-        uint64_t grid = (n16 + hh::kThreads * hh::kUnroll - 1) / (hh::kThreads * hh::kUnroll);
-        if (grid > 4ull * cus) grid = 4ull * cus;
+    // one workgroup per 16 KiB piece, launches of at most 2^31 - 1 pieces
+    const uint64_t piece = (uint64_t)hh::kThreads * hh::kUnroll;
+    for (uint64_t done = 0; done < n16;) {
+        uint64_t n = n16 - done;
+        const uint64_t max_n = 0x7fffffffull * piece;
+        if (n > max_n) n = max_n;
+        const uint64_t grid = (n + piece - 1) / piece;
         hipLaunchKernelGGL(hh::copy16_kernel, dim3((uint32_t)grid), dim3(hh::kThreads), 0, s,
-                           reinterpret_cast<const hh::u32x4 *>(s8 + head), reinterpret_cast<hh::u32x4 *>(d8 + head),
-                           n16);
+                           reinterpret_cast<const hh::u32x4 *>(s8 + head) + done,
+                           reinterpret_cast<hh::u32x4 *>(d8 + head) + done, n);
+        done += n;
     }
     if (tail)
         hipLaunchKernelGGL(hh::copy_bytes_kernel, dim3((uint32_t)((tail + 255) / 256)), dim3(256), 0, s,
