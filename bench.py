@@ -176,6 +176,7 @@ LZ4_KERNEL_NAMES = {"auto": "lz4_ring_kernel<4096, 4096>", "seq": "lz4_seq_kerne
 def new_ctx(H, args):
     ctx = H.HipContext(0)
     ctx.set_lz4_decoder(args.lz4_decoder)
+    ctx.set_dct_route(args.dct_route)
     return ctx
 
 
@@ -657,20 +658,36 @@ def wl_hct3(args, torch, H, O):
     torch.cuda.synchronize()
     ms_step = T.mean_s() * 1e3 / args.steps
     per = ms_step / 1e3
-    flop = 4.0 * n ** 3          # the two dense n x n x n products of the transform
-    achieved = flop / per / 1e12
-    peak = 2500.0
-    roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
-            "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA on the even / odd split of the "
-                       "cosine bases: half-depth products, 2 + 3 passes, f32 accumulation; + butterfly, "
-                       "bitmap scatter and the amax / scale passes)"),
-            "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
-            "mfma_type": "f16", "mfma_flop_per_launch": 5 * n ** 3}
-    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, "f16-split-mfma/f32",
+    if args.dct_route != "dense":
+        # the FFT route (the default at this size): bound by HBM; algorithmic
+        # bytes = the container read once + the bf16 output written once
+        alg = len(data) + n * n * 2
+        achieved = alg / per / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(achieved / 8000.0, 4), "traffic": traffic_for("hct3-4096-fft"),
+                "kernel": ("bitmap scatter into an f32 matrix + dct_fft_rows_kernel x2 (Makhoul rows over an "
+                           "f32 Stockham FFT in LDS) + transpose_kernel x2 (the second converting to bf16)"),
+                "avg_launch_us": round(per * 1e6, 1), "algorithmic_bytes_per_launch": alg,
+                # scatter write, two row passes and the first transpose (read + write each), the last
+                # transpose's f32 read and bf16 write
+                "f32_matrix_passes_bytes": 4 * n * n * 8 + 2 * n * n}
+        dt = "f32-fft"
+    else:
+        flop = 4.0 * n ** 3          # the two dense n x n x n products of the transform
+        achieved = flop / per / 1e12
+        peak = 2500.0
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
+                "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA on the even / odd split of the "
+                           "cosine bases: half-depth products, 2 + 3 passes, f32 accumulation; + butterfly, "
+                           "bitmap scatter and the amax / scale passes)"),
+                "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
+                "mfma_type": "f16", "mfma_flop_per_launch": 5 * n ** 3}
+        dt = "f16-split-mfma/f32"
+    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, dt,
                 "synthetic (4096x4096 N(0,0.02), torch seed 17, turbo defaults)",
                 {"rows": n, "cols": n, "retention": 0.20, "coefficients": int(keep),
-                 "container_bytes": len(data), "out_dtype": "bf16"}, roof, cpu,
+                 "container_bytes": len(data), "out_dtype": "bf16", "dct_route": args.dct_route}, roof, cpu,
                 {"spot_check_max_err_over_rms": check})
 
 
@@ -963,6 +980,8 @@ def main():
     ap.add_argument("--path", choices=["fused", "two-launch"], default="fused",
                     help="llama3-8b-layer: one fused LZ4 + tile launch per layer (hh_hctt_decode_lz4_fused) "
                          "or the LZ4 and tile launches through a scratch buffer (hh_hctt_decode_lz4_batch)")
+    ap.add_argument("--dct-route", default="auto", choices=["auto", "dense", "fft"],
+                    help="whole-matrix transform route of hct3-4096 (the context's HH_OPT_DCT_ROUTE)")
     ap.add_argument("--lz4-decoder", default="auto", choices=sorted(LZ4_KERNEL_NAMES),
                     help="LZ4 block decoder of the batched LZ4 launches (the context's HH_OPT_LZ4_DECODER)")
     ap.add_argument("--lz4-block", type=int, default=16384,

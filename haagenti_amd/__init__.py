@@ -44,9 +44,11 @@ CORRUPT_BITMAP_COUNT = 3
 
 F32, F16, BF16 = 0, 1, 2
 
-# hh_context_set_option options and LZ4 decoders (diagnostics and tests)
-OPT_LZ4_DECODER, OPT_FUSED_POLL_LIMIT = 1, 2
+# hh_context_set_option options, LZ4 decoders and whole-matrix transform
+# routes (diagnostics and tests)
+OPT_LZ4_DECODER, OPT_FUSED_POLL_LIMIT, OPT_DCT_ROUTE = 1, 2, 3
 LZ4_DECODERS = {"auto": 0, "seq": 1, "seq8": 2, "ring4": 3, "ring8": 4, "ring16": 5, "ring32": 6, "window": 7}
+DCT_ROUTES = {"auto": 0, "dense": 1, "fft": 2}
 
 
 class BlockStatus(C.Structure):
@@ -351,12 +353,18 @@ class HipContext:
         _check(_lib.hh_context_synchronize(self._p))
 
     def set_option(self, option, value):
-        """hh_context_set_option: OPT_LZ4_DECODER (a value of LZ4_DECODERS) or
-        OPT_FUSED_POLL_LIMIT (polls per wait of the fused decode, 0 = default)."""
+        """hh_context_set_option: OPT_LZ4_DECODER (a value of LZ4_DECODERS),
+        OPT_FUSED_POLL_LIMIT (polls per wait of the fused decode, 0 = default)
+        or OPT_DCT_ROUTE (a value of DCT_ROUTES)."""
         _check(_lib.hh_context_set_option(self._p, int(option), int(value)), "hh_context_set_option")
 
     def set_lz4_decoder(self, name):
         self.set_option(OPT_LZ4_DECODER, LZ4_DECODERS[name])
+
+    def set_dct_route(self, name):
+        """Whole-matrix transform route: "auto" (the FFT route when both sides
+        allow it and the larger is at least 1024), "dense" or "fft"."""
+        self.set_option(OPT_DCT_ROUTE, DCT_ROUTES[name])
 
     def close(self):
         if getattr(self, "_p", None):

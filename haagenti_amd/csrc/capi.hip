@@ -178,6 +178,7 @@ void hh_context_destroy(hh_context *ctx) {
     if (ctx->d_basis) (void)hipFree(ctx->d_basis);
     if (ctx->d_scratch) (void)hipFree(ctx->d_scratch);
     hh::release_dct_resources(ctx);
+    hh::release_fft_resources(ctx);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -199,6 +200,10 @@ int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value) {
         case HH_OPT_FUSED_POLL_LIMIT:
             if (value < 0 || value > (1 << 24)) return HH_ERR_INVALID_ARGUMENT;
             ctx->fused_poll_limit = (uint32_t)value;
+            return HH_OK;
+        case HH_OPT_DCT_ROUTE:
+            if (value < HH_DCT_AUTO || value > HH_DCT_FFT) return HH_ERR_INVALID_ARGUMENT;
+            ctx->dct_route = (int32_t)value;
             return HH_OK;
         default: return HH_ERR_INVALID_ARGUMENT;
     }

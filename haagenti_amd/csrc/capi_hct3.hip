@@ -475,13 +475,20 @@ int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t c
     if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
     hh::DeviceGuard guard(ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (hh::use_fft(ctx, rows, cols) &&
+        (reinterpret_cast<uintptr_t>(d_out) & (out_dtype == HH_F32 ? 15u : 7u)) == 0) {
+        float *a, *b;
+        int32_t rc = hh::fft_scratch(ctx, total, s, &a, &b);
+        if (rc != HH_OK) return rc;
+        return hh::dct2d_fft(ctx, true, d_in, a, b, rows, cols, out_dtype, d_out, s);
+    }
     const size_t mat = align16((size_t)total * sizeof(float));
     int32_t rc = ensure_scratch(ctx, out_dtype == HH_F32 ? mat : 2 * mat);
     if (rc != HH_OK) return rc;
     float *d_tmp = reinterpret_cast<float *>(ctx->d_scratch);
     float *x = out_dtype == HH_F32 ? reinterpret_cast<float *>(d_out)
                                    : reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->d_scratch) + mat);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     rc = hh::dct2d_full(ctx, true, d_in, d_tmp, x, rows, cols, s);
     if (rc == HH_OK && out_dtype != HH_F32) rc = from_hip(hh::launch_f32_convert(x, total, out_dtype, d_out, s));
     return rc;
@@ -495,10 +502,16 @@ int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t co
     if (!d_in || !d_out || d_in == d_out) return HH_ERR_INVALID_ARGUMENT;
     hh::DeviceGuard guard(ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (hh::use_fft(ctx, rows, cols) && ((reinterpret_cast<uintptr_t>(d_out) | reinterpret_cast<uintptr_t>(d_in)) & 15u) == 0) {
+        float *a, *b;
+        int32_t rc = hh::fft_scratch(ctx, total, s, &a, &b);
+        if (rc != HH_OK) return rc;
+        return hh::dct2d_fft(ctx, false, d_in, a, b, rows, cols, HH_F32, d_out, s);
+    }
     int32_t rc = ensure_scratch(ctx, align16((size_t)total * sizeof(float)));
     if (rc != HH_OK) return rc;
-    return hh::dct2d_full(ctx, false, d_in, reinterpret_cast<float *>(ctx->d_scratch), d_out, rows, cols,
-                          reinterpret_cast<hipStream_t>(stream));
+    return hh::dct2d_full(ctx, false, d_in, reinterpret_cast<float *>(ctx->d_scratch), d_out, rows, cols, s);
 }
 
 size_t hh_spectral_encoded_size(uint32_t width, uint32_t height, uint16_t num_fragments, float retention,

@@ -1,0 +1,561 @@
+// Whole-matrix DCT-II / DCT-III (orthonormal) in O(n^2 log n): a 1-D
+// transform along every row, a transpose, the 1-D transform along every
+// row of the transposed matrix, and a transpose back (converted to the
+// output type on the way).
+//
+// 1-D transform of a row of length N (N even), by Makhoul's reordering
+// (J. Makhoul, "A fast cosine transform in one and two dimensions", IEEE
+// Trans. ASSP 28(1), 1980) and the usual packing of a real sequence of
+// length N into a complex one of length L = N / 2:
+//   forward  v[m] = x[2m], v[N-1-m] = x[2m+1];  z[j] = v[2j] + i v[2j+1];
+//            Z = DFT_L(z);  V[k] = E_k - i w_N^-k O_k with
+//            E_k = (Z[k] + conj Z[L-k]) / 2, O_k = (Z[k] - conj Z[L-k]) / 2;
+//            X[k] = s_k Re(w_4N^-k V[k]), X[N-k] = -s_{N-k} Im(w_4N^-k V[k])
+//   inverse  c = s X;  H[0] = c[0], H[k] = w_4N^k (c[k] - i c[N-k]) / 2;
+//            Z[k] = (H[k] + H[k+L]) + i w_N^k (H[k] - H[k+L]);
+//            z = unnormalised inverse DFT_L(Z);  v[2j] = Re z[j],
+//            v[2j+1] = Im z[j];  x[2m] = v[m], x[2m+1] = v[N-1-m]
+// with w_n = e^(2 pi i / n), s_0 = sqrt(1/N), s_k = sqrt(2/N).  The complex
+// DFT of length L runs in LDS as a Stockham autosort FFT (radix 8, 4, 2, 3,
+// 5, 7 passes; each pass reads all its butterflies' inputs into registers,
+// then writes the outputs in place), one workgroup per row, with f32
+// arithmetic and twiddles rounded from double.
+//
+// The reference's whole-matrix transforms switch to an FFT above 4096
+// (haagenti-cuda/src/dct_gpu.rs:1081,1381-1412, via cufft_ffi.rs:423-506);
+// its CPU path is the same Makhoul construction (haagenti-core/src/
+// dct.rs:154-259).
+#include "hh_internal.hpp"
+
+namespace hh {
+namespace {
+
+constexpr uint32_t kMaxLds = 160u * 1024u;
+
+struct FftRows {
+    const float *in;
+    float *out;
+    const float2 *roots;  // e^(+2 pi i t / L), t in [0, L)
+    const float2 *w4;     // e^(+i pi k / (2N)), k in [0, 2N)
+    uint32_t N, L;
+    uint32_t nr;
+    uint8_t r[16];
+};
+
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+// i^S a for S = +1 (INV) or -1
+template <bool INV>
+__device__ __forceinline__ float2 rot90(float2 a) {
+    return INV ? make_float2(-a.y, a.x) : make_float2(a.y, -a.x);
+}
+
+// In-register DFT of length R with e^(+-2 pi i / R) (+ for INV).
+template <int R, bool INV>
+struct Dft;
+
+template <bool INV>
+struct Dft<2, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        const float2 a = x[0], b = x[1];
+        x[0] = cadd(a, b);
+        x[1] = csub(a, b);
+    }
+};
+
+template <bool INV>
+struct Dft<4, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        const float2 t0 = cadd(x[0], x[2]), t1 = csub(x[0], x[2]);
+        const float2 t2 = cadd(x[1], x[3]), t3 = rot90<INV>(csub(x[1], x[3]));
+        x[0] = cadd(t0, t2);
+        x[2] = csub(t0, t2);
+        x[1] = cadd(t1, t3);
+        x[3] = csub(t1, t3);
+    }
+};
+
+template <bool INV>
+struct Dft<8, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        float2 e[4] = {x[0], x[2], x[4], x[6]};
+        float2 o[4] = {x[1], x[3], x[5], x[7]};
+        Dft<4, INV>::run(e);
+        Dft<4, INV>::run(o);
+        constexpr float h = 7.071067812e-01f;  // 1 / sqrt(2)
+        // o[q] *= w_8^(+-q)
+        o[1] = INV ? make_float2(h * (o[1].x - o[1].y), h * (o[1].x + o[1].y))
+                   : make_float2(h * (o[1].x + o[1].y), h * (o[1].y - o[1].x));
+        o[2] = rot90<INV>(o[2]);
+        o[3] = INV ? make_float2(-h * (o[3].x + o[3].y), h * (o[3].x - o[3].y))
+                   : make_float2(h * (o[3].y - o[3].x), -h * (o[3].x + o[3].y));
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            x[q] = cadd(e[q], o[q]);
+            x[q + 4] = csub(e[q], o[q]);
+        }
+    }
+};
+
+template <bool INV>
+struct Dft<3, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        constexpr float s3 = 8.660254038e-01f;  // sin(2 pi / 3)
+        const float2 t = cadd(x[1], x[2]);
+        const float2 u = rot90<INV>(csub(x[1], x[2]));
+        const float2 m = make_float2(x[0].x - 0.5f * t.x, x[0].y - 0.5f * t.y);
+        x[0] = cadd(x[0], t);
+        x[1] = make_float2(m.x + s3 * u.x, m.y + s3 * u.y);
+        x[2] = make_float2(m.x - s3 * u.x, m.y - s3 * u.y);
+    }
+};
+
+// odd R: y_q = x_0 + sum_m a_m cos(2 pi m q / R) +- i sum_m b_m sin(2 pi m q / R)
+// over m = 1 .. (R-1)/2 with a_m = x_m + x_{R-m}, b_m = x_m - x_{R-m}
+template <int R, bool INV>
+__device__ __forceinline__ void dft_odd(float2 *x, const float *c, const float *sn) {
+    constexpr int H = (R - 1) / 2;
+    float2 a[H], b[H];
+#pragma unroll
+    for (int m = 1; m <= H; m++) {
+        a[m - 1] = cadd(x[m], x[R - m]);
+        b[m - 1] = rot90<INV>(csub(x[m], x[R - m]));
+    }
+    float2 y[R];
+    y[0] = x[0];
+#pragma unroll
+    for (int m = 0; m < H; m++) y[0] = cadd(y[0], a[m]);
+#pragma unroll
+    for (int q = 1; q <= H; q++) {
+        float2 re = x[0], im = make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int m = 1; m <= H; m++) {
+            const int j = (m * q) % R;  // cos / sin of 2 pi j / R, j in [1, R)
+            const float cj = j <= H ? c[j - 1] : c[R - j - 1];
+            const float sj = j <= H ? sn[j - 1] : -sn[R - j - 1];
+            re = make_float2(re.x + cj * a[m - 1].x, re.y + cj * a[m - 1].y);
+            im = make_float2(im.x + sj * b[m - 1].x, im.y + sj * b[m - 1].y);
+        }
+        y[q] = cadd(re, im);
+        y[R - q] = csub(re, im);
+    }
+#pragma unroll
+    for (int q = 0; q < R; q++) x[q] = y[q];
+}
+
+template <bool INV>
+struct Dft<5, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        constexpr float c[2] = {3.090169944e-01f, -8.090169944e-01f};
+        constexpr float sn[2] = {9.510565163e-01f, 5.877852523e-01f};
+        dft_odd<5, INV>(x, c, sn);
+    }
+};
+
+template <bool INV>
+struct Dft<7, INV> {
+    __device__ __forceinline__ static void run(float2 *x) {
+        constexpr float c[3] = {6.234898019e-01f, -2.225209340e-01f, -9.009688679e-01f};
+        constexpr float sn[3] = {7.818314825e-01f, 9.749279122e-01f, 4.338837391e-01f};
+        dft_odd<7, INV>(x, c, sn);
+    }
+};
+
+// One Stockham pass of radix R over the L points in LDS, p = the product
+// of the earlier passes' radices: butterfly i (of L / R) takes points
+// i + j L/R, multiplies point j by w_L^(+-j k L/(p R)) with k = i mod p
+// (an exponent below L), transforms, and writes output j to
+// (i - k) R + k + j p.  All inputs are read before the barrier, so the
+// pass runs in place.
+template <int R, int MAXB, bool INV>
+__device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, const float2 *__restrict__ roots) {
+    // the twiddles are loaded with the pass's LDS reads, before the barrier,
+    // where the registers allow (roots[0] is exactly 1: no branch for k = 0)
+    constexpr bool kPre = MAXB * (R - 1) <= 16;
+    const uint32_t T = blockDim.x, tid = threadIdx.x;
+    const uint32_t nb = L / R;
+    const uint32_t stride = L / (p * R);
+    float2 x[MAXB][R];
+    float2 w[kPre ? MAXB : 1][R - 1];
+#pragma unroll
+    for (int b = 0; b < MAXB; b++) {
+        const uint32_t i = tid + b * T;
+        if (i < nb) {
+#pragma unroll
+            for (int j = 0; j < R; j++) x[b][j] = buf[i + j * nb];
+            if (kPre) {
+                const uint32_t t = (i % p) * stride;
+#pragma unroll
+                for (int j = 1; j < R; j++) w[kPre ? b : 0][j - 1] = roots[j * t];
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < MAXB; b++) {
+        const uint32_t i = tid + b * T;
+        if (i < nb) {
+            const uint32_t k = i % p;
+            const uint32_t t = k * stride;
+#pragma unroll
+            for (int j = 1; j < R; j++) {
+                float2 tw = kPre ? w[kPre ? b : 0][j - 1] : roots[j * t];
+                if (!INV) tw.y = -tw.y;
+                x[b][j] = cmul(x[b][j], tw);
+            }
+            Dft<R, INV>::run(x[b]);
+            const uint32_t base = (i - k) * R + k;
+#pragma unroll
+            for (int j = 0; j < R; j++) buf[base + j * p] = x[b][j];
+        }
+    }
+    __syncthreads();
+}
+
+template <bool INV, int MAXB>
+__global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
+    extern __shared__ float2 buf[];
+    const uint32_t N = P.N, L = P.L, T = blockDim.x, tid = threadIdx.x;
+    const float *__restrict__ in = P.in + (uint64_t)blockIdx.x * N;
+    float *__restrict__ out = P.out + (uint64_t)blockIdx.x * N;
+    const float2 *__restrict__ w4 = P.w4;
+    const float s0 = sqrtf(1.0f / (float)N), s1 = sqrtf(2.0f / (float)N);
+    // the row's loads are issued kB per thread at a time, before any use
+    constexpr int kB = 4;
+    if (INV) {
+        // Z[k] and Z[L-k] from c[k], c[N-k], c[k+L], c[L-k] for 0 < k < L/2;
+        // k = 0's thread also makes Z[0] (from c[0], c[L]) and the
+        // self-paired Z[L/2] (from c[L/2], c[3L/2])
+        for (uint32_t k0 = 0; k0 < L / 2; k0 += kB * T) {
+            float a[kB], b[kB], d[kB], e[kB];
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const uint32_t k = k0 + tid + u * T;
+                if (k < L / 2) {
+                    a[u] = in[k];
+                    b[u] = in[k == 0 ? 3 * L / 2 : N - k];
+                    d[u] = in[k + L];
+                    e[u] = in[k == 0 ? L / 2 : L - k];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const uint32_t k = k0 + tid + u * T;
+                if (k >= L / 2) continue;
+                const float au = a[u] * (k == 0 ? s0 : s1), bu = b[u] * s1, du = d[u] * s1, eu = e[u] * s1;
+                if (k == 0) {
+                    const float2 h0 = make_float2(au, 0.0f);
+                    const float2 hl = cmul(w4[L], make_float2(0.5f * du, -0.5f * du));
+                    buf[0] = cadd(cadd(h0, hl), rot90<true>(csub(h0, hl)));
+                    const float2 hm = cmul(w4[L / 2], make_float2(0.5f * eu, -0.5f * bu));
+                    const float2 hml = cmul(w4[3 * L / 2], make_float2(0.5f * bu, -0.5f * eu));
+                    buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(w4[N], csub(hm, hml))));
+                    continue;
+                }
+                const float2 hk = cmul(w4[k], make_float2(0.5f * au, -0.5f * bu));
+                const float2 hkl = cmul(w4[k + L], make_float2(0.5f * du, -0.5f * eu));
+                buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(w4[4 * k], csub(hk, hkl))));
+                const uint32_t k2 = L - k;
+                const float2 h2 = cmul(w4[k2], make_float2(0.5f * eu, -0.5f * du));
+                const float2 h2l = cmul(w4[N - k], make_float2(0.5f * bu, -0.5f * au));
+                buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(w4[4 * k2], csub(h2, h2l))));
+            }
+        }
+    } else {
+        // z[q] = x[4q] + i x[4q+2], z[L-1-q] = x[4q+3] + i x[4q+1]
+        const float4 *in4 = reinterpret_cast<const float4 *>(in);
+        for (uint32_t q0 = 0; q0 < L / 2; q0 += kB * T) {
+            float4 v[kB];
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const uint32_t q = q0 + tid + u * T;
+                if (q < L / 2) v[u] = in4[q];
+            }
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const uint32_t q = q0 + tid + u * T;
+                if (q < L / 2) {
+                    buf[q] = make_float2(v[u].x, v[u].z);
+                    buf[L - 1 - q] = make_float2(v[u].w, v[u].y);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t p = 1;
+    for (uint32_t q = 0; q < P.nr; q++) {
+        switch (P.r[q]) {
+            case 8: fft_pass<8, MAXB, INV>(buf, L, p, P.roots); break;
+            case 4: fft_pass<4, MAXB, INV>(buf, L, p, P.roots); break;
+            case 2: fft_pass<2, MAXB, INV>(buf, L, p, P.roots); break;
+            case 3: fft_pass<3, MAXB, INV>(buf, L, p, P.roots); break;
+            case 5: fft_pass<5, MAXB, INV>(buf, L, p, P.roots); break;
+            default: fft_pass<7, MAXB, INV>(buf, L, p, P.roots); break;
+        }
+        p *= P.r[q];
+    }
+    if (INV) {
+        // x[4q .. 4q+3] = Re z[q], Im z[L-1-q], Im z[q], Re z[L-1-q]
+        float4 *out4 = reinterpret_cast<float4 *>(out);
+        for (uint32_t q = tid; q < L / 2; q += T) {
+            const float2 za = buf[q], zb = buf[L - 1 - q];
+            out4[q] = make_float4(za.x, zb.y, za.y, zb.x);
+        }
+    } else {
+        // X[k], X[N-k] from V[k], for k and L - k
+        for (uint32_t k = tid; k <= L / 2; k += T) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t kk = h == 0 ? k : L - k;
+                if (h == 1 && 2 * k == L) break;
+                const float2 zk = buf[kk == L ? 0 : kk];
+                const float2 zc = cconj(buf[kk == 0 ? 0 : L - kk]);
+                const float2 E = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y + zc.y));
+                const float2 D = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y - zc.y));
+                const float2 wn = kk == L ? make_float2(-1.0f, 0.0f) : cconj(w4[4 * kk]);
+                const float2 V = csub(E, rot90<true>(cmul(wn, D)));
+                const float2 W = cmul(cconj(w4[kk]), V);
+                out[kk] = (kk == 0 ? s0 : s1) * W.x;
+                if (kk != 0 && kk != L) out[N - kk] = -s1 * W.y;
+            }
+        }
+    }
+}
+
+// out (cols x rows) = transpose of in (rows x cols), both multiples of 64,
+// converted to OUT (HH_F32, HH_BF16 or HH_F16): 64 x 64 tiles through LDS.
+template <int OUT>
+__global__ __launch_bounds__(256) void transpose_kernel(const float *__restrict__ in, uint32_t rows, uint32_t cols,
+                                                         void *__restrict__ out) {
+    __shared__ float tile[64][65];
+    const uint32_t c0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = ty + 16 * i;
+        const float4 v = *reinterpret_cast<const float4 *>(in + (uint64_t)(r0 + r) * cols + c0 + 4 * tx);
+        tile[r][4 * tx + 0] = v.x;
+        tile[r][4 * tx + 1] = v.y;
+        tile[r][4 * tx + 2] = v.z;
+        tile[r][4 * tx + 3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = ty + 16 * i;
+        const float a = tile[4 * tx + 0][c], b = tile[4 * tx + 1][c];
+        const float d = tile[4 * tx + 2][c], e = tile[4 * tx + 3][c];
+        const uint64_t o = (uint64_t)(c0 + c) * rows + r0 + 4 * tx;
+        if (OUT == HH_F32) {
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + o) = make_float4(a, b, d, e);
+        } else {
+            auto cv = [](float v) { return OUT == HH_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v); };
+            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(out) + o) =
+                make_uint2(cv(a) | (cv(b) << 16), cv(d) | (cv(e) << 16));
+        }
+    }
+}
+
+// roots[t] = e^(2 pi i t / L) for t < L, then w4[k] = e^(i pi k / (2N)) for k < 2N
+__global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ tab, uint32_t L, uint32_t N) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= L + 2 * N) return;
+    double s, c;
+    if (i < L)
+        sincospi(2.0 * (double)i / (double)L, &s, &c);
+    else
+        sincospi((double)(i - L) / (2.0 * (double)N), &s, &c);
+    tab[i] = make_float2((float)c, (float)s);
+}
+
+struct Plan {
+    uint32_t N = 0, L = 0, threads = 0, maxb = 0, nr = 0;
+    uint8_t r[16] = {};
+};
+
+// Radices of L (8s, then 4 or 2, then 3, 5, 7), the workgroup size and
+// the butterflies per thread of the widest pass; false when N is not a
+// multiple of 64, L has another prime factor, L points do not fit in LDS
+// or a pass would need more than 4 butterflies per thread (more registers
+// than a 1024-thread workgroup has: the MAXB = 8 variant spilled).
+bool make_plan(uint32_t N, Plan &P) {
+    if (N == 0 || N % 64u != 0) return false;
+    const uint32_t L = N / 2;
+    if ((uint64_t)L * 8u > kMaxLds) return false;
+    uint32_t n = L, nr = 0;
+    uint8_t r[16];
+    while (n % 8 == 0) r[nr++] = 8, n /= 8;
+    if (n % 4 == 0) r[nr++] = 4, n /= 4;
+    if (n % 2 == 0) r[nr++] = 2, n /= 2;
+    for (uint32_t f : {3u, 5u, 7u})
+        while (n % f == 0 && nr < 16) r[nr++] = (uint8_t)f, n /= f;
+    if (n != 1) return false;
+    uint32_t T = (L / 8 + 63) / 64 * 64;
+    T = T < 64 ? 64 : T > 1024 ? 1024 : T;
+    uint32_t mb = 0;
+    for (uint32_t q = 0; q < nr; q++) {
+        const uint32_t b = (L / r[q] + T - 1) / T;
+        mb = b > mb ? b : mb;
+    }
+    if (mb > 4) return false;
+    P.N = N;
+    P.L = L;
+    P.threads = T;
+    P.maxb = mb <= 1 ? 1 : mb <= 2 ? 2 : 4;
+    P.nr = nr;
+    for (uint32_t q = 0; q < nr; q++) P.r[q] = r[q];
+    return true;
+}
+
+template <bool INV, int MAXB>
+hipError_t launch_rows_t(const FftRows &A, uint32_t rows, uint32_t threads, hipStream_t s) {
+    const uint32_t lds = A.L * 8u;
+    hipError_t e = hipFuncSetAttribute((const void *)dct_fft_rows_kernel<INV, MAXB>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((dct_fft_rows_kernel<INV, MAXB>), dim3(rows), dim3(threads), lds, s, A);
+    return hipGetLastError();
+}
+
+hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out, uint32_t rows,
+                       const float2 *tab, hipStream_t s) {
+    FftRows A;
+    A.in = in;
+    A.out = out;
+    A.roots = tab;
+    A.w4 = tab + P.L;
+    A.N = P.N;
+    A.L = P.L;
+    A.nr = P.nr;
+    for (int q = 0; q < 16; q++) A.r[q] = P.r[q];
+    switch (P.maxb | (inverse ? 16 : 0)) {
+        case 1: return launch_rows_t<false, 1>(A, rows, P.threads, s);
+        case 2: return launch_rows_t<false, 2>(A, rows, P.threads, s);
+        case 4: return launch_rows_t<false, 4>(A, rows, P.threads, s);
+        case 17: return launch_rows_t<true, 1>(A, rows, P.threads, s);
+        case 18: return launch_rows_t<true, 2>(A, rows, P.threads, s);
+        default: return launch_rows_t<true, 4>(A, rows, P.threads, s);
+    }
+}
+
+hipError_t launch_transpose(const float *in, uint32_t rows, uint32_t cols, int32_t dtype, void *out, hipStream_t s) {
+    const dim3 grid(cols / 64u, rows / 64u);
+    switch (dtype) {
+        case HH_BF16: hipLaunchKernelGGL(transpose_kernel<HH_BF16>, grid, dim3(256), 0, s, in, rows, cols, out); break;
+        case HH_F16: hipLaunchKernelGGL(transpose_kernel<HH_F16>, grid, dim3(256), 0, s, in, rows, cols, out); break;
+        default: hipLaunchKernelGGL(transpose_kernel<HH_F32>, grid, dim3(256), 0, s, in, rows, cols, out); break;
+    }
+    return hipGetLastError();
+}
+
+// The context's twiddle tables for length n (two cached, the older replaced).
+int32_t tables_for(hh_context *ctx, const Plan &P, hipStream_t s, const float2 **out) {
+    for (int i = 0; i < 2; i++) {
+        hh_context::FftTables &t = ctx->fft_tab[i];
+        if (t.tab && t.n == P.N) {
+            t.stamp = ++ctx->dct_stamp;
+            *out = reinterpret_cast<const float2 *>(t.tab);
+            return HH_OK;
+        }
+    }
+    const int v = !ctx->fft_tab[0].tab ? 0 : !ctx->fft_tab[1].tab ? 1
+                  : ctx->fft_tab[0].stamp <= ctx->fft_tab[1].stamp ? 0 : 1;
+    hh_context::FftTables &t = ctx->fft_tab[v];
+    if (t.tab) {
+        // the stream may still read the old table: wait before freeing
+        hipError_t e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = hipFree(t.tab);
+        t.tab = nullptr;
+        t.n = 0;
+        if (e != hipSuccess) return from_hip(e);
+    }
+    const uint32_t n = P.L + 2 * P.N;
+    hipError_t e = hipMalloc(&t.tab, (size_t)n * sizeof(float2));
+    if (e != hipSuccess) {
+        t.tab = nullptr;
+        return from_hip(e);
+    }
+    t.n = P.N;
+    t.stamp = ++ctx->dct_stamp;
+    hipLaunchKernelGGL(fft_tables_kernel, dim3((n + 255) / 256), dim3(256), 0, s,
+                       reinterpret_cast<float2 *>(t.tab), P.L, P.N);
+    e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e);
+    *out = reinterpret_cast<const float2 *>(t.tab);
+    return HH_OK;
+}
+
+}  // namespace
+
+bool fft_supported(uint32_t n) {
+    Plan P;
+    return make_plan(n, P);
+}
+
+bool use_fft(const hh_context *ctx, uint32_t rows, uint32_t cols) {
+    if (ctx->dct_route == HH_DCT_DENSE) return false;
+    if (!fft_supported(rows) || !fft_supported(cols)) return false;
+    if (ctx->dct_route == HH_DCT_FFT) return true;
+    return (rows > cols ? rows : cols) >= kFftAutoMin;
+}
+
+int32_t fft_scratch(hh_context *ctx, uint64_t total, hipStream_t s, float **a, float **b) {
+    const size_t mat = ((size_t)total * sizeof(float) + 255) & ~(size_t)255;
+    if (ctx->fft_bytes < 2 * mat) {
+        if (ctx->d_fft) {
+            hipError_t e = hipStreamSynchronize(s);
+            if (e == hipSuccess) e = hipFree(ctx->d_fft);
+            ctx->d_fft = nullptr;
+            ctx->fft_bytes = 0;
+            if (e != hipSuccess) return from_hip(e);
+        }
+        hipError_t e = hipMalloc(&ctx->d_fft, 2 * mat);
+        if (e != hipSuccess) {
+            ctx->d_fft = nullptr;
+            return from_hip(e);
+        }
+        ctx->fft_bytes = 2 * mat;
+    }
+    *a = reinterpret_cast<float *>(ctx->d_fft);
+    *b = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->d_fft) + mat);
+    return HH_OK;
+}
+
+int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
+                  uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s) {
+    Plan Pw, Ph;
+    if (!make_plan(w, Pw) || !make_plan(h, Ph)) return HH_ERR_UNSUPPORTED;
+    if (reinterpret_cast<uintptr_t>(d_out) & (out_dtype == HH_F32 ? 15u : 7u)) return HH_ERR_UNSUPPORTED;
+    // the forward route reads its rows as 16-byte vectors
+    if (!inverse && (reinterpret_cast<uintptr_t>(d_in) & 15u)) return HH_ERR_UNSUPPORTED;
+    const float2 *tw, *th;
+    int32_t rc = tables_for(ctx, Pw, s, &tw);
+    if (rc != HH_OK) return rc;
+    rc = tables_for(ctx, Ph, s, &th);
+    if (rc != HH_OK) return rc;
+    if (h == w) tw = th;  // the second lookup may have replaced the first's slot
+    // rows of length w: in -> b (h x w); b^T -> a (w x h); rows of length h:
+    // a -> b (w x h); b^T -> out (h x w), converted
+    hipError_t e = launch_rows(inverse, Pw, d_in, d_b, h, tw, s);
+    if (e == hipSuccess) e = launch_transpose(d_b, h, w, HH_F32, d_a, s);
+    if (e == hipSuccess) e = launch_rows(inverse, Ph, d_a, d_b, w, th, s);
+    if (e == hipSuccess) e = launch_transpose(d_b, w, h, out_dtype, d_out, s);
+    return from_hip(e);
+}
+
+void release_fft_resources(hh_context *ctx) {
+    for (int i = 0; i < 2; i++) {
+        if (ctx->fft_tab[i].tab) (void)hipFree(ctx->fft_tab[i].tab);
+        ctx->fft_tab[i].tab = nullptr;
+        ctx->fft_tab[i].n = 0;
+    }
+    if (ctx->d_fft) (void)hipFree(ctx->d_fft);
+    ctx->d_fft = nullptr;
+    ctx->fft_bytes = 0;
+}
+
+}  // namespace hh

@@ -557,6 +557,25 @@ int32_t hct3_decode_eo(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, 
     if (h % 512u || w % 512u || nfrags == 0 || nfrags > kEoPartials / 256u ||
         (out_addr & (dtype == HH_F32 ? 15u : 7u)))
         return HH_ERR_UNSUPPORTED;
+    const uint64_t total = (uint64_t)h * w;
+    const uint32_t nwords = blocks_for(total, 64);
+    const uint32_t nblk = blocks_for(nwords, kWordsPerBlock);
+    uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
+    uint64_t *d_bits = reinterpret_cast<uint64_t *>(d_stage + ((hct3_block_sums_bytes(total) + 15u) & ~(size_t)15));
+    if (use_fft(ctx, h, w)) {
+        // the fragments scattered into an f32 matrix, then the FFT route
+        float *a, *b;
+        int32_t rc = fft_scratch(ctx, total, s, &a, &b);
+        if (rc != HH_OK) return rc;
+        for (uint32_t i = 0; i < nfrags; i++) {
+            hipError_t e = launch_pack_bits(frags[i].bitmap, (total + 7) / 8, d_bits, s);
+            if (e == hipSuccess)
+                e = launch_hct3_scatter(d_bits, total, d_sums, frags[i].coef, frags[i].ncoef, 0, a, i == 0 ? 1 : 0,
+                                        s);
+            if (e != hipSuccess) return from_hip(e);
+        }
+        return dct2d_fft(ctx, true, a, a, b, h, w, dtype, d_out, s);
+    }
     EoScratch S;
     int32_t rc = eo_scratch(ctx, h, w, true, s, S);
     if (rc != HH_OK) return rc;
@@ -568,11 +587,6 @@ int32_t hct3_decode_eo(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, 
     hipLaunchKernelGGL(split_scale_kernel, dim3(1), dim3(256), 0, s, S.partial, 256u * nfrags, w, S.consts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return from_hip(e);
-    const uint64_t total = (uint64_t)h * w;
-    const uint32_t nwords = blocks_for(total, 64);
-    const uint32_t nblk = blocks_for(nwords, kWordsPerBlock);
-    uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
-    uint64_t *d_bits = reinterpret_cast<uint64_t *>(d_stage + ((hct3_block_sums_bytes(total) + 15u) & ~(size_t)15));
     for (uint32_t i = 0; i < nfrags; i++) {
         e = launch_pack_bits(frags[i].bitmap, (total + 7) / 8, d_bits, s);
         if (e != hipSuccess) return from_hip(e);
@@ -595,6 +609,19 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
     if (rows == 0 || cols == 0) return HH_OK;
     const uint32_t h = rows, w = cols;
     const uint64_t total = (uint64_t)h * w;
+    if (use_fft(ctx, h, w)) {
+        const bool cvt = inverse && cvt_out != nullptr;
+        void *out = cvt ? cvt_out : static_cast<void *>(d_out);
+        const int32_t dt = cvt ? cvt_dtype : HH_F32;
+        if ((reinterpret_cast<uintptr_t>(out) & (dt == HH_F32 ? 15u : 7u)) == 0 &&
+            (inverse || (reinterpret_cast<uintptr_t>(d_in) & 15u) == 0)) {
+            float *a, *b;
+            int32_t rc = fft_scratch(ctx, total, s, &a, &b);
+            if (rc == HH_OK) rc = dct2d_fft(ctx, inverse, d_in, a, b, h, w, dt, out, s);
+            if (rc == HH_OK && converted) *converted = cvt;
+            return rc;
+        }
+    }
     // the inverse needs B^T planes, the forward B planes; a square matrix
     // uses one set for both products
     // the inverse of a matrix whose sides are multiples of 512 runs on the

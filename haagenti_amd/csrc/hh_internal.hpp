@@ -42,6 +42,17 @@ struct hh_context {
     // the poll limit of the fused decode's waits (0: the default)
     int32_t lz4_decoder = HH_LZ4_AUTO;
     uint32_t fused_poll_limit = 0;
+    // whole-matrix transform route (hh_dct_route), the FFT route's twiddle
+    // tables (two lengths cached) and its two f32 matrices of scratch
+    int32_t dct_route = HH_DCT_AUTO;
+    struct FftTables {
+        uint32_t n = 0;
+        void *tab = nullptr;
+        uint64_t stamp = 0;
+    };
+    FftTables fft_tab[2];
+    void *d_fft = nullptr;
+    size_t fft_bytes = 0;
 };
 
 namespace hh {
@@ -277,6 +288,23 @@ int32_t dct2d_full(hh_context *ctx, bool inverse, const float *d_in, float *d_tm
                    uint32_t rows, uint32_t cols, hipStream_t s, bool f16_exact = false,
                    int32_t cvt_dtype = HH_F32, void *cvt_out = nullptr, bool *converted = nullptr);
 void release_dct_resources(hh_context *ctx);
+
+// FFT route of the whole-matrix transforms (dct_fft.hip).  fft_supported:
+// n a multiple of 64 whose half factors into 2, 3, 5, 7 and fits in LDS.
+// use_fft: the route the context's setting takes for a rows x cols matrix
+// (HH_DCT_AUTO: both sides supported and the larger at least kFftAutoMin).
+// fft_scratch: two f32 matrices of `total` elements from the context.
+// dct2d_fft: the orthonormal 2-D DCT-II (forward) or DCT-III of the h x w
+// d_in into d_out (out_dtype; 16-byte aligned f32 or 8-byte aligned 16-bit;
+// the forward's d_in 16-byte aligned), with d_a and d_b (fft_scratch) as the
+// intermediates; d_in may be d_a.
+constexpr uint32_t kFftAutoMin = 1024;
+bool fft_supported(uint32_t n);
+bool use_fft(const hh_context *ctx, uint32_t rows, uint32_t cols);
+int32_t fft_scratch(hh_context *ctx, uint64_t total, hipStream_t s, float **a, float **b);
+int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
+                  uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s);
+void release_fft_resources(hh_context *ctx);
 // zstd::decode_all on the host (host_zstd.cpp): false on a malformed stream.
 bool zstd_decode_all(const uint8_t *in, size_t len, std::vector<uint8_t> &out);
 

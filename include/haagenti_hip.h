@@ -107,9 +107,18 @@ int32_t hh_context_synchronize(hh_context *ctx);
  * into blocks of many short LZ4 sequences) and the ring decoder otherwise
  * (denser tiles leave a few long runs per block).  HH_OPT_FUSED_POLL_LIMIT bounds every wait of
  * the fused layer decode to that many polls (1 .. 2^24; 0 restores 2^24),
- * so a test can drive the path taken when a wait runs out.  Returns
+ * so a test can drive the path taken when a wait runs out.
+ * HH_OPT_DCT_ROUTE picks the whole-matrix transform of hh_idct_2d,
+ * hh_dct_2d and the HCT3 decode entries (hh_dct_route): HH_DCT_AUTO (the
+ * default) takes the FFT route when both sides allow it and the larger is
+ * at least 1024, the dense MFMA products otherwise.  Returns
  * HH_ERR_INVALID_ARGUMENT for an unknown option or value. */
-typedef enum hh_option { HH_OPT_LZ4_DECODER = 1, HH_OPT_FUSED_POLL_LIMIT = 2 } hh_option;
+typedef enum hh_option { HH_OPT_LZ4_DECODER = 1, HH_OPT_FUSED_POLL_LIMIT = 2, HH_OPT_DCT_ROUTE = 3 } hh_option;
+typedef enum hh_dct_route {
+    HH_DCT_AUTO = 0,
+    HH_DCT_DENSE = 1, /* split-f16 MFMA products against cached bases, O(n^3) */
+    HH_DCT_FFT = 2    /* row transforms through an FFT, O(n^2 log n), where the sides allow it */
+} hh_dct_route;
 typedef enum hh_lz4_decoder {
     HH_LZ4_AUTO = 0,   /* per entry point, as above */
     HH_LZ4_SEQ = 1,    /* sequences parsed in batches, copies lane-parallel; 4 KiB ring */
@@ -587,16 +596,22 @@ int32_t hh_turbo_tensor_decode(hh_context *ctx, const uint8_t *data, size_t len,
 
 /* GpuDctContext::idct_2d_gpu / idct_2d for a whole rows x cols matrix
  * (crates/haagenti-cuda/src/dct_gpu.rs:1163-1227, 1404-1412): orthonormal
- * 2-D DCT-III of the row-major f32 d_in into d_out (out_dtype), as two
- * split-f16 MFMA products against cached DCT bases (~1e-6 x RMS; the 16-bit
- * outputs are the round-to-nearest-even of the f32 result).  Asynchronous on
- * the stream. */
+ * 2-D DCT-III of the row-major f32 d_in into d_out (out_dtype).  Two routes
+ * (HH_OPT_DCT_ROUTE), as the reference switches to idct_2d_fft above 4096
+ * (dct_gpu.rs:1081,1714-1722): an FFT route -- each side a multiple of 64
+ * whose half has no prime factor above 7 and is at most 20480; every row
+ * transformed by Makhoul's construction over an f32 FFT in LDS, a
+ * transpose, the same along the other side, a transpose back -- and two
+ * split-f16 MFMA products against cached DCT bases for every other shape
+ * (both ~1e-6 x RMS; the 16-bit outputs are the round-to-nearest-even of
+ * the f32 result).  Asynchronous on the stream. */
 int32_t hh_idct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, int32_t out_dtype,
                    void *d_out, void *stream);
 
-/* GpuDctContext::dct_2d (dct_gpu.rs, used by the turbo encoder,
- * crates/haagenti/src/pipeline/turbo.rs:351-369): orthonormal 2-D DCT-II of
- * a row-major f32 matrix (dct_2d, dct.rs:282-308).  Asynchronous. */
+/* GpuDctContext::dct_2d (dct_gpu.rs:1381-1389, dct_2d_fft above 4096;
+ * used by the turbo encoder, crates/haagenti/src/pipeline/turbo.rs:351-369):
+ * orthonormal 2-D DCT-II of a row-major f32 matrix (dct_2d, dct.rs:282-308),
+ * on the same two routes as hh_idct_2d.  Asynchronous. */
 int32_t hh_dct_2d(hh_context *ctx, const float *d_in, uint32_t rows, uint32_t cols, float *d_out,
                   void *stream);
 

@@ -8,7 +8,13 @@
   restatement of the reference's idct_2d (crates/haagenti-core/src/dct.rs:
   311-337) -- the IDCT tolerance of the decode path; the achieved error is
   ~1e-6 x RMS -- and against the reference's own C decoder where it is
-  built; 16-bit outputs are the round-to-nearest-even of the f32 result."""
+  built; 16-bit outputs are the round-to-nearest-even of the f32 result.
+
+Both whole-matrix routes are covered (the context's HH_OPT_DCT_ROUTE): the
+dense split-f16 MFMA products and the FFT route (Makhoul row transforms over
+an f32 FFT in LDS, the route the reference takes above 4096,
+crates/haagenti-cuda/src/dct_gpu.rs:1081,1404-1412)."""
+import contextlib
 import struct
 
 import numpy as np
@@ -29,6 +35,26 @@ def H():
 
 def dec():
     return H().GpuDecompressor(G.ctx())
+
+
+@contextlib.contextmanager
+def route(name):
+    G.ctx().set_dct_route(name)
+    try:
+        yield
+    finally:
+        G.ctx().set_dct_route("auto")
+
+
+@pytest.fixture
+def dense_route():
+    with route("dense"):
+        yield
+
+
+def basis(n, kk):
+    s = np.sqrt((1.0 if kk == 0 else 2.0) / n)
+    return s * np.cos(np.pi * kk * (2 * np.arange(n) + 1) / (2 * n))
 
 
 def rel_err(got, ref):
@@ -135,24 +161,31 @@ def test_decompress_16bit_outputs_and_device_variant():
     assert np.array_equal(out.cpu().numpy().view(np.uint32), f32.view(np.uint32))
 
 
+@pytest.mark.parametrize("way", ["dense", "fft"])
 @pytest.mark.parametrize("rows,cols", [(64, 64), (1, 77), (77, 1), (37, 53), (200, 120), (512, 512), (1024, 512),
-                                       (512, 1536)])
-def test_idct_dct_2d(rows, cols):
+                                       (512, 1536), (192, 2048)])
+def test_idct_dct_2d(rows, cols, way):
+    # against the f64 closed form; "fft" takes the FFT route where both sides
+    # allow it (multiples of 64 whose halves factor into 2, 3, 5, 7) and the
+    # dense route for the others
     T = G.torch()
     rng = np.random.default_rng(rows + 7 * cols)
     c = rng.normal(0, 1, (rows, cols)).astype(np.float32)
     d_c = T.from_numpy(c).cuda()
     x = T.empty_like(d_c)
-    G.ctx().idct_2d(d_c, rows, cols, x, stream=G.stream())
+    y = T.empty_like(d_c)
+    with route(way):
+        G.ctx().idct_2d(d_c, rows, cols, x, stream=G.stream())
+        # forward, and the round trip
+        G.ctx().dct_2d(x, rows, cols, y, stream=G.stream())
+        G.sync()
     x64 = np.zeros((rows, cols))
     O.lib().hho_idct_2d_f64(O._p(c.astype(np.float64)), O._p(x64), cols, rows)
     assert rel_err(x.cpu().numpy(), x64) <= 1e-5
-    # forward, and the round trip
-    y = T.empty_like(d_c)
-    G.ctx().dct_2d(x, rows, cols, y, stream=G.stream())
     assert rel_err(y.cpu().numpy(), c) <= 1e-5
 
 
+@pytest.mark.usefixtures("dense_route")
 @pytest.mark.parametrize("rows,cols,k,l", [(512, 1024, 5, 30), (1024, 512, 0, 1), (512, 512, 511, 256)])
 def test_idct_even_odd_split_single_coefficient(rows, cols, k, l):
     # sides that are multiples of 512 take the even / odd split of the bases:
@@ -163,14 +196,62 @@ def test_idct_even_odd_split_single_coefficient(rows, cols, k, l):
     c[k, l] = 1.0
     x = T.empty(rows, cols, dtype=T.float32, device="cuda")
     G.ctx().idct_2d(T.from_numpy(c).cuda(), rows, cols, x)
-
-    def basis(n, kk):
-        s = np.sqrt((1.0 if kk == 0 else 2.0) / n)
-        return s * np.cos(np.pi * kk * (2 * np.arange(n) + 1) / (2 * n))
     ref = np.outer(basis(rows, k), basis(cols, l))
     assert np.abs(x.cpu().numpy() - ref).max() <= 1e-6
 
 
+# lengths whose halves run radix 8, 4 (64, 192, 1536, 320, 448, 1344), 2
+# (2048: three radix-8 passes and one radix-2 with four butterflies per
+# thread, the widest variant), 3 (192, 1536, 1344), 5 (320, 640), 7 (448,
+# 896, 1344)
+@pytest.mark.parametrize("rows,cols", [(64, 192), (320, 448), (1536, 640), (896, 1344), (2048, 128)])
+def test_fft_route_single_coefficient_closed_form(rows, cols):
+    # C = e_k e_l^T inverts to the outer product of two basis rows, and the
+    # forward transform of that product is e_k e_l^T again; k, l include 0,
+    # n/2 and n-1, which the real-to-complex packing pairs specially
+    T = G.torch()
+    with route("fft"):
+        for k, l in [(0, 0), (rows // 2, 1), (rows - 1, cols // 2), (7, cols - 1), (rows // 4 + 3, cols // 4)]:
+            c = np.zeros((rows, cols), np.float32)
+            c[k, l] = 1.0
+            x = T.empty(rows, cols, dtype=T.float32, device="cuda")
+            G.ctx().idct_2d(T.from_numpy(c).cuda(), rows, cols, x)
+            ref = np.outer(basis(rows, k), basis(cols, l))
+            assert np.abs(x.cpu().numpy() - ref).max() <= 1e-6, (k, l)
+            y = T.empty_like(x)
+            G.ctx().dct_2d(T.from_numpy(ref.astype(np.float32)).cuda(), rows, cols, y)
+            assert np.abs(y.cpu().numpy() - c).max() <= 1e-5, (k, l)
+
+
+def test_fft_route_matches_dense_route_4096():
+    # one 4096 x 4096 HCT3 tensor decoded on both routes (f32 within
+    # 1e-5 x RMS of each other); the FFT route's bf16 and f16 outputs are the
+    # rounding of its f32 output, and the device-resident entry gives the
+    # same bits
+    Hm = H()
+    T = G.torch()
+    rng = np.random.default_rng(4097)
+    shape = (4096, 4096)
+    total = 4096 * 4096
+    data = container([random_fragment(rng, total, 0.2), random_fragment(rng, total, 0.02)])
+    with route("dense"):
+        dense = dec().decompress_to_gpu(data, shape, stream=G.stream()).cpu().numpy()
+    with route("fft"):
+        got = dec().decompress_to_gpu(data, shape, stream=G.stream()).cpu().numpy()
+        b16 = dec().decompress_to_gpu(data, shape, dtype=Hm.BF16).view(T.int16).cpu().numpy().view(np.uint16)
+        h16 = dec().decompress_to_gpu(data, shape, dtype=Hm.F16).view(T.int16).cpu().numpy().view(np.uint16)
+        out = T.empty(total, dtype=T.float32, device="cuda")
+        dec().decompress_device(data, G.dev(np.frombuffer(data, np.uint8)), shape, out, stream=G.stream())
+        G.sync()
+    err = rel_err(got, dense)
+    print(f"[hct3] 4096 x 4096: max|fft - dense| = {err:.2e} x RMS", flush=True)
+    assert err <= 1e-5
+    assert np.array_equal(b16, G.bf16_bits(got))
+    assert np.array_equal(h16, G.f16_bits(got))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.usefixtures("dense_route")
 def test_decompress_even_odd_split_vs_oracle_and_16bit():
     # a 1024 x 512 HCT3 tensor: the split inverse against the oracle, and its
     # bf16 / f16 outputs the rounding of its f32 output
@@ -214,6 +295,7 @@ def _direct_vs_dense(data, shape):
     return got, e_ref, e_dense
 
 
+@pytest.mark.usefixtures("dense_route")
 def test_decompress_direct_plane_scatter_matches_dense_route():
     # sides that are multiples of 512: the fragments' values are scattered
     # straight into the split transform's operand plane, scaled by a power of
@@ -233,6 +315,7 @@ def test_decompress_direct_plane_scatter_matches_dense_route():
     assert np.array_equal(b16, G.bf16_bits(got))
 
 
+@pytest.mark.usefixtures("dense_route")
 def test_decompress_direct_plane_scatter_overwritten_maximum():
     # the second fragment overwrites part of the first, including its largest
     # value (400, against values of ~0.05): the scale comes from a value the
@@ -262,10 +345,6 @@ def test_idct_single_coefficient_closed_form():
     c[k, l] = 1.0
     x = T.empty(rows, cols, dtype=T.float32, device="cuda")
     G.ctx().idct_2d(T.from_numpy(c).cuda(), rows, cols, x)
-
-    def basis(n, kk):
-        s = np.sqrt((1.0 if kk == 0 else 2.0) / n)
-        return s * np.cos(np.pi * kk * (2 * np.arange(n) + 1) / (2 * n))
     ref = np.outer(basis(rows, k), basis(cols, l))
     assert np.abs(x.cpu().numpy() - ref).max() <= 1e-6
 
@@ -388,16 +467,18 @@ def test_decompress_batch_pipelined_matches_decompress():
         assert rel_err(o, O.hct3_decode(c, shp)[1]) <= TOL
 
 
-def _real_size(rows, cols, seed):
+def _real_size(rows, cols, seed, way="auto"):
     # one fragment at the turbo pipeline's 20 % retention: the GPU decode
-    # (direct plane scatter + even / odd split products at these sizes)
-    # against the oracle's bit-exact scatter and f32 idct_2d (the same 1-D
-    # transforms as hct3_decode, run on every host thread)
+    # (the FFT route at these sizes by default; "dense": direct plane
+    # scatter + even / odd split products) against the oracle's bit-exact
+    # scatter and f32 idct_2d (the same 1-D transforms as hct3_decode, run on
+    # every host thread)
     rng = np.random.default_rng(seed)
     total = rows * cols
     data = container([random_fragment(rng, total, 0.2)])
-    print(f"[hct3] {rows} x {cols}: {len(data)} container bytes", flush=True)
-    got = dec().decompress_to_gpu(data, (rows, cols), stream=G.stream()).cpu().numpy()
+    print(f"[hct3] {rows} x {cols} ({way}): {len(data)} container bytes", flush=True)
+    with route(way):
+        got = dec().decompress_to_gpu(data, (rows, cols), stream=G.stream()).cpu().numpy()
     rc, coef = O.hct3_coefficients(data, total)
     assert rc == O.OK
     ref = O.idct_2d_mt(coef.reshape(rows, cols)).ravel()
@@ -408,12 +489,14 @@ def _real_size(rows, cols, seed):
     return data, got
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 4096), (8192, 8192)])
-def test_decompress_real_sizes_vs_oracle(rows, cols):
-    data, got = _real_size(rows, cols, seed=rows // 64)
+@pytest.mark.parametrize("rows,cols,way", [(4096, 4096, "dense"), (4096, 4096, "auto"), (8192, 8192, "dense"),
+                                           (8192, 8192, "auto")])
+def test_decompress_real_sizes_vs_oracle(rows, cols, way):
+    data, got = _real_size(rows, cols, seed=rows // 64, way=way)
     if rows == 8192:
         T = G.torch()
-        b16 = dec().decompress_to_gpu(data, (rows, cols), dtype=H().BF16).view(T.int16).cpu().numpy()
+        with route(way):
+            b16 = dec().decompress_to_gpu(data, (rows, cols), dtype=H().BF16).view(T.int16).cpu().numpy()
         assert np.array_equal(b16.view(np.uint16), G.bf16_bits(got))
 
 
