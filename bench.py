@@ -39,12 +39,14 @@ Other workloads (one JSON line each, same contract):
                    blocks of lz4-256mib (one wavefront per block), the
                    checksum HctReaderV2 verifies per block; value = hashed
                    bytes per second (the kernel reads its input once)
-  hct3-4096        one 4096x4096 N(0, 0.02) tensor as an HCT V3 fragment
-                   container (whole-tensor DCT, turbo defaults: top 20 %,
-                   f16 coefficients); GPU bitmap scatter + whole-matrix
-                   inverse DCT as two hand-written split-f16 MFMA products
-                   (five f16 passes, f32 accumulation), bf16 out; roofline
-                   against the dense f16 MFMA peak
+  hct3-4096        one 4096x4096 N(0, 0.02) tensor (--hct3-size n: n x n)
+                   as an HCT V3 fragment container (whole-tensor DCT, turbo
+                   defaults: top 20 %, f16 coefficients); GPU bitmap scatter
+                   + whole-matrix inverse DCT, bf16 out: by default the FFT
+                   route (row transforms through an f32 FFT in LDS and two
+                   transposes; roofline against HBM), --dct-route dense the
+                   two hand-written split-f16 MFMA products (five f16 passes,
+                   f32 accumulation; roofline against the f16 MFMA peak)
   hbm-copy         a 1 GiB device copy by the library's streaming copy kernel
                    (hh_hbm_copy): the HBM reference rate and the calibration
                    for the FETCH_SIZE / WRITE_SIZE counters
@@ -600,12 +602,12 @@ def wl_idct(args, torch, H, O):
 
 def wl_hct3(args, torch, H, O):
     """Whole-tensor HCT3 spectral decode (GpuDecompressor::decompress_to_gpu)
-    of one 4096x4096 N(0, 0.02) tensor encoded with the turbo defaults
+    of one n x n (default 4096) N(0, 0.02) tensor encoded with the turbo defaults
     (retention 0.20, 4 fragments, essential ratio 0.20,
     crates/haagenti/src/pipeline/turbo.rs:88-96), the container resident in
     HBM, bf16 output."""
     import struct
-    n = 4096
+    n = args.hct3_size
     ctx = new_ctx(H, args)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
@@ -664,7 +666,7 @@ def wl_hct3(args, torch, H, O):
         alg = len(data) + n * n * 2
         achieved = alg / per / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4), "traffic": traffic_for("hct3-4096-fft"),
+                "frac": round(achieved / 8000.0, 4), "traffic": traffic_for(f"hct3-{n}-fft"),
                 "kernel": ("bitmap scatter into an f32 matrix + dct_fft_rows_kernel x2 (Makhoul rows over an "
                            "f32 Stockham FFT in LDS) + transpose_kernel x2 (the second converting to bf16)"),
                 "avg_launch_us": round(per * 1e6, 1), "algorithmic_bytes_per_launch": alg,
@@ -677,15 +679,15 @@ def wl_hct3(args, torch, H, O):
         achieved = flop / per / 1e12
         peak = 2500.0
         roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": traffic_for("hct3-4096"),
+                "frac": round(achieved / peak, 4), "traffic": traffic_for(f"hct3-{n}"),
                 "kernel": ("dct_gemm_kernel x2 (hand-written split-f16 MFMA on the even / odd split of the "
                            "cosine bases: half-depth products, 2 + 3 passes, f32 accumulation; + butterfly, "
                            "bitmap scatter and the amax / scale passes)"),
                 "avg_launch_us": round(per * 1e6, 1), "algorithmic_flop_per_launch": flop,
                 "mfma_type": "f16", "mfma_flop_per_launch": 5 * n ** 3}
         dt = "f16-split-mfma/f32"
-    return line("hct3-4096", n * n * 2 / per / 1e9, ms_step, args, dt,
-                "synthetic (4096x4096 N(0,0.02), torch seed 17, turbo defaults)",
+    return line(f"hct3-{n}", n * n * 2 / per / 1e9, ms_step, args, dt,
+                f"synthetic ({n}x{n} N(0,0.02), torch seed 17, turbo defaults)",
                 {"rows": n, "cols": n, "retention": 0.20, "coefficients": int(keep),
                  "container_bytes": len(data), "out_dtype": "bf16", "dct_route": args.dct_route}, roof, cpu,
                 {"spot_check_max_err_over_rms": check})
@@ -980,6 +982,7 @@ def main():
     ap.add_argument("--path", choices=["fused", "two-launch"], default="fused",
                     help="llama3-8b-layer: one fused LZ4 + tile launch per layer (hh_hctt_decode_lz4_fused) "
                          "or the LZ4 and tile launches through a scratch buffer (hh_hctt_decode_lz4_batch)")
+    ap.add_argument("--hct3-size", type=int, default=4096, help="hct3-4096: side of the square tensor")
     ap.add_argument("--dct-route", default="auto", choices=["auto", "dense", "fft"],
                     help="whole-matrix transform route of hct3-4096 (the context's HH_OPT_DCT_ROUTE)")
     ap.add_argument("--lz4-decoder", default="auto", choices=sorted(LZ4_KERNEL_NAMES),

@@ -110,6 +110,18 @@ def test_idct_2d_vs_reference_c_decoder():
         assert np.abs(mine - ref).max() < 2e-6 * np.abs(ref).max() * 8
 
 
+@pytest.mark.parametrize("shape,threads", [((1, 64), 4), ((37, 53), 3), ((256, 64), 16), ((96, 640), 0),
+                                           ((1000, 24), 7)])
+def test_idct_2d_threaded_equals_one_thread(shape, threads):
+    # the threaded form used for real-size GPU checks splits rows and then
+    # columns over threads; every 1-D transform is the one-thread code, so
+    # the result must be identical bit for bit (odd, tall, wide and
+    # non-power-of-two shapes; more threads than rows)
+    rng = np.random.default_rng(shape[0] * 31 + shape[1])
+    x = rng.normal(0, 1, shape).astype(np.float32)
+    assert np.array_equal(O.idct_2d_mt(x, threads).view(np.uint32), O.idct_2d(x).view(np.uint32))
+
+
 # ---------------------------------------------------------------- retention
 def test_retain_count():
     assert O.retain_count(4096, 0.3) == 1228
