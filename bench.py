@@ -108,10 +108,10 @@ def traffic_for(workload):
         return None
 
 
-def roofline(workload, kernel, algo_bytes, avg_s, extra=None):
+def roofline(workload, kernel, algo_bytes, avg_s, extra=None, traffic_key=None):
     achieved = algo_bytes / avg_s / 1e9
     r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(workload),
+         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(traffic_key or workload),
          "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
          "algorithmic_bytes_per_launch": int(algo_bytes)}
     if extra:
@@ -529,7 +529,9 @@ def wl_lz4(args, torch, H, O):
                 "synthetic (64 distinct seeded blocks, seeded coin per block)",
                 {"blocks": nb, "block_bytes": 65536, "in_bytes": int(blob.size),
                  "launches_per_step": launches},
-                roofline("lz4-256mib", LZ4_KERNEL_NAMES[args.lz4_decoder], blob.size + out_b, per), cpu,
+                roofline("lz4-256mib", LZ4_KERNEL_NAMES[args.lz4_decoder], blob.size + out_b, per,
+                         traffic_key={"auto": "lz4-256mib", "ring4": "lz4-256mib",
+                                      "seq": "lz4-256mib:seq"}.get(args.lz4_decoder, "-")), cpu,
                 {"bit_exact": exact})
 
 
