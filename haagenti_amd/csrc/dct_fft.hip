@@ -35,12 +35,42 @@ constexpr uint32_t kMaxLds = 160u * 1024u;
 struct FftRows {
     const float *in;
     float *out;
-    const float2 *roots;  // e^(+2 pi i t / L), t in [0, L)
-    const float2 *w4;     // e^(+i pi k / (2N)), k in [0, 2N)
+    // twiddle tables (fft_tables_kernel): per pass q (radix R_q, p_q the
+    // product of the earlier radices) w_L^(j k L / (p_q R_q)) at
+    // [off_q + (j - 1) p_q + k] for k < p_q, 1 <= j < R_q -- the lanes of a
+    // wave read consecutive k, so each load is coalesced; then w_4N^k for
+    // k <= N and w_N^k for k < L
+    const float2 *ptab;
+    const float2 *w4;
+    const float2 *wn;
     uint32_t N, L;
     uint32_t nr;
     uint8_t r[16];
 };
+
+// table[idx]: the table's base (a kernel argument, scalar) plus a 32-bit
+// byte offset, so the load needs no 64-bit address arithmetic per lane
+__device__ __forceinline__ float2 tab_at(const float2 *__restrict__ table, uint32_t idx) {
+    return *reinterpret_cast<const float2 *>(reinterpret_cast<const uint8_t *>(table) + (size_t)(idx * 8u));
+}
+__device__ __forceinline__ float2 tab_at_byte(const float2 *__restrict__ table, uint32_t off) {
+    return *reinterpret_cast<const float2 *>(reinterpret_cast<const uint8_t *>(table) + (size_t)off);
+}
+// the byte offsets of a pass table's entries (j, k), j = 1 .. R-1: k + (j -
+// 1) p, stepped by additions (the empty asm keeps the compiler from turning
+// the steps into quarter-rate multiplies)
+template <int R>
+__device__ __forceinline__ void twiddle_offsets(uint32_t k, uint32_t p, uint32_t (&off)[R]) {
+    const uint32_t p8 = p * 8u;
+    uint32_t o = k * 8u;
+    off[1] = o;
+#pragma unroll
+    for (int j = 2; j < R; j++) {
+        o += p8;
+        __asm__("" : "+v"(o));
+        off[j] = o;
+    }
+}
 
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
     return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
@@ -172,13 +202,13 @@ struct Dft<7, INV> {
 // (i - k) R + k + j p.  All inputs are read before the barrier, so the
 // pass runs in place.
 template <int R, int MAXB, bool INV>
-__device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, const float2 *__restrict__ roots) {
+__device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, const float2 *__restrict__ ptab) {
     // the twiddles are loaded with the pass's LDS reads, before the barrier,
-    // where the registers allow (roots[0] is exactly 1: no branch for k = 0)
+    // where the registers allow; the first pass (p = 1) has none
     constexpr bool kPre = MAXB * (R - 1) <= 16;
+    const bool tw = p > 1;
     const uint32_t T = blockDim.x, tid = threadIdx.x;
     const uint32_t nb = L / R;
-    const uint32_t stride = L / (p * R);
     // i mod p without a division: (i + 1/2) / p lies at least 1/(2p) from an
     // integer, and the float product's relative error (2^-23 with 1/p
     // rounded) stays below that for i < 2^22 (i < L <= 20480 here)
@@ -192,10 +222,11 @@ __device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, co
         if (i < nb) {
 #pragma unroll
             for (int j = 0; j < R; j++) x[b][j] = buf[i + j * nb];
-            if (kPre) {
-                const uint32_t t = mod_p(i) * stride;
+            if (kPre && tw) {
+                uint32_t off[R];
+                twiddle_offsets<R>(mod_p(i), p, off);
 #pragma unroll
-                for (int j = 1; j < R; j++) w[kPre ? b : 0][j - 1] = roots[j * t];
+                for (int j = 1; j < R; j++) w[kPre ? b : 0][j - 1] = tab_at_byte(ptab, off[j]);
             }
         }
     }
@@ -205,12 +236,15 @@ __device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, co
         const uint32_t i = tid + b * T;
         if (i < nb) {
             const uint32_t k = mod_p(i);
-            const uint32_t t = k * stride;
+            if (tw) {
+                uint32_t off[R];
+                if (!kPre) twiddle_offsets<R>(k, p, off);
 #pragma unroll
-            for (int j = 1; j < R; j++) {
-                float2 tw = kPre ? w[kPre ? b : 0][j - 1] : roots[j * t];
-                if (!INV) tw.y = -tw.y;
-                x[b][j] = cmul(x[b][j], tw);
+                for (int j = 1; j < R; j++) {
+                    float2 t = kPre ? w[kPre ? b : 0][j - 1] : tab_at_byte(ptab, off[j]);
+                    if (!INV) t.y = -t.y;
+                    x[b][j] = cmul(x[b][j], t);
+                }
             }
             Dft<R, INV>::run(x[b]);
             const uint32_t base = (i - k) * R + k;
@@ -228,6 +262,7 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
     const float *__restrict__ in = P.in + (uint64_t)blockIdx.x * N;
     float *__restrict__ out = P.out + (uint64_t)blockIdx.x * N;
     const float2 *__restrict__ w4 = P.w4;
+    const float2 *__restrict__ wn = P.wn;
     const float s0 = sqrtf(1.0f / (float)N), s1 = sqrtf(2.0f / (float)N);
     // the row's loads are issued kB per thread at a time, before any use
     constexpr int kB = 4;
@@ -254,20 +289,20 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
                 const float au = a[u] * (k == 0 ? s0 : s1), bu = b[u] * s1, du = d[u] * s1, eu = e[u] * s1;
                 if (k == 0) {
                     const float2 h0 = make_float2(au, 0.0f);
-                    const float2 hl = cmul(w4[L], make_float2(0.5f * du, -0.5f * du));
+                    const float2 hl = cmul(tab_at(w4, L), make_float2(0.5f * du, -0.5f * du));
                     buf[0] = cadd(cadd(h0, hl), rot90<true>(csub(h0, hl)));
-                    const float2 hm = cmul(w4[L / 2], make_float2(0.5f * eu, -0.5f * bu));
-                    const float2 hml = cmul(w4[3 * L / 2], make_float2(0.5f * bu, -0.5f * eu));
-                    buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(w4[N], csub(hm, hml))));
+                    const float2 hm = cmul(tab_at(w4, L / 2), make_float2(0.5f * eu, -0.5f * bu));
+                    const float2 hml = cmul(tab_at(w4, 3 * L / 2), make_float2(0.5f * bu, -0.5f * eu));
+                    buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(tab_at(w4, N), csub(hm, hml))));
                     continue;
                 }
-                const float2 hk = cmul(w4[k], make_float2(0.5f * au, -0.5f * bu));
-                const float2 hkl = cmul(w4[k + L], make_float2(0.5f * du, -0.5f * eu));
-                buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(w4[4 * k], csub(hk, hkl))));
+                const float2 hk = cmul(tab_at(w4, k), make_float2(0.5f * au, -0.5f * bu));
+                const float2 hkl = cmul(tab_at(w4, k + L), make_float2(0.5f * du, -0.5f * eu));
+                buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(tab_at(wn, k), csub(hk, hkl))));
                 const uint32_t k2 = L - k;
-                const float2 h2 = cmul(w4[k2], make_float2(0.5f * eu, -0.5f * du));
-                const float2 h2l = cmul(w4[N - k], make_float2(0.5f * bu, -0.5f * au));
-                buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(w4[4 * k2], csub(h2, h2l))));
+                const float2 h2 = cmul(tab_at(w4, k2), make_float2(0.5f * eu, -0.5f * du));
+                const float2 h2l = cmul(tab_at(w4, N - k), make_float2(0.5f * bu, -0.5f * au));
+                buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(tab_at(wn, k2), csub(h2, h2l))));
             }
         }
     } else {
@@ -291,16 +326,17 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
         }
     }
     __syncthreads();
-    uint32_t p = 1;
+    uint32_t p = 1, poff = 0;
     for (uint32_t q = 0; q < P.nr; q++) {
         switch (P.r[q]) {
-            case 8: fft_pass<8, MAXB, INV>(buf, L, p, P.roots); break;
-            case 4: fft_pass<4, MAXB, INV>(buf, L, p, P.roots); break;
-            case 2: fft_pass<2, MAXB, INV>(buf, L, p, P.roots); break;
-            case 3: fft_pass<3, MAXB, INV>(buf, L, p, P.roots); break;
-            case 5: fft_pass<5, MAXB, INV>(buf, L, p, P.roots); break;
-            default: fft_pass<7, MAXB, INV>(buf, L, p, P.roots); break;
+            case 8: fft_pass<8, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            case 4: fft_pass<4, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            case 2: fft_pass<2, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            case 3: fft_pass<3, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            case 5: fft_pass<5, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            default: fft_pass<7, MAXB, INV>(buf, L, p, P.ptab + poff); break;
         }
+        poff += p * (P.r[q] - 1u);
         p *= P.r[q];
     }
     if (INV) {
@@ -321,9 +357,9 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
                 const float2 zc = cconj(buf[kk == 0 ? 0 : L - kk]);
                 const float2 E = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y + zc.y));
                 const float2 D = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y - zc.y));
-                const float2 wn = kk == L ? make_float2(-1.0f, 0.0f) : cconj(w4[4 * kk]);
-                const float2 V = csub(E, rot90<true>(cmul(wn, D)));
-                const float2 W = cmul(cconj(w4[kk]), V);
+                const float2 wq = kk == L ? make_float2(-1.0f, 0.0f) : cconj(tab_at(wn, kk));
+                const float2 V = csub(E, rot90<true>(cmul(wq, D)));
+                const float2 W = cmul(cconj(tab_at(w4, kk)), V);
                 out[kk] = (kk == 0 ? s0 : s1) * W.x;
                 if (kk != 0 && kk != L) out[N - kk] = -s1 * W.y;
             }
@@ -365,15 +401,41 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *__restrict_
     }
 }
 
-// roots[t] = e^(2 pi i t / L) for t < L, then w4[k] = e^(i pi k / (2N)) for k < 2N
-__global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ tab, uint32_t L, uint32_t N) {
+// The twiddle tables of a length-N plan (FftRows): the pass tables (L - 1
+// entries: sum_q p_q (R_q - 1) = L - 1), then w_4N^k for k <= N, then w_N^k
+// for k < L; each entry computed in double and rounded once.
+struct TabPlan {
+    uint32_t L, N, nr;
+    uint8_t r[16];
+};
+constexpr uint32_t tab_w4(uint32_t L) { return L; }              // after the pass tables (L - 1, one pad)
+constexpr uint32_t tab_wn(uint32_t L, uint32_t N) { return L + N + 1; }
+constexpr uint32_t tab_len(uint32_t L, uint32_t N) { return L + N + 1 + L; }
+
+__global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ tab, TabPlan P) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= L + 2 * N) return;
-    double s, c;
-    if (i < L)
-        sincospi(2.0 * (double)i / (double)L, &s, &c);
-    else
+    const uint32_t L = P.L, N = P.N;
+    if (i >= tab_len(L, N)) return;
+    double s = 0.0, c = 1.0;
+    if (i < L) {
+        // pass q: entry (j, k) at off_q + (j - 1) p_q + k
+        uint32_t p = 1, off = 0;
+        for (uint32_t q = 0; q < P.nr; q++) {
+            const uint32_t R = P.r[q], n = p * (R - 1u);
+            if (i < off + n) {
+                const uint32_t j = (i - off) / p + 1u, k = (i - off) % p;
+                // w_L^(j k L / (p R)) = e^(2 pi i j k / (p R))
+                sincospi(2.0 * (double)(j * k) / (double)(p * R), &s, &c);
+                break;
+            }
+            off += n;
+            p *= R;
+        }
+    } else if (i < tab_wn(L, N)) {
         sincospi((double)(i - L) / (2.0 * (double)N), &s, &c);
+    } else {
+        sincospi(2.0 * (double)(i - tab_wn(L, N)) / (double)N, &s, &c);
+    }
     tab[i] = make_float2((float)c, (float)s);
 }
 
@@ -431,8 +493,9 @@ hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out,
     FftRows A;
     A.in = in;
     A.out = out;
-    A.roots = tab;
-    A.w4 = tab + P.L;
+    A.ptab = tab;
+    A.w4 = tab + tab_w4(P.L);
+    A.wn = tab + tab_wn(P.L, P.N);
     A.N = P.N;
     A.L = P.L;
     A.nr = P.nr;
@@ -478,7 +541,7 @@ int32_t tables_for(hh_context *ctx, const Plan &P, hipStream_t s, const float2 *
         t.n = 0;
         if (e != hipSuccess) return from_hip(e);
     }
-    const uint32_t n = P.L + 2 * P.N;
+    const uint32_t n = tab_len(P.L, P.N);
     hipError_t e = hipMalloc(&t.tab, (size_t)n * sizeof(float2));
     if (e != hipSuccess) {
         t.tab = nullptr;
@@ -486,8 +549,13 @@ int32_t tables_for(hh_context *ctx, const Plan &P, hipStream_t s, const float2 *
     }
     t.n = P.N;
     t.stamp = ++ctx->dct_stamp;
+    TabPlan TP;
+    TP.L = P.L;
+    TP.N = P.N;
+    TP.nr = P.nr;
+    for (int q = 0; q < 16; q++) TP.r[q] = P.r[q];
     hipLaunchKernelGGL(fft_tables_kernel, dim3((n + 255) / 256), dim3(256), 0, s,
-                       reinterpret_cast<float2 *>(t.tab), P.L, P.N);
+                       reinterpret_cast<float2 *>(t.tab), TP);
     e = hipGetLastError();
     if (e != hipSuccess) return from_hip(e);
     *out = reinterpret_cast<const float2 *>(t.tab);

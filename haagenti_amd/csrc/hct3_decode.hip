@@ -124,9 +124,33 @@ __global__ __launch_bounds__(256) void hct3_scatter_kernel(const uint64_t *__res
     P[threadIdx.x] = block_pref[blockIdx.x] + excl;
     __syncthreads();
     const uint64_t e0 = w0 * 64;
-    // values are read bytewise: inside a fragment container they may sit
-    // at any byte offset
     const uint8_t *cb = reinterpret_cast<const uint8_t *>(coef);
+    if (!coef_f32 && ((uintptr_t)coef & 1u) == 0 && ncoef > 0) {
+        // 2-byte aligned f16 values: eight elements' values loaded together
+        // (an element without a value loads value 0 and discards it)
+        const uint16_t *hv16 = reinterpret_cast<const uint16_t *>(coef);
+        for (uint32_t j0 = 0; j0 < 64; j0 += 8) {
+            uint32_t x[8];
+            bool hv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t el = threadIdx.x + kWordsPerBlock * (j0 + k);
+                const uint64_t bw = W[el >> 6];
+                const uint32_t bit = el & 63u;
+                const uint32_t rk = P[el >> 6] + (uint32_t)__popcll(bw & ((1ull << bit) - 1ull));
+                hv[k] = ((bw >> bit) & 1ull) && rk < ncoef;  // bits past nbits are clear
+                x[k] = hv16[hv[k] ? rk : 0u];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint64_t e = e0 + threadIdx.x + kWordsPerBlock * (j0 + k);
+                if (e < nbits && (first || hv[k])) dense[e] = hv[k] ? f16_bits_to_f32(x[k]) : 0.0f;
+            }
+        }
+        return;
+    }
+    // values read bytewise: inside a fragment container they may sit at any
+    // byte offset
     for (uint32_t j = 0; j < 64; j++) {
         const uint32_t el = threadIdx.x + kWordsPerBlock * j;
         const uint64_t e = e0 + el;

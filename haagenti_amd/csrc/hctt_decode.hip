@@ -179,6 +179,7 @@ struct TileBatch {
     int32_t *status[kMaxTensors];
     uint32_t start[kMaxTensors + 1];
     uint32_t tiles_per_row[kMaxTensors];
+    float tpr_inv[kMaxTensors];  // 1 / tiles_per_row, rounded to f32 on the host
     uint32_t cols[kMaxTensors];
     uint32_t k[kMaxTensors];
     uint32_t tb[kMaxTensors];
@@ -461,7 +462,10 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * pitch;
     constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
     const uint32_t tpr = uniform(B.tiles_per_row[ti]);
-    const uint32_t tr = t / tpr, tc = t % tpr;
+    // t / tpr without a division below 2^22 tiles: (t + 1/2) / tpr lies at
+    // least 1/(2 tpr) from an integer, beyond the float product's error
+    const uint32_t tr = t < (1u << 22) ? uniform((uint32_t)(((float)t + 0.5f) * B.tpr_inv[ti])) : t / tpr;
+    const uint32_t tc = t - tr * tpr;
     const size_t base = (size_t)(64 * tr) * cols + 64 * tc;
     // the tile's first output byte and the row pitch, in scalar registers:
     // a store addresses scalar base + 32-bit lane offset (no 64-bit vector
@@ -1148,6 +1152,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
             B.status[j] = T.d_tile_status;
             B.start[j] = total;
             B.tiles_per_row[j] = T.cols / 64;
+            B.tpr_inv[j] = 1.0f / (float)(T.cols / 64);
             B.cols[j] = T.cols;
             B.k[j] = T.k;
             B.tb[j] = tb;
@@ -1246,6 +1251,7 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
             B.status[j] = T.d_tile_status;
             B.start[j] = total;
             B.tiles_per_row[j] = T.cols / 64;
+            B.tpr_inv[j] = 1.0f / (float)(T.cols / 64);
             B.cols[j] = T.cols;
             B.k[j] = T.k;
             B.tb[j] = (uint32_t)hh_hctt_tile_bytes(T.k);
