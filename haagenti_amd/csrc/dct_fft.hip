@@ -31,6 +31,11 @@ namespace hh {
 namespace {
 
 constexpr uint32_t kMaxLds = 160u * 1024u;
+constexpr uint32_t kFftMaxFrags = 16;
+constexpr uint32_t kStaticLds = 64;  // the row kernel's scan words, beside the dynamic LDS
+// elements (k pairs) per thread of a fused-scatter pre-step, read before any
+// write (the row and the FFT points share the LDS)
+constexpr uint32_t kScatK = 8;
 
 struct FftRows {
     const float *in;
@@ -46,6 +51,14 @@ struct FftRows {
     uint32_t N, L;
     uint32_t nr;
     uint8_t r[16];
+    // HCT3 fragments scattered into the rows in LDS (the fused first pass of
+    // an inverse; `in` unused): fragment f's bitmap as 64-bit words, the
+    // rank of each row's first bit, its f16 values and their count
+    uint32_t nfrag;
+    const uint64_t *fbits[kFftMaxFrags];
+    const uint32_t *fpref[kFftMaxFrags];
+    const uint8_t *fcoef[kFftMaxFrags];
+    uint32_t fncoef[kFftMaxFrags];
 };
 
 // table[idx]: the table's base (a kernel argument, scalar) plus a 32-bit
@@ -195,6 +208,97 @@ struct Dft<7, INV> {
     }
 };
 
+// Exclusive sum of v over the workgroup's threads (up to 1024; sm: 16
+// words of LDS).
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *sm) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint32_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(incl, d);
+        if (lane >= (uint32_t)d) incl += t;
+    }
+    if (lane == 63u) sm[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t i = 0; i < nw; i++) before += i < wave ? sm[i] : 0u;
+    __syncthreads();  // sm reusable after
+    return before + incl - v;
+}
+
+// Set bits per row of a bitmap of `rows` rows of wpr 64-bit words: one wave
+// per row.
+__global__ __launch_bounds__(256) void row_counts_kernel(const uint64_t *__restrict__ bits, uint32_t wpr,
+                                                         uint32_t rows, uint32_t *__restrict__ cnt) {
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (row >= rows) return;
+    const uint64_t *rb = bits + (uint64_t)row * wpr;
+    uint32_t c = 0;
+    for (uint32_t i = lane; i < wpr; i += 64u) c += (uint32_t)__popcll(rb[i]);
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d);
+    if (lane == 0) cnt[row] = c;
+}
+
+// Builds row `row` of the coefficient matrix in LDS as N f32 values (rowf)
+// from the fragments, in order: zeros, then every set bit whose rank is
+// below the fragment's value count takes that value (later fragments
+// overwrite earlier ones), as the HCT3 scatter does.  wds / wpre: N / 64
+// words of LDS each (the row's bitmap words and their ranks).
+__device__ __forceinline__ void scatter_row(const FftRows &P, uint32_t row, float *rowf, uint64_t *wds,
+                                            uint32_t *wpre, uint32_t *sm) {
+    const uint32_t N = P.N, T = blockDim.x, tid = threadIdx.x, nw = N / 64u;
+    for (uint32_t i = tid; i < N / 4u; i += T) reinterpret_cast<float4 *>(rowf)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t f = 0; f < P.nfrag; f++) {
+        // this row's words and the rank of each word's first bit (nw <= T)
+        uint64_t wv = 0;
+        if (tid < nw) wv = P.fbits[f][(uint64_t)row * nw + tid];
+        const uint32_t ex = block_excl_scan(tid < nw ? (uint32_t)__popcll(wv) : 0u, sm);
+        if (tid < nw) {
+            wds[tid] = wv;
+            wpre[tid] = P.fpref[f][row] + ex;
+        }
+        __syncthreads();
+        const uint32_t nc = P.fncoef[f];
+        const uint8_t *cb = P.fcoef[f];
+        if (nc > 0 && ((uintptr_t)cb & 1u) == 0) {
+            // eight elements' values loaded together (an element without a
+            // value loads value 0 and discards it)
+            const uint16_t *c16 = reinterpret_cast<const uint16_t *>(cb);
+            for (uint32_t e0 = 0; e0 < N; e0 += 8u * T) {
+                uint32_t x[8];
+                bool hv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const uint32_t e = e0 + tid + (uint32_t)u * T;
+                    hv[u] = false;
+                    uint32_t rk = 0;
+                    if (e < N) {
+                        const uint64_t bw = wds[e >> 6];
+                        const uint32_t bit = e & 63u;
+                        rk = wpre[e >> 6] + (uint32_t)__popcll(bw & ((1ull << bit) - 1ull));
+                        hv[u] = ((bw >> bit) & 1ull) && rk < nc;
+                    }
+                    x[u] = c16[hv[u] ? rk : 0u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (hv[u]) rowf[e0 + tid + (uint32_t)u * T] = f16_bits_to_f32(x[u]);
+            }
+        } else {
+            // values at an odd byte offset: read bytewise
+            for (uint32_t e = tid; e < N; e += T) {
+                const uint64_t bw = wds[e >> 6];
+                const uint32_t bit = e & 63u;
+                const uint32_t rk = wpre[e >> 6] + (uint32_t)__popcll(bw & ((1ull << bit) - 1ull));
+                if (((bw >> bit) & 1ull) && rk < nc)
+                    rowf[e] = f16_bits_to_f32((uint32_t)cb[2ull * rk] | ((uint32_t)cb[2ull * rk + 1] << 8));
+            }
+        }
+        __syncthreads();  // the next fragment rewrites wds / wpre
+    }
+}
+
 // One Stockham pass of radix R over the L points in LDS, p = the product
 // of the earlier passes' radices: butterfly i (of L / R) takes points
 // i + j L/R, multiplies point j by w_L^(+-j k L/(p R)) with k = i mod p
@@ -255,21 +359,66 @@ __device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, co
     __syncthreads();
 }
 
-template <bool INV, int MAXB>
+template <bool INV, int MAXB, bool SCAT = false>
 __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
     extern __shared__ float2 buf[];
+    __shared__ uint32_t scan_sm[16];
     const uint32_t N = P.N, L = P.L, T = blockDim.x, tid = threadIdx.x;
     const float *__restrict__ in = P.in + (uint64_t)blockIdx.x * N;
     float *__restrict__ out = P.out + (uint64_t)blockIdx.x * N;
     const float2 *__restrict__ w4 = P.w4;
     const float2 *__restrict__ wn = P.wn;
     const float s0 = sqrtf(1.0f / (float)N), s1 = sqrtf(2.0f / (float)N);
-    // the row's loads are issued kB per thread at a time, before any use
-    constexpr int kB = 4;
-    if (INV) {
-        // Z[k] and Z[L-k] from c[k], c[N-k], c[k+L], c[L-k] for 0 < k < L/2;
-        // k = 0's thread also makes Z[0] (from c[0], c[L]) and the
-        // self-paired Z[L/2] (from c[L/2], c[3L/2])
+    // Z[k] and Z[L-k] from c[k], c[N-k], c[k+L], c[L-k] for 0 < k < L/2;
+    // k = 0's thread also makes Z[0] (from c[0], c[L]) and the self-paired
+    // Z[L/2] (from c[L/2], c[3L/2]); the inputs come as c[k], c[3L/2 or
+    // N-k], c[k+L], c[L/2 or L-k]
+    auto emit = [&](uint32_t k, float a, float b, float d, float e) {
+        const float au = a * (k == 0 ? s0 : s1), bu = b * s1, du = d * s1, eu = e * s1;
+        if (k == 0) {
+            const float2 h0 = make_float2(au, 0.0f);
+            const float2 hl = cmul(tab_at(w4, L), make_float2(0.5f * du, -0.5f * du));
+            buf[0] = cadd(cadd(h0, hl), rot90<true>(csub(h0, hl)));
+            const float2 hm = cmul(tab_at(w4, L / 2), make_float2(0.5f * eu, -0.5f * bu));
+            const float2 hml = cmul(tab_at(w4, 3 * L / 2), make_float2(0.5f * bu, -0.5f * eu));
+            buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(tab_at(w4, N), csub(hm, hml))));
+            return;
+        }
+        const float2 hk = cmul(tab_at(w4, k), make_float2(0.5f * au, -0.5f * bu));
+        const float2 hkl = cmul(tab_at(w4, k + L), make_float2(0.5f * du, -0.5f * eu));
+        buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(tab_at(wn, k), csub(hk, hkl))));
+        const uint32_t k2 = L - k;
+        const float2 h2 = cmul(tab_at(w4, k2), make_float2(0.5f * eu, -0.5f * du));
+        const float2 h2l = cmul(tab_at(w4, N - k), make_float2(0.5f * bu, -0.5f * au));
+        buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(tab_at(wn, k2), csub(h2, h2l))));
+    };
+    if constexpr (SCAT) {
+        // the row built in LDS from the fragments; every thread reads all of
+        // its inputs (L/2 <= kScatK T) before any Z overwrites them
+        float *rowf = reinterpret_cast<float *>(buf);
+        uint64_t *wds = reinterpret_cast<uint64_t *>(buf + L);
+        uint32_t *wpre = reinterpret_cast<uint32_t *>(wds + N / 64u);
+        scatter_row(P, blockIdx.x, rowf, wds, wpre, scan_sm);
+        float a[kScatK], b[kScatK], d[kScatK], e[kScatK];
+#pragma unroll
+        for (uint32_t u = 0; u < kScatK; u++) {
+            const uint32_t k = tid + u * T;
+            if (k < L / 2) {
+                a[u] = rowf[k];
+                b[u] = rowf[k == 0 ? 3 * L / 2 : N - k];
+                d[u] = rowf[k + L];
+                e[u] = rowf[k == 0 ? L / 2 : L - k];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t u = 0; u < kScatK; u++) {
+            const uint32_t k = tid + u * T;
+            if (k < L / 2) emit(k, a[u], b[u], d[u], e[u]);
+        }
+    } else if (INV) {
+        // the row's loads are issued kB per thread at a time, before any use
+        constexpr int kB = 4;
         for (uint32_t k0 = 0; k0 < L / 2; k0 += kB * T) {
             float a[kB], b[kB], d[kB], e[kB];
 #pragma unroll
@@ -285,28 +434,12 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
 #pragma unroll
             for (int u = 0; u < kB; u++) {
                 const uint32_t k = k0 + tid + u * T;
-                if (k >= L / 2) continue;
-                const float au = a[u] * (k == 0 ? s0 : s1), bu = b[u] * s1, du = d[u] * s1, eu = e[u] * s1;
-                if (k == 0) {
-                    const float2 h0 = make_float2(au, 0.0f);
-                    const float2 hl = cmul(tab_at(w4, L), make_float2(0.5f * du, -0.5f * du));
-                    buf[0] = cadd(cadd(h0, hl), rot90<true>(csub(h0, hl)));
-                    const float2 hm = cmul(tab_at(w4, L / 2), make_float2(0.5f * eu, -0.5f * bu));
-                    const float2 hml = cmul(tab_at(w4, 3 * L / 2), make_float2(0.5f * bu, -0.5f * eu));
-                    buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(tab_at(w4, N), csub(hm, hml))));
-                    continue;
-                }
-                const float2 hk = cmul(tab_at(w4, k), make_float2(0.5f * au, -0.5f * bu));
-                const float2 hkl = cmul(tab_at(w4, k + L), make_float2(0.5f * du, -0.5f * eu));
-                buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(tab_at(wn, k), csub(hk, hkl))));
-                const uint32_t k2 = L - k;
-                const float2 h2 = cmul(tab_at(w4, k2), make_float2(0.5f * eu, -0.5f * du));
-                const float2 h2l = cmul(tab_at(w4, N - k), make_float2(0.5f * bu, -0.5f * au));
-                buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(tab_at(wn, k2), csub(h2, h2l))));
+                if (k < L / 2) emit(k, a[u], b[u], d[u], e[u]);
             }
         }
     } else {
         // z[q] = x[4q] + i x[4q+2], z[L-1-q] = x[4q+3] + i x[4q+1]
+        constexpr int kB = 4;
         const float4 *in4 = reinterpret_cast<const float4 *>(in);
         for (uint32_t q0 = 0; q0 < L / 2; q0 += kB * T) {
             float4 v[kB];
@@ -452,7 +585,7 @@ struct Plan {
 bool make_plan(uint32_t N, Plan &P) {
     if (N == 0 || N % 64u != 0) return false;
     const uint32_t L = N / 2;
-    if ((uint64_t)L * 8u > kMaxLds) return false;
+    if ((uint64_t)L * 8u + kStaticLds > kMaxLds) return false;
     uint32_t n = L, nr = 0;
     uint8_t r[16];
     while (n % 8 == 0) r[nr++] = 8, n /= 8;
@@ -478,19 +611,23 @@ bool make_plan(uint32_t N, Plan &P) {
     return true;
 }
 
-template <bool INV, int MAXB>
+template <bool INV, int MAXB, bool SCAT>
 hipError_t launch_rows_t(const FftRows &A, uint32_t rows, uint32_t threads, hipStream_t s) {
-    const uint32_t lds = A.L * 8u;
-    hipError_t e = hipFuncSetAttribute((const void *)dct_fft_rows_kernel<INV, MAXB>,
+    const uint32_t lds = A.L * 8u + (SCAT ? (A.N / 64u) * 12u : 0u);
+    hipError_t e = hipFuncSetAttribute((const void *)dct_fft_rows_kernel<INV, MAXB, SCAT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((dct_fft_rows_kernel<INV, MAXB>), dim3(rows), dim3(threads), lds, s, A);
+    hipLaunchKernelGGL((dct_fft_rows_kernel<INV, MAXB, SCAT>), dim3(rows), dim3(threads), lds, s, A);
     return hipGetLastError();
 }
 
+// The row pass of plan P over `rows` rows; `scat` (an inverse's first pass)
+// supplies the HCT3 fragments in place of `in`.
 hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out, uint32_t rows,
-                       const float2 *tab, hipStream_t s) {
+                       const float2 *tab, hipStream_t s, const FftRows *scat = nullptr) {
     FftRows A;
+    if (scat) A = *scat;
+    else A.nfrag = 0;
     A.in = in;
     A.out = out;
     A.ptab = tab;
@@ -500,14 +637,29 @@ hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out,
     A.L = P.L;
     A.nr = P.nr;
     for (int q = 0; q < 16; q++) A.r[q] = P.r[q];
-    switch (P.maxb | (inverse ? 16 : 0)) {
-        case 1: return launch_rows_t<false, 1>(A, rows, P.threads, s);
-        case 2: return launch_rows_t<false, 2>(A, rows, P.threads, s);
-        case 4: return launch_rows_t<false, 4>(A, rows, P.threads, s);
-        case 17: return launch_rows_t<true, 1>(A, rows, P.threads, s);
-        case 18: return launch_rows_t<true, 2>(A, rows, P.threads, s);
-        default: return launch_rows_t<true, 4>(A, rows, P.threads, s);
+    if (scat) {
+        switch (P.maxb) {
+            case 1: return launch_rows_t<true, 1, true>(A, rows, P.threads, s);
+            case 2: return launch_rows_t<true, 2, true>(A, rows, P.threads, s);
+            default: return launch_rows_t<true, 4, true>(A, rows, P.threads, s);
+        }
     }
+    switch (P.maxb | (inverse ? 16 : 0)) {
+        case 1: return launch_rows_t<false, 1, false>(A, rows, P.threads, s);
+        case 2: return launch_rows_t<false, 2, false>(A, rows, P.threads, s);
+        case 4: return launch_rows_t<false, 4, false>(A, rows, P.threads, s);
+        case 17: return launch_rows_t<true, 1, false>(A, rows, P.threads, s);
+        case 18: return launch_rows_t<true, 2, false>(A, rows, P.threads, s);
+        default: return launch_rows_t<true, 4, false>(A, rows, P.threads, s);
+    }
+}
+
+// Whether plan P's rows can take the fragments in LDS: every thread's
+// pre-step inputs read at once (L/2 <= kScatK threads), one bitmap word per
+// thread, and the row's words and ranks beside the points in LDS.
+bool scat_ok(const Plan &P) {
+    return P.L / 2u <= kScatK * P.threads && P.N / 64u <= P.threads &&
+           (uint64_t)P.L * 8u + (P.N / 64u) * 12u + kStaticLds <= kMaxLds;
 }
 
 hipError_t launch_transpose(const float *in, uint32_t rows, uint32_t cols, int32_t dtype, void *out, hipStream_t s) {
@@ -598,8 +750,9 @@ int32_t fft_scratch(hh_context *ctx, uint64_t total, hipStream_t s, float **a, f
     return HH_OK;
 }
 
-int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
-                  uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s) {
+namespace {
+int32_t dct2d_fft_impl(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
+                       uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s, const FftRows *scat) {
     Plan Pw, Ph;
     if (!make_plan(w, Pw) || !make_plan(h, Ph)) return HH_ERR_UNSUPPORTED;
     if (reinterpret_cast<uintptr_t>(d_out) & (out_dtype == HH_F32 ? 15u : 7u)) return HH_ERR_UNSUPPORTED;
@@ -613,11 +766,52 @@ int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, 
     if (h == w) tw = th;  // the second lookup may have replaced the first's slot
     // rows of length w: in -> b (h x w); b^T -> a (w x h); rows of length h:
     // a -> b (w x h); b^T -> out (h x w), converted
-    hipError_t e = launch_rows(inverse, Pw, d_in, d_b, h, tw, s);
+    hipError_t e = launch_rows(inverse, Pw, d_in, d_b, h, tw, s, scat);
     if (e == hipSuccess) e = launch_transpose(d_b, h, w, HH_F32, d_a, s);
     if (e == hipSuccess) e = launch_rows(inverse, Ph, d_a, d_b, w, th, s);
     if (e == hipSuccess) e = launch_transpose(d_b, w, h, out_dtype, d_out, s);
     return from_hip(e);
+}
+}  // namespace
+
+int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
+                  uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s) {
+    return dct2d_fft_impl(ctx, inverse, d_in, d_a, d_b, h, w, out_dtype, d_out, s, nullptr);
+}
+
+int32_t hct3_decode_fft(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, uint32_t h, uint32_t w,
+                        int32_t dtype, void *d_out, hipStream_t s) {
+    Plan Pw, Ph;
+    if (nfrags == 0 || nfrags > kFftMaxFrags || !make_plan(w, Pw) || !make_plan(h, Ph) || !scat_ok(Pw))
+        return HH_ERR_UNSUPPORTED;
+    if (reinterpret_cast<uintptr_t>(d_out) & (dtype == HH_F32 ? 15u : 7u)) return HH_ERR_UNSUPPORTED;
+    const uint64_t total = (uint64_t)h * w;
+    float *a, *b;
+    int32_t rc = fft_scratch(ctx, total, s, &a, &b);
+    if (rc != HH_OK) return rc;
+    // in a (free until the first pass has run): per fragment its bitmap as
+    // words (total / 8 bytes: w is a multiple of 64) and its row ranks
+    const size_t bits_bytes = (size_t)(total / 8u);
+    const size_t pref_bytes = ((size_t)h * 4u + 255u) & ~(size_t)255u;
+    uint8_t *pa = reinterpret_cast<uint8_t *>(a);
+    FftRows F;
+    F.nfrag = nfrags;
+    for (uint32_t f = 0; f < nfrags; f++) {
+        uint64_t *bits = reinterpret_cast<uint64_t *>(pa + f * (bits_bytes + pref_bytes));
+        uint32_t *pref = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(bits) + bits_bytes);
+        hipError_t e = launch_pack_bits(frags[f].bitmap, bits_bytes, bits, s);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(row_counts_kernel, dim3((h + 3u) / 4u), dim3(256), 0, s, bits, w / 64u, h, pref);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = launch_scan_counts(pref, h, s);
+        if (e != hipSuccess) return from_hip(e);
+        F.fbits[f] = bits;
+        F.fpref[f] = pref;
+        F.fcoef[f] = frags[f].coef;
+        F.fncoef[f] = frags[f].ncoef;
+    }
+    return dct2d_fft_impl(ctx, true, nullptr, a, b, h, w, dtype, d_out, s, &F);
 }
 
 void release_fft_resources(hh_context *ctx) {

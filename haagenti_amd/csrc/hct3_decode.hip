@@ -386,6 +386,12 @@ hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t 
     return hipGetLastError();
 }
 
+hipError_t launch_scan_counts(uint32_t *d, uint32_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(1024), 0, s, d, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_words, hipStream_t s) {
     const uint64_t nwords = (nbytes + 7) / 8;
     if (nwords == 0) return hipSuccess;
@@ -587,9 +593,12 @@ int32_t hct3_decode_eo(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, 
     uint32_t *d_sums = reinterpret_cast<uint32_t *>(d_stage);
     uint64_t *d_bits = reinterpret_cast<uint64_t *>(d_stage + ((hct3_block_sums_bytes(total) + 15u) & ~(size_t)15));
     if (use_fft(ctx, h, w)) {
-        // the fragments scattered into an f32 matrix, then the FFT route
+        // the fragments scattered into the first row pass in LDS, or where
+        // its limits do not allow that into an f32 matrix, then the FFT route
+        int32_t rc = hct3_decode_fft(ctx, frags, nfrags, h, w, dtype, d_out, s);
+        if (rc != HH_ERR_UNSUPPORTED) return rc;
         float *a, *b;
-        int32_t rc = fft_scratch(ctx, total, s, &a, &b);
+        rc = fft_scratch(ctx, total, s, &a, &b);
         if (rc != HH_OK) return rc;
         for (uint32_t i = 0; i < nfrags; i++) {
             hipError_t e = launch_pack_bits(frags[i].bitmap, (total + 7) / 8, d_bits, s);

@@ -214,6 +214,8 @@ hipError_t launch_hct3_scatter(const uint64_t *d_bits, uint64_t nbits, uint32_t 
 size_t hct3_block_sums_bytes(uint64_t nbits);
 // Bitmap bytes at any device address -> zero-padded 64-bit words.
 hipError_t launch_pack_bits(const uint8_t *d_src, uint64_t nbytes, uint64_t *d_words, hipStream_t s);
+// In-place exclusive scan of n 32-bit counts (one workgroup).
+hipError_t launch_scan_counts(uint32_t *d, uint32_t n, hipStream_t s);
 hipError_t launch_f32_convert(const float *d_x, uint64_t n, int dtype, void *d_out, hipStream_t s);
 // One HCT3 fragment in device memory: its bitmap bytes and its f16
 // coefficient values (both at any byte address).
@@ -305,6 +307,13 @@ int32_t fft_scratch(hh_context *ctx, uint64_t total, hipStream_t s, float **a, f
 int32_t dct2d_fft(hh_context *ctx, bool inverse, const float *d_in, float *d_a, float *d_b, uint32_t h,
                   uint32_t w, int32_t out_dtype, void *d_out, hipStream_t s);
 void release_fft_resources(hh_context *ctx);
+// The h x w HCT3 decode on the FFT route with the fragments scattered in
+// order (HCT3 rules) straight into the first row pass's LDS; d_out as for
+// dct2d_fft.  HH_ERR_UNSUPPORTED (nothing launched) when the shape or
+// fragment count leaves that fused pass's limits (more than 16 fragments,
+// a row's inputs past 8 per thread or past the LDS).
+int32_t hct3_decode_fft(hh_context *ctx, const Hct3Frag *frags, uint32_t nfrags, uint32_t h, uint32_t w,
+                        int32_t dtype, void *d_out, hipStream_t s);
 // zstd::decode_all on the host (host_zstd.cpp): false on a malformed stream.
 bool zstd_decode_all(const uint8_t *in, size_t len, std::vector<uint8_t> &out);
 

@@ -251,6 +251,38 @@ def test_fft_route_matches_dense_route_4096():
     assert np.array_equal(out.cpu().numpy().view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("odd", [False, True])
+def test_fft_route_fragments_scattered_in_the_first_pass(odd):
+    # on the FFT route the first row pass builds each row from the fragments
+    # in LDS: three fragments, the second overwriting part of the first, the
+    # third running out of values; values 2-byte aligned, or read bytewise
+    # when the container sits at an odd device address -- against the oracle
+    # and the dense route
+    T = G.torch()
+    rng = np.random.default_rng(777 + int(odd))
+    shape = (1024, 1536)
+    total = shape[0] * shape[1]
+    bm2, v2, _ = random_fragment(rng, total, 0.02)
+    data = container([random_fragment(rng, total, 0.2), random_fragment(rng, total, 0.05),
+                      (bm2, v2[: v2.size // 2], None)])
+    rc, ref = O.hct3_decode(data, shape)
+    assert rc == O.OK
+    with route("dense"):
+        dense = dec().decompress_to_gpu(data, shape).cpu().numpy()
+    raw = np.frombuffer(data, np.uint8)
+    buf = np.zeros(raw.size + 1, np.uint8)
+    buf[int(odd):int(odd) + raw.size] = raw
+    d_buf = G.dev(buf)
+    out = T.empty(total, dtype=T.float32, device="cuda")
+    with route("fft"):
+        dec().decompress_device(data, d_buf[int(odd):], shape, out, stream=G.stream())
+        G.sync()
+    got = out.cpu().numpy()
+    e_ref, e_dense = rel_err(got, ref), rel_err(got, dense)
+    print(f"[hct3] fused scatter (odd={odd}): max|fft - oracle| = {e_ref:.2e}, |fft - dense| = {e_dense:.2e} x RMS")
+    assert e_ref <= 1e-5 and e_dense <= 2e-5
+
+
 @pytest.mark.usefixtures("dense_route")
 def test_decompress_even_odd_split_vs_oracle_and_16bit():
     # a 1024 x 512 HCT3 tensor: the split inverse against the oracle, and its
