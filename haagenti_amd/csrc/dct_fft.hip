@@ -48,6 +48,11 @@ struct FftRows {
     const float2 *ptab;
     const float2 *w4;
     const float2 *wn;
+    // the inverse pre-step's combined factors for k < L: alpha_k =
+    // s1 w_4N^k (1 + i w_N^k) / 2, beta_k = s1 w_4N^(k+L) (1 - i w_N^k) / 2
+    // (x, y = alpha; z, w = beta), so that Z[k] = alpha_k (c[k] - i c[N-k])
+    // + beta_k (c[k+L] - i c[L-k]) with the inputs unscaled
+    const float4 *ab;
     uint32_t N, L;
     uint32_t nr;
     uint8_t r[16];
@@ -373,24 +378,24 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
     // k = 0's thread also makes Z[0] (from c[0], c[L]) and the self-paired
     // Z[L/2] (from c[L/2], c[3L/2]); the inputs come as c[k], c[3L/2 or
     // N-k], c[k+L], c[L/2 or L-k]
+    // (a - i b) scaled by the factor f: (f.x a + f.y b, f.y a - f.x b)
+    auto fm = [](float fx, float fy, float a, float b) {
+        return make_float2(__builtin_fmaf(fx, a, fy * b), __builtin_fmaf(fy, a, -(fx * b)));
+    };
+    const float4 *__restrict__ ab = P.ab;
     auto emit = [&](uint32_t k, float a, float b, float d, float e) {
-        const float au = a * (k == 0 ? s0 : s1), bu = b * s1, du = d * s1, eu = e * s1;
         if (k == 0) {
-            const float2 h0 = make_float2(au, 0.0f);
-            const float2 hl = cmul(tab_at(w4, L), make_float2(0.5f * du, -0.5f * du));
-            buf[0] = cadd(cadd(h0, hl), rot90<true>(csub(h0, hl)));
-            const float2 hm = cmul(tab_at(w4, L / 2), make_float2(0.5f * eu, -0.5f * bu));
-            const float2 hml = cmul(tab_at(w4, 3 * L / 2), make_float2(0.5f * bu, -0.5f * eu));
-            buf[L / 2] = cadd(cadd(hm, hml), rot90<true>(cmul(tab_at(w4, N), csub(hm, hml))));
+            // Z[0] = s0 c[0] (1 + i) + beta_0 (c[L] - i c[L]);
+            // Z[L/2] = alpha_{L/2} (c[L/2] - i c[3L/2]) + beta_{L/2} (c[3L/2] - i c[L/2])
+            const float4 f0 = ab[0], fm2 = ab[L / 2];
+            const float as = a * s0;
+            buf[0] = cadd(make_float2(as, as), fm(f0.z, f0.w, d, d));
+            buf[L / 2] = cadd(fm(fm2.x, fm2.y, e, b), fm(fm2.z, fm2.w, b, e));
             return;
         }
-        const float2 hk = cmul(tab_at(w4, k), make_float2(0.5f * au, -0.5f * bu));
-        const float2 hkl = cmul(tab_at(w4, k + L), make_float2(0.5f * du, -0.5f * eu));
-        buf[k] = cadd(cadd(hk, hkl), rot90<true>(cmul(tab_at(wn, k), csub(hk, hkl))));
-        const uint32_t k2 = L - k;
-        const float2 h2 = cmul(tab_at(w4, k2), make_float2(0.5f * eu, -0.5f * du));
-        const float2 h2l = cmul(tab_at(w4, N - k), make_float2(0.5f * bu, -0.5f * au));
-        buf[k2] = cadd(cadd(h2, h2l), rot90<true>(cmul(tab_at(wn, k2), csub(h2, h2l))));
+        const float4 fk = ab[k], fk2 = ab[L - k];
+        buf[k] = cadd(fm(fk.x, fk.y, a, b), fm(fk.z, fk.w, d, e));
+        buf[L - k] = cadd(fm(fk2.x, fk2.y, e, d), fm(fk2.z, fk2.w, b, a));
     };
     if constexpr (SCAT) {
         // the row built in LDS from the fragments; every thread reads all of
@@ -543,7 +548,8 @@ struct TabPlan {
 };
 constexpr uint32_t tab_w4(uint32_t L) { return L; }              // after the pass tables (L - 1, one pad)
 constexpr uint32_t tab_wn(uint32_t L, uint32_t N) { return L + N + 1; }
-constexpr uint32_t tab_len(uint32_t L, uint32_t N) { return L + N + 1 + L; }
+constexpr uint32_t tab_ab(uint32_t L, uint32_t N) { return 2 * L + N + 2; }  // 16-byte aligned (one pad)
+constexpr uint32_t tab_len(uint32_t L, uint32_t N) { return tab_ab(L, N) + 2 * L; }
 
 __global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ tab, TabPlan P) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
@@ -566,8 +572,19 @@ __global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ ta
         }
     } else if (i < tab_wn(L, N)) {
         sincospi((double)(i - L) / (2.0 * (double)N), &s, &c);
-    } else {
+    } else if (i < tab_wn(L, N) + L) {
         sincospi(2.0 * (double)(i - tab_wn(L, N)) / (double)N, &s, &c);
+    } else if (i >= tab_ab(L, N)) {
+        // alpha_k (even entry) or beta_k (odd entry)
+        const uint32_t k = (i - tab_ab(L, N)) >> 1, beta = (i - tab_ab(L, N)) & 1u;
+        double s4, c4, sn, cn;
+        sincospi((double)(k + (beta ? L : 0u)) / (2.0 * (double)N), &s4, &c4);  // w_4N^(k or k+L)
+        sincospi(2.0 * (double)k / (double)N, &sn, &cn);                          // w_N^k
+        // (1 + i w_N^k) = (1 - sn, cn); (1 - i w_N^k) = (1 + sn, -cn)
+        const double fr = beta ? 1.0 + sn : 1.0 - sn, fi = beta ? -cn : cn;
+        const double h = 0.5 * sqrt(2.0 / (double)N);
+        c = h * (c4 * fr - s4 * fi);
+        s = h * (c4 * fi + s4 * fr);
     }
     tab[i] = make_float2((float)c, (float)s);
 }
@@ -633,6 +650,7 @@ hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out,
     A.ptab = tab;
     A.w4 = tab + tab_w4(P.L);
     A.wn = tab + tab_wn(P.L, P.N);
+    A.ab = reinterpret_cast<const float4 *>(tab + tab_ab(P.L, P.N));
     A.N = P.N;
     A.L = P.L;
     A.nr = P.nr;
