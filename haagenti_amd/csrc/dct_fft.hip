@@ -56,6 +56,11 @@ struct FftRows {
     uint32_t N, L;
     uint32_t nr;
     uint8_t r[16];
+    // LDS layout of the L points: point x at x + (x >> psh), one pad slot
+    // per 32 points (psh = 5, when L is a multiple of 256) so that the
+    // strided writes of the first passes spread over the banks, or none
+    // (psh = 31)
+    uint32_t psh;
     // HCT3 fragments scattered into the rows in LDS (the fused first pass of
     // an inverse; `in` unused): fragment f's bitmap as 64-bit words, the
     // rank of each row's first bit, its f16 values and their count
@@ -311,7 +316,8 @@ __device__ __forceinline__ void scatter_row(const FftRows &P, uint32_t row, floa
 // (i - k) R + k + j p.  All inputs are read before the barrier, so the
 // pass runs in place.
 template <int R, int MAXB, bool INV>
-__device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, const float2 *__restrict__ ptab) {
+__device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, const float2 *__restrict__ ptab,
+                                         uint32_t psh) {
     // the twiddles are loaded with the pass's LDS reads, before the barrier,
     // where the registers allow; the first pass (p = 1) has none
     constexpr bool kPre = MAXB * (R - 1) <= 16;
@@ -325,12 +331,18 @@ __device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, co
     auto mod_p = [&](uint32_t i) { return i - (uint32_t)(((float)i + 0.5f) * invp) * p; };
     float2 x[MAXB][R];
     float2 w[kPre ? MAXB : 1][R - 1];
+    // padded layout: point i + j nb at pad(i) + j (nb + nb / 32), point
+    // base + j p at pad(base) + j p + j p / 32 (nb and, past the first
+    // passes, p are multiples of 32 when padded; the first passes' p R
+    // divides 32)
+    const uint32_t rstep = nb + (nb >> psh);
 #pragma unroll
     for (int b = 0; b < MAXB; b++) {
         const uint32_t i = tid + b * T;
         if (i < nb) {
+            const uint32_t ri = i + (i >> psh);
 #pragma unroll
-            for (int j = 0; j < R; j++) x[b][j] = buf[i + j * nb];
+            for (int j = 0; j < R; j++) x[b][j] = buf[ri + j * rstep];
             if (kPre && tw) {
                 uint32_t off[R];
                 twiddle_offsets<R>(mod_p(i), p, off);
@@ -357,8 +369,9 @@ __device__ __forceinline__ void fft_pass(float2 *buf, uint32_t L, uint32_t p, co
             }
             Dft<R, INV>::run(x[b]);
             const uint32_t base = (i - k) * R + k;
+            const uint32_t wb = base + (base >> psh);
 #pragma unroll
-            for (int j = 0; j < R; j++) buf[base + j * p] = x[b][j];
+            for (int j = 0; j < R; j++) buf[wb + j * p + ((j * p) >> psh)] = x[b][j];
         }
     }
     __syncthreads();
@@ -374,6 +387,8 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
     const float2 *__restrict__ w4 = P.w4;
     const float2 *__restrict__ wn = P.wn;
     const float s0 = sqrtf(1.0f / (float)N), s1 = sqrtf(2.0f / (float)N);
+    const uint32_t psh = P.psh;
+    auto pd = [psh](uint32_t x) { return x + (x >> psh); };  // LDS slot of point x
     // Z[k] and Z[L-k] from c[k], c[N-k], c[k+L], c[L-k] for 0 < k < L/2;
     // k = 0's thread also makes Z[0] (from c[0], c[L]) and the self-paired
     // Z[L/2] (from c[L/2], c[3L/2]); the inputs come as c[k], c[3L/2 or
@@ -390,18 +405,18 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
             const float4 f0 = ab[0], fm2 = ab[L / 2];
             const float as = a * s0;
             buf[0] = cadd(make_float2(as, as), fm(f0.z, f0.w, d, d));
-            buf[L / 2] = cadd(fm(fm2.x, fm2.y, e, b), fm(fm2.z, fm2.w, b, e));
+            buf[pd(L / 2)] = cadd(fm(fm2.x, fm2.y, e, b), fm(fm2.z, fm2.w, b, e));
             return;
         }
         const float4 fk = ab[k], fk2 = ab[L - k];
-        buf[k] = cadd(fm(fk.x, fk.y, a, b), fm(fk.z, fk.w, d, e));
-        buf[L - k] = cadd(fm(fk2.x, fk2.y, e, d), fm(fk2.z, fk2.w, b, a));
+        buf[pd(k)] = cadd(fm(fk.x, fk.y, a, b), fm(fk.z, fk.w, d, e));
+        buf[pd(L - k)] = cadd(fm(fk2.x, fk2.y, e, d), fm(fk2.z, fk2.w, b, a));
     };
     if constexpr (SCAT) {
         // the row built in LDS from the fragments; every thread reads all of
         // its inputs (L/2 <= kScatK T) before any Z overwrites them
         float *rowf = reinterpret_cast<float *>(buf);
-        uint64_t *wds = reinterpret_cast<uint64_t *>(buf + L);
+        uint64_t *wds = reinterpret_cast<uint64_t *>(buf + pd(L - 1) + 1);
         uint32_t *wpre = reinterpret_cast<uint32_t *>(wds + N / 64u);
         scatter_row(P, blockIdx.x, rowf, wds, wpre, scan_sm);
         float a[kScatK], b[kScatK], d[kScatK], e[kScatK];
@@ -457,8 +472,8 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
             for (int u = 0; u < kB; u++) {
                 const uint32_t q = q0 + tid + u * T;
                 if (q < L / 2) {
-                    buf[q] = make_float2(v[u].x, v[u].z);
-                    buf[L - 1 - q] = make_float2(v[u].w, v[u].y);
+                    buf[pd(q)] = make_float2(v[u].x, v[u].z);
+                    buf[pd(L - 1 - q)] = make_float2(v[u].w, v[u].y);
                 }
             }
         }
@@ -467,12 +482,12 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
     uint32_t p = 1, poff = 0;
     for (uint32_t q = 0; q < P.nr; q++) {
         switch (P.r[q]) {
-            case 8: fft_pass<8, MAXB, INV>(buf, L, p, P.ptab + poff); break;
-            case 4: fft_pass<4, MAXB, INV>(buf, L, p, P.ptab + poff); break;
-            case 2: fft_pass<2, MAXB, INV>(buf, L, p, P.ptab + poff); break;
-            case 3: fft_pass<3, MAXB, INV>(buf, L, p, P.ptab + poff); break;
-            case 5: fft_pass<5, MAXB, INV>(buf, L, p, P.ptab + poff); break;
-            default: fft_pass<7, MAXB, INV>(buf, L, p, P.ptab + poff); break;
+            case 8: fft_pass<8, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
+            case 4: fft_pass<4, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
+            case 2: fft_pass<2, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
+            case 3: fft_pass<3, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
+            case 5: fft_pass<5, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
+            default: fft_pass<7, MAXB, INV>(buf, L, p, P.ptab + poff, psh); break;
         }
         poff += p * (P.r[q] - 1u);
         p *= P.r[q];
@@ -481,7 +496,7 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
         // x[4q .. 4q+3] = Re z[q], Im z[L-1-q], Im z[q], Re z[L-1-q]
         float4 *out4 = reinterpret_cast<float4 *>(out);
         for (uint32_t q = tid; q < L / 2; q += T) {
-            const float2 za = buf[q], zb = buf[L - 1 - q];
+            const float2 za = buf[pd(q)], zb = buf[pd(L - 1 - q)];
             out4[q] = make_float4(za.x, zb.y, za.y, zb.x);
         }
     } else {
@@ -491,8 +506,8 @@ __global__ __launch_bounds__(1024) void dct_fft_rows_kernel(FftRows P) {
             for (int h = 0; h < 2; h++) {
                 const uint32_t kk = h == 0 ? k : L - k;
                 if (h == 1 && 2 * k == L) break;
-                const float2 zk = buf[kk == L ? 0 : kk];
-                const float2 zc = cconj(buf[kk == 0 ? 0 : L - kk]);
+                const float2 zk = buf[pd(kk == L ? 0 : kk)];
+                const float2 zc = cconj(buf[pd(kk == 0 ? 0 : L - kk)]);
                 const float2 E = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y + zc.y));
                 const float2 D = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y - zc.y));
                 const float2 wq = kk == L ? make_float2(-1.0f, 0.0f) : cconj(tab_at(wn, kk));
@@ -590,9 +605,12 @@ __global__ __launch_bounds__(256) void fft_tables_kernel(float2 *__restrict__ ta
 }
 
 struct Plan {
-    uint32_t N = 0, L = 0, threads = 0, maxb = 0, nr = 0;
+    uint32_t N = 0, L = 0, threads = 0, maxb = 0, nr = 0, psh = 31;
     uint8_t r[16] = {};
 };
+// LDS slots of L points in the layout of shift psh (one pad slot per 32
+// points when psh = 5)
+constexpr uint32_t slots_of(uint32_t L, uint32_t psh) { return L + (psh == 5u ? L / 32u : 0u); }
 
 // Radices of L (8s, then 4 or 2, then 3, 5, 7), the workgroup size and
 // the butterflies per thread of the widest pass; false when N is not a
@@ -602,7 +620,10 @@ struct Plan {
 bool make_plan(uint32_t N, Plan &P) {
     if (N == 0 || N % 64u != 0) return false;
     const uint32_t L = N / 2;
-    if ((uint64_t)L * 8u + kStaticLds > kMaxLds) return false;
+    // the padded layout when every pass keeps its strides multiples of 32
+    // (L a multiple of 256)
+    const uint32_t psh = L % 256u == 0 ? 5u : 31u;
+    if ((uint64_t)slots_of(L, psh) * 8u + kStaticLds > kMaxLds) return false;
     uint32_t n = L, nr = 0;
     uint8_t r[16];
     while (n % 8 == 0) r[nr++] = 8, n /= 8;
@@ -621,6 +642,7 @@ bool make_plan(uint32_t N, Plan &P) {
     if (mb > 4) return false;
     P.N = N;
     P.L = L;
+    P.psh = psh;
     P.threads = T;
     P.maxb = mb <= 1 ? 1 : mb <= 2 ? 2 : 4;
     P.nr = nr;
@@ -630,7 +652,7 @@ bool make_plan(uint32_t N, Plan &P) {
 
 template <bool INV, int MAXB, bool SCAT>
 hipError_t launch_rows_t(const FftRows &A, uint32_t rows, uint32_t threads, hipStream_t s) {
-    const uint32_t lds = A.L * 8u + (SCAT ? (A.N / 64u) * 12u : 0u);
+    const uint32_t lds = slots_of(A.L, A.psh) * 8u + (SCAT ? (A.N / 64u) * 12u : 0u);
     hipError_t e = hipFuncSetAttribute((const void *)dct_fft_rows_kernel<INV, MAXB, SCAT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
@@ -653,6 +675,7 @@ hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out,
     A.ab = reinterpret_cast<const float4 *>(tab + tab_ab(P.L, P.N));
     A.N = P.N;
     A.L = P.L;
+    A.psh = P.psh;
     A.nr = P.nr;
     for (int q = 0; q < 16; q++) A.r[q] = P.r[q];
     if (scat) {
@@ -677,7 +700,7 @@ hipError_t launch_rows(bool inverse, const Plan &P, const float *in, float *out,
 // thread, and the row's words and ranks beside the points in LDS.
 bool scat_ok(const Plan &P) {
     return P.L / 2u <= kScatK * P.threads && P.N / 64u <= P.threads &&
-           (uint64_t)P.L * 8u + (P.N / 64u) * 12u + kStaticLds <= kMaxLds;
+           (uint64_t)slots_of(P.L, P.psh) * 8u + (P.N / 64u) * 12u + kStaticLds <= kMaxLds;
 }
 
 hipError_t launch_transpose(const float *in, uint32_t rows, uint32_t cols, int32_t dtype, void *out, hipStream_t s) {
