@@ -14,7 +14,11 @@
  * pool; it is not thread-safe (one context per host thread), matching
  * GpuDctContext / GpuContext (crates/haagenti-cuda/src/lib.rs:99-108).
  * Device entry points are asynchronous on the given stream; results are
- * valid after that stream is synchronised.  Host-pointer entry points are
+ * valid after that stream is synchronised.  A context's device scratch
+ * (LZ4 scratch, whole-matrix transform buffers and tables) is shared by its
+ * calls, so the asynchronous calls of one context must be ordered: the
+ * same stream, or a synchronisation between calls made on different
+ * streams.  Host-pointer entry points are
  * synchronous.  Every entry point makes the context's device current while
  * it runs and restores the calling thread's current device before it
  * returns.
