@@ -169,6 +169,7 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
 constexpr int kMaxTensors = 8;
+static_assert((kMaxTensors & (kMaxTensors - 1)) == 0 && kMaxTensors <= 64, "tensor_of reads one start per lane");
 // Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs with
 // at most 2 KiB of tile bytes prefetched (168 registers, no spills; the LDS
 // also fits 3 workgroups per CU), else 2.
@@ -191,16 +192,14 @@ struct TileBatch {
     int32_t neg4;
 };
 
-// The tensor holding batch tile gt (wave-uniform): the count of tensor
-// starts after the first at or below gt (the starts ascend).  The loads are
-// independent, so they overlap instead of taking one LDS round trip per
-// tensor passed.
-__device__ __forceinline__ uint32_t tensor_of(const TileBatch &B, uint32_t gt) {
-    const uint32_t n = uniform(B.n);
-    uint32_t ti = 0;
-#pragma unroll
-    for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += (j < n && gt >= uniform(B.start[j])) ? 1u : 0u;
-    return ti;
+// The tensor holding batch tile gt (wave-uniform; every lane active): the
+// count of tensor starts after the first at or below gt.  The starts ascend,
+// start[n] is the tile total and the unused ones past it are all-ones, so no
+// start past tensor n - 1 counts.  Lane j compares start[j]: one LDS read
+// and a ballot.
+__device__ __forceinline__ uint32_t tensor_of(const TileBatch &B, uint32_t gt, int lane) {
+    const uint32_t s = B.start[lane & (kMaxTensors - 1)];
+    return (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(gt >= s) & (((1ull << kMaxTensors) - 1ull) & ~1ull));
 }
 
 // Workgroup LDS layout: [zero word][batch descriptor][M fragment table][per-wave areas].
@@ -215,7 +214,7 @@ constexpr uint32_t kBatchBytes = (sizeof(TileBatch) + 15u) & ~15u;
 constexpr uint32_t kMTabOff = kBatchOff + kBatchBytes;
 constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 
-// Loads the bytes of global tile gt into registers, 16 bytes per lane per
+// Loads the bytes of global tile gt (of tensor ti) into registers, 16 bytes per lane per
 // KiB, always issuing NP loads (NP KiB cover the tile) so that the wait
 // counts stay static.  DW: every tile of the batch starts 4-byte aligned and
 // has a size divisible by 4; register chunk i holds tile bytes
@@ -227,9 +226,8 @@ constexpr uint32_t kSharedBytes = kMTabOff + kMTabBytes;
 // inside the tensor's tile bytes, bytes one by one where it would leave them
 // (the tensor's first and last chunks), anything for chunks past the tile.
 template <bool DW, int NP>
-__device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, int lane,
+__device__ __forceinline__ void prefetch_tile(const TileBatch &B, uint32_t gt, uint32_t ti, int lane,
                                               u32x4 (&pf)[NP]) {
-    const uint32_t ti = tensor_of(B, gt);
     const uint32_t tb = uniform(B.tb[ti]), st = uniform(B.start[ti]), sn = uniform(B.start[ti + 1]);
     const uint64_t s0 = uniform((uint64_t)(uintptr_t)B.tiles[ti]);
     g_u8 *src = (g_u8 *)(uintptr_t)s0 + (size_t)(gt - st) * tb;
@@ -591,14 +589,18 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
     const uint32_t stride = gridDim.x * kWaves;
     u32x4 pf[NP];
     uint32_t gt = blockIdx.x * kWaves + wave;
+    // tensor of the tile staged next (looked up once per tile, when its
+    // bytes are fetched)
+    uint32_t ti_next = 0;
     if (gt < ntiles) {
-        prefetch_tile<DW, NP>(B, gt, lane, pf);
+        ti_next = tensor_of(B, gt, lane);
+        prefetch_tile<DW, NP>(B, gt, ti_next, lane, pf);
 #pragma unroll
         for (int i = 0; i < NP; i++)
             *reinterpret_cast<u32x4 *>(smem + pbase + 16 * (lane + 64 * i)) = pf[i];
     }
     for (; gt < ntiles; gt += stride) {
-        const uint32_t ti = tensor_of(B, gt);
+        const uint32_t ti = ti_next;
         const uint32_t t = gt - uniform(B.start[ti]);
 
         // This tile's bytes are staged in LDS.  Fetch the next tile now; it is
@@ -606,7 +608,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
         // and before this tile's output stores are issued (the wait counter
         // is in order, so stores issued earlier would have to drain first).
         const bool has_next = gt + stride < ntiles;
-        prefetch_tile<DW, NP>(B, has_next ? gt + stride : gt, lane, pf);
+        const uint32_t gn = has_next ? gt + stride : gt;
+        ti_next = has_next ? tensor_of(B, gn, lane) : ti;
+        prefetch_tile<DW, NP>(B, gn, ti_next, lane, pf);
         wave_sync();
 
         tile_body<DT, false, false, true>(B, ti, t, pay + tile_shift<DW>(B, ti, t), V, wbase, mtab, lane, one, n4, [&]() {
@@ -798,11 +802,11 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // block lb -> tensor, first tile, tile count
     auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
         // the count of tensor first blocks after the first at or below lb
-        // (independent loads, as in tensor_of)
-        const uint32_t n = uniform(B.n);
+        // (the unused entries past blk_start[n] are all-ones; no branches,
+        // so the loads overlap)
         ti = 0;
 #pragma unroll
-        for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += (j < n && lb >= uniform(F.blk_start[j])) ? 1u : 0u;
+        for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += lb >= uniform(F.blk_start[j]) ? 1u : 0u;
         const uint32_t tpb_i = uniform(F.tpb[ti]);
         t0 = (lb - uniform(F.blk_start[ti])) * tpb_i;
         nt = min(tpb_i, uniform(B.start[ti + 1]) - uniform(B.start[ti]) - t0);
@@ -1163,6 +1167,7 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
         }
         if (B.n == 0) continue;
         B.start[B.n] = total;
+        for (uint32_t j = B.n + 1; j <= (uint32_t)kMaxTensors; j++) B.start[j] = 0xffffffffu;
         B.one = 1.0f;
         B.neg4 = -4;
         // per wave: the V table (k words) shares space with the parked output
@@ -1265,6 +1270,7 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
         if (B.n == 0) continue;
         B.start[B.n] = total;
         F.blk_start[B.n] = nb;
+        for (uint32_t j = B.n + 1; j <= (uint32_t)kMaxTensors; j++) B.start[j] = F.blk_start[j] = 0xffffffffu;
         B.one = 1.0f;
         B.neg4 = -4;
         // per wave: the V table shares space with the parked output tile, and
