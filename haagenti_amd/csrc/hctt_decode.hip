@@ -652,11 +652,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd(DT, NP)) void hctt_decode_k
 //   state[x]  (64 bits) 1 + the slot of the block the buffer holds, and
 //             the bytes of it decoded so far (published after LZ4
 //             sequences; the whole block only by its final store);
-//   done[x]   how many of that block's tiles have been read.  Slot i may
-//             take buffer x once state[x] names slot i - nbuf (placed there
-//             by another wave, possibly late) and done[x] equals that
-//             block's tile count; its decoder clears done[x] before
-//             publishing slot i.
+//   done[x]   how many of that block's tiles are still to be read (its
+//             decoder sets the block's tile count before publishing slot
+//             i; every tile read takes one off).  Slot i may take buffer x
+//             once state[x] names slot i - nbuf (placed there by another
+//             wave, possibly late) and done[x] is 0.
 // A tile is decoded as soon as the published bytes cover it.  Two LDS
 // bitmaps over the workgroup's slots record which are complete and which
 // failed.  A failed block's decoder zeroes its buffer from the first tile it
@@ -796,6 +796,9 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // kernel arguments, where the compiler knows them to be global
     const FusedBlocks &F = *reinterpret_cast<const FusedBlocks *>(smem + kFusedFOff);
     const uint32_t nw = nthr >> 6, nbuf = Fk.nbuf;
+    // slot q's buffer, q mod nbuf without a division (exact: q < 2^22)
+    const float nbuf_inv = 1.0f / (float)nbuf;
+    auto buf_of = [&](uint32_t q) { return q - nbuf * uniform((uint32_t)(((float)q + 0.5f) * nbuf_inv)); };
     auto state_w = [](uint32_t x) { return kFusedStateOff + 8u * x; };
     auto done_w = [](uint32_t x) { return kFusedDoneOff + 4u * x; };
 
@@ -862,15 +865,20 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     uint8_t *stage = smem + wbase + FusedRing::kSFront;
     uint32_t *V = reinterpret_cast<uint32_t *>(smem + wbase);
 
-    // may slot q take its buffer now?  (once true, true until q is placed)
+    // may slot q take its buffer now?  (once true, true until q is placed.)
+    // A probe with both words read at once: decode() waits on them again
+    // with acquire loads before it touches the buffer.  The state is read
+    // first (one wave's LDS reads are performed in order, and the count is
+    // set before the state names its slot).
     auto buf_free = [&](uint32_t q) {
         if (q < nbuf) return true;
-        const uint32_t x = q % nbuf;
-        const uint64_t sv = uniform(lds_load_acq(state_w(x), uint64_t{}));
-        if ((uint32_t)(sv >> 32) != q - nbuf + 1u) return false;
-        uint32_t pti, pt0, pnt;
-        locate(lb_of(q - nbuf), pti, pt0, pnt);
-        return uniform(lds_load_acq(done_w(x), uint32_t{})) == pnt;
+        const uint32_t x = buf_of(q);
+        const uint64_t sv =
+            __hip_atomic_load((lds_dword *)(size_t)state_w(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        asm volatile("" ::: "memory");
+        const uint32_t rem =
+            __hip_atomic_load((lds_word *)(size_t)done_w(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return (uint32_t)(uniform(sv) >> 32) == q - nbuf + 1u && uniform(rem) == 0u;
     };
     // the next slot to claim (the word counts the slots claimed)
     auto next_block = [&]() {
@@ -889,27 +897,26 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // waiting for the buffer; false when a wait ran out
     auto decode = [&](uint32_t q) {
         const int ln = opaque_lane();
-        const uint32_t x = q % nbuf;
+        const uint32_t x = buf_of(q);
         if (q >= nbuf) {
             // the buffer's previous block (slot q - nbuf, possibly placed late
             // by another wave) must have been placed there, then read: its
-            // done count is only meaningful once its stamp is up
-            uint32_t pti, pt0, pnt, v;
+            // count is only meaningful once its stamp is up
+            uint32_t v;
             uint64_t sv;
-            locate(lb_of(q - nbuf), pti, pt0, pnt);
             if (!fused_poll(state_w(x), ln, Fk.spin_limit, sv,
                             [&](uint64_t s) { return (uint32_t)(s >> 32) == q - nbuf + 1u; }) ||
-                !fused_poll(done_w(x), ln, Fk.spin_limit, v, [&](uint32_t c) { return c == pnt; }))
+                !fused_poll(done_w(x), ln, Fk.spin_limit, v, [&](uint32_t c) { return c == 0u; }))
                 return false;
-        }
-        const uint64_t stamp = (uint64_t)(q + 1u) << 32;
-        if (ln == 0) {
-            __hip_atomic_store((lds_word *)(size_t)done_w(x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         const uint32_t lb = lb_of(q);
         uint32_t ti, t0, nt;
         locate(lb, ti, t0, nt);
+        const uint64_t stamp = (uint64_t)(q + 1u) << 32;
+        if (ln == 0) {
+            __hip_atomic_store((lds_word *)(size_t)done_w(x), nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         const uint32_t tb = uniform(B.tb[ti]);
         const uint32_t cap = nt * tb;
         uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
@@ -1002,20 +1009,20 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     // per block + the waves' last claims)
     const float tpb_inv = 1.0f / (float)tpb;
     // the block of the wave's last tile (a wave usually takes several tiles
-    // of one block in a row)
-    uint32_t cq = ~0u, cti = 0, ct0 = 0, cnt = 0;
+    // of one block in a row): its tensor, first tile, tile count and tile
+    // bytes, and the bytes of it seen published (the state's low word,
+    // read with acquire by this wave)
+    uint32_t cq = ~0u, cti = 0, ct0 = 0, cnt = 0, ctb = 0, cpub = 0;
     bool aborted = false;
     for (;;) {
         // the next block, when its buffer is free
-        {
-            const uint32_t nq = next_block();
-            if (nq < Q && buf_free(nq) && claim(nq, opaque_lane())) {
-                if (!decode(nq)) {
-                    aborted = true;
-                    break;
-                }
-                continue;
+        const uint32_t nq = next_block();
+        if (nq < Q && buf_free(nq) && claim(nq, opaque_lane())) {
+            if (!decode(nq)) {
+                aborted = true;
+                break;
             }
+            continue;
         }
         // else the next kTileClaim tiles (one atomic): slot v / tpb, tile
         // v % tpb of its block (slots past the block's tiles are skipped).
@@ -1037,37 +1044,46 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
             }
             if (q != cq) {
                 locate(lb_of(q), cti, ct0, cnt);
+                ctb = uniform(B.tb[cti]);
                 cq = q;
+                cpub = 0;
             }
-            const uint32_t ti = cti, t0 = ct0, nt = cnt;
+            const uint32_t ti = cti, t0 = ct0, nt = cnt, tb = ctb;
             if (off >= nt) continue;
-            // its block and every one before it claimed (by this wave if need be)
-            for (;;) {
-                const uint32_t nq = next_block();
-                if (nq > q) break;
-                if (claim(nq, opaque_lane()) && !decode(nq)) {
+            // its block and every one before it claimed (by this wave if need
+            // be; the count read above only grows)
+            if (nq <= q) {
+                for (;;) {
+                    const uint32_t n2 = next_block();
+                    if (n2 > q) break;
+                    if (claim(n2, opaque_lane()) && !decode(n2)) {
+                        aborted = true;
+                        break;
+                    }
+                }
+                if (aborted) break;
+            }
+            const int ln2 = opaque_lane();
+            const uint32_t x = buf_of(q);
+            const uint32_t need = (off + 1u) * tb;
+            // the tile's bytes are there: published bytes only grow while the
+            // buffer holds slot q, and it holds q until this tile is read
+            if (cpub < need) {
+                uint64_t sv;
+                if (!fused_poll(state_w(x), ln2, Fk.spin_limit, sv, [&](uint64_t s) {
+                        return (uint32_t)(s >> 32) == q + 1u && (uint32_t)s >= need;
+                    })) {
                     aborted = true;
                     break;
                 }
-            }
-            if (aborted) break;
-            const int ln2 = opaque_lane();
-            const uint32_t x = q % nbuf;
-            const uint32_t tb = uniform(B.tb[ti]);
-            const uint32_t need = (off + 1u) * tb;
-            uint64_t sv;
-            if (!fused_poll(state_w(x), ln2, Fk.spin_limit, sv, [&](uint64_t s) {
-                    return (uint32_t)(s >> 32) == q + 1u && (uint32_t)s >= need;  // the tile's bytes are there
-                })) {
-                aborted = true;
-                break;
+                cpub = (uint32_t)sv;
             }
             const uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
             tile_body<DT, false, true>(B, ti, t0 + off, rbuf + off * tb, V, wbase, mtab, ln2, one, n4, [&]() {
                 // the tile's LDS reads are complete (their values fed the V table)
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
                 if (ln2 == 0)
-                    __hip_atomic_fetch_add((lds_word *)(size_t)done_w(x), 1u, __ATOMIC_RELAXED,
+                    __hip_atomic_fetch_sub((lds_word *)(size_t)done_w(x), 1u, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_WORKGROUP);
             });
         }
