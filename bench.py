@@ -179,6 +179,7 @@ def new_ctx(H, args):
     ctx = H.HipContext(0)
     ctx.set_lz4_decoder(args.lz4_decoder)
     ctx.set_dct_route(args.dct_route)
+    ctx.set_pipeline_route(args.pipeline_route)
     return ctx
 
 
@@ -861,6 +862,18 @@ def wl_stream(args, torch, H, O):
                "kind": "port",
                "sample": f"{reps} x LZ4 of the whole 70B layer + tile decode of its k and v tensors "
                          f"({ne} elements), {cpu_threads()} threads, {secs:.1f} s"}
+    # the route's launches (as hh_pipeline_submit plans them: every block of
+    # this encoding holds whole tiles) and its algorithmic bytes: compressed
+    # in, bf16 out, and the tile bytes of the two-launch tensors written and
+    # read back through the scratch
+    fused_ks = {"auto": {t["k"] for t in L["tensors"] if t["k"] >= 1024}, "two-launch": set(),
+                "fused": {t["k"] for t in L["tensors"]}}[args.pipeline_route]
+    two_launch_tile_bytes = sum(t["tlen"] for t in L["tensors"] if t["k"] not in fused_ks)
+    rest_ks = [t["k"] for t in L["tensors"] if t["k"] not in fused_ks]
+    lz4_name = LZ4_KERNEL_NAMES[("seq" if min(rest_ks) < 1024 else "ring4") if args.lz4_decoder == "auto"
+                                else args.lz4_decoder].split("<")[0] if rest_ks else None
+    stream_kernels = " + ".join((["hctt_lz4_fused_kernel<bf16>"] if fused_ks else []) +
+                                ([lz4_name, "hctt_decode_kernel<bf16>"] if rest_ks else []))
     res = line("llama70b-stream", value, e2e_ms / args.stream_layers, args,
                "f16-split-mfma/f32",
                "synthetic (one seeded 70B layer encoding streamed %d times)" % args.stream_layers,
@@ -868,12 +881,10 @@ def wl_stream(args, torch, H, O):
                 "rho": [round(float(r), 4) for r in rhos], "k": ks,
                 "compressed_bytes_per_layer": nin, "out_dtype": "bf16",
                 "source": file_info["source"] if file_info else "pinned host memory (hh_pinned_alloc)",
-                "value_is": "decode-only (events around LZ4 + tile decode on the pipeline's compute stream)",
+                "value_is": "decode-only (events around the unit's decode launches on the pipeline's compute stream)",
                 "runtime": "hh_pipeline_* (copy stream + compute stream, 2 staging slots)"},
-               roofline("llama70b-stream",
-                        LZ4_KERNEL_NAMES["seq" if args.lz4_decoder == "auto" else args.lz4_decoder].split("<")[0]
-                        + " + hctt_decode_kernel<bf16>",
-                        L["scratch_bytes"] + out_layer + nin + L["scratch_bytes"], dec_s),
+               roofline("llama70b-stream", stream_kernels, nin + out_layer + 2 * two_launch_tile_bytes, dec_s,
+                        {"fused_tensors": [t["name"] for t in L["tensors"] if t["k"] in fused_ks]}),
                cpu,
                {"end_to_end_gbs": round(e2e, 2), "h2d_gbs": round(h2d_gbs, 2),
                 "decode_ms_per_layer": round(dec_s * 1e3, 3),
@@ -997,6 +1008,10 @@ def main():
                     help="whole-matrix transform route of hct3-4096 (the context's HH_OPT_DCT_ROUTE)")
     ap.add_argument("--lz4-decoder", default="auto", choices=sorted(LZ4_KERNEL_NAMES),
                     help="LZ4 block decoder of the batched LZ4 launches (the context's HH_OPT_LZ4_DECODER)")
+    ap.add_argument("--pipeline-route", default="auto", choices=["auto", "two-launch", "fused"],
+                    help="llama70b-stream: how the pipeline decodes a layer's tensors (the context's "
+                         "HH_OPT_PIPELINE_ROUTE): dense tensors in the fused launch (auto), two launches "
+                         "for every tensor, or the fused launch for every tensor")
     ap.add_argument("--lz4-block", type=int, default=16384,
                     help="LZ4 block size in bytes before rounding down to whole tiles "
                          "(the reference HctWriter default is 16 KiB)")

@@ -46,9 +46,10 @@ F32, F16, BF16 = 0, 1, 2
 
 # hh_context_set_option options, LZ4 decoders and whole-matrix transform
 # routes (diagnostics and tests)
-OPT_LZ4_DECODER, OPT_FUSED_POLL_LIMIT, OPT_DCT_ROUTE = 1, 2, 3
+OPT_LZ4_DECODER, OPT_FUSED_POLL_LIMIT, OPT_DCT_ROUTE, OPT_PIPELINE_ROUTE = 1, 2, 3, 4
 LZ4_DECODERS = {"auto": 0, "seq": 1, "seq8": 2, "ring4": 3, "ring8": 4, "ring16": 5, "ring32": 6, "window": 7}
 DCT_ROUTES = {"auto": 0, "dense": 1, "fft": 2}
+PIPELINE_ROUTES = {"auto": 0, "two-launch": 1, "fused": 2}
 
 
 class BlockStatus(C.Structure):
@@ -354,8 +355,9 @@ class HipContext:
 
     def set_option(self, option, value):
         """hh_context_set_option: OPT_LZ4_DECODER (a value of LZ4_DECODERS),
-        OPT_FUSED_POLL_LIMIT (polls per wait of the fused decode, 0 = default)
-        or OPT_DCT_ROUTE (a value of DCT_ROUTES)."""
+        OPT_FUSED_POLL_LIMIT (polls per wait of the fused decode, 0 = default),
+        OPT_DCT_ROUTE (a value of DCT_ROUTES) or OPT_PIPELINE_ROUTE (a value
+        of PIPELINE_ROUTES)."""
         _check(_lib.hh_context_set_option(self._p, int(option), int(value)), "hh_context_set_option")
 
     def set_lz4_decoder(self, name):
@@ -365,6 +367,13 @@ class HipContext:
         """Whole-matrix transform route: "auto" (the FFT route when both sides
         allow it and the larger is at least 1024), "dense" or "fft"."""
         self.set_option(OPT_DCT_ROUTE, DCT_ROUTES[name])
+
+    def set_pipeline_route(self, name):
+        """How DecompressionPipeline.submit decodes a unit's tensors: "auto"
+        (tensors with k >= 1024 whose blocks hold whole tiles in the fused
+        launch, the others through the LZ4 and tile launches), "two-launch"
+        or "fused" (every tensor whose blocks allow it)."""
+        self.set_option(OPT_PIPELINE_ROUTE, PIPELINE_ROUTES[name])
 
     def close(self):
         if getattr(self, "_p", None):

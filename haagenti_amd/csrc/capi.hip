@@ -205,6 +205,10 @@ int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value) {
             if (value < HH_DCT_AUTO || value > HH_DCT_FFT) return HH_ERR_INVALID_ARGUMENT;
             ctx->dct_route = (int32_t)value;
             return HH_OK;
+        case HH_OPT_PIPELINE_ROUTE:
+            if (value < HH_PIPE_AUTO || value > HH_PIPE_FUSED) return HH_ERR_INVALID_ARGUMENT;
+            ctx->pipeline_route = (int32_t)value;
+            return HH_OK;
         default: return HH_ERR_INVALID_ARGUMENT;
     }
 }
@@ -214,7 +218,7 @@ int32_t hh_context_set_option(hh_context *ctx, int32_t option, int64_t value) {
 static int32_t lz4_batch_with(hh_context *ctx, int32_t decoder, const uint8_t *d_in, size_t in_total,
                               const uint64_t *d_in_off, const uint32_t *d_in_len, uint8_t *d_out,
                               const uint64_t *d_out_off, const uint32_t *d_out_cap, uint32_t nblocks,
-                              hh_block_status *d_status, void *stream) {
+                              hh_block_status *d_status, void *stream, bool zero_tail = false) {
     if (!ctx) return HH_ERR_INVALID_ARGUMENT;
     if (nblocks == 0) return HH_OK;
     if (!d_in || !d_in_off || !d_in_len || !d_out || !d_out_off || !d_out_cap || !d_status)
@@ -223,8 +227,8 @@ static int32_t lz4_batch_with(hh_context *ctx, int32_t decoder, const uint8_t *d
     hipError_t e = guard.status();
     if (e != hipSuccess) return from_hip(e);
     // the caller's output buffer has no stated size: its block table is trusted
-    const hh::Lz4Batch B = {d_in,      in_total,  d_in_off, d_in_len, d_out, ~0ull,
-                            d_out_off, d_out_cap, nblocks,  d_status};
+    const hh::Lz4Batch B = {d_in,      in_total,  d_in_off, d_in_len, d_out,    ~0ull,
+                            d_out_off, d_out_cap, nblocks,  d_status, zero_tail};
     return from_hip(hh::launch_lz4_batch(B, decoder, pick_stream(ctx, stream)));
 }
 
@@ -341,7 +345,7 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
     // scratch after every block has been written
     if (!ctx || (!tensors && ntensors)) return HH_ERR_INVALID_ARGUMENT;
     int32_t rc = lz4_batch_with(ctx, hh::lz4_decoder_for_tiles(ctx, tensors, ntensors), d_in, in_total, d_in_off,
-                                d_in_len, d_scratch, d_out_off, d_out_cap, nblocks, d_status, stream);
+                                d_in_len, d_scratch, d_out_off, d_out_cap, nblocks, d_status, stream, true);
     if (rc != HH_OK) return rc;
     return hh_hctt_decode_batch(ctx, tensors, ntensors, out_dtype, stream);
 }

@@ -91,7 +91,7 @@ int32_t hh_hctt_decode_lz4_batch_noalloc(hh_context *ctx, const uint8_t *d_in, s
     if (nblocks) {
         // blocks writing outside the packed tile bytes are reported, not run
         const hh::Lz4Batch B = {d_in, in_total, d_in_off, d_in_len, base, total, d_out_off, d_out_cap,
-                                nblocks, d_status};
+                                nblocks, d_status, 1u};
         const hipError_t e = hh::launch_lz4_batch(B, hh::lz4_decoder_for_tiles(ctx, tensors, ntensors), s);
         if (e != hipSuccess) return hh::from_hip(e);
     }

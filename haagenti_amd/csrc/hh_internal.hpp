@@ -38,10 +38,12 @@ struct hh_context {
     // at context creation (capi_noalloc.hip), and the lookup's result.
     uint8_t *noalloc_scratch = nullptr;
     hipError_t noalloc_status = hipErrorNotInitialized;
-    // hh_context_set_option settings: the LZ4 decoder (hh_lz4_decoder) and
-    // the poll limit of the fused decode's waits (0: the default)
+    // hh_context_set_option settings: the LZ4 decoder (hh_lz4_decoder), the
+    // poll limit of the fused decode's waits (0: the default)
     int32_t lz4_decoder = HH_LZ4_AUTO;
     uint32_t fused_poll_limit = 0;
+    // how hh_pipeline_submit decodes a unit's tensors (hh_pipeline_route)
+    int32_t pipeline_route = HH_PIPE_AUTO;
     // whole-matrix transform route (hh_dct_route), the FFT route's twiddle
     // tables (two lengths cached) and its two f32 matrices of scratch
     int32_t dct_route = HH_DCT_AUTO;
@@ -171,6 +173,10 @@ struct Lz4Batch {
     const uint32_t *out_cap;
     uint32_t nblocks;
     hh_block_status *status;
+    // tile layer entries: a block that decodes short (no error, fewer bytes
+    // than its capacity) zeroes the rest of its capacity, so the tiles there
+    // fail their bitmap count instead of reading what the buffer held
+    uint32_t zero_tail = 0;
 };
 
 // Batched LZ4 with the decoder `decoder` (hh_lz4_decoder; HH_LZ4_AUTO is

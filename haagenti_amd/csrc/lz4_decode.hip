@@ -337,6 +337,8 @@ __global__ __launch_bounds__(kThreads) void lz4_batch_kernel(Lz4Batch B) {
     if (code != HH_OK && out_ok) {
         wave_fence();
         wave_zero_fill(out, cap, lane);
+    } else if (code == HH_OK && B.zero_tail && op < cap) {
+        wave_zero_fill(out + op, cap - op, lane);
     }
     if (lane == 0) {
         hh_block_status st;

@@ -49,6 +49,8 @@ __global__ __launch_bounds__(64) void lz4_seq_kernel(Lz4Batch B) {
     if (code != HH_OK && out_ok) {
         __asm__ __volatile__("" ::: "memory");
         wave_zero_fill(out, d.cap, lane);
+    } else if (code == HH_OK && B.zero_tail && d.op < d.cap) {
+        wave_zero_fill(out + d.op, d.cap - d.op, lane);
     }
     if (lane == 0) {
         hh_block_status st;

@@ -136,6 +136,8 @@ struct Slot {
     bool busy = false;                 // holds a unit not yet collected
     uint64_t ticket = 0;
     uint32_t nblocks = 0;
+    // caller's block index of each staged block (empty: the same order)
+    std::vector<uint32_t> order;
     uint64_t in_bytes = 0, lz4_bytes = 0, out_bytes = 0;
 };
 
@@ -216,13 +218,16 @@ int32_t collect(hh_pipeline *p, Slot &s) {
     const hipError_t e = hipEventSynchronize(s.done);
     if (e != hipSuccess) return from_hip(e);
     Result r;
-    for (uint32_t b = 0; b < s.nblocks; b++)
-        if (s.h_status[b].code != HH_OK) {
+    // the first failing block in the caller's order
+    for (uint32_t b = 0; b < s.nblocks; b++) {
+        const int64_t cb = s.order.empty() ? (int64_t)b : (int64_t)s.order[b];
+        if (s.h_status[b].code != HH_OK && (r.failed_block < 0 || cb < r.failed_block)) {
             r.code = s.h_status[b].code;
             r.status = s.h_status[b];
-            r.failed_block = b;
-            break;
+            r.failed_block = cb;
+            if (s.order.empty()) break;
         }
+    }
     r.times.h2d_start_ms = ms_between(p->t0, s.h2d_start);
     r.times.h2d_end_ms = ms_between(p->t0, s.copied);
     r.times.decode_start_ms = ms_between(p->t0, s.dec_start);
@@ -243,6 +248,80 @@ int32_t collect(hh_pipeline *p, Slot &s) {
 }
 
 size_t elem_bytes(int32_t dtype) { return dtype == HH_F32 ? 4 : 2; }
+
+// Tensors of a unit that the fused launch decodes (hh_pipeline_submit with
+// the tile scratch as LZ4 output).  Tensor i's tiles are packed at pos[i] of
+// the LZ4 output; it qualifies when the blocks whose output lies in its
+// tile bytes cut them into runs of tpb whole tiles in ascending output
+// order (the last run the rest), each at most fused_block_max() bytes, and
+// no block reaches into it from outside.  With HH_PIPE_AUTO only tensors
+// with k >= 1024 are taken: sparser tiles compress into blocks of many short
+// sequences, which the LZ4 launch decodes with more blocks in flight per CU
+// than the fused launch's three LDS block buffers allow.  `order` lists the
+// fused tensors' blocks first (tensor by tensor), then every other block in
+// the caller's order.
+struct FusedPlan {
+    std::vector<uint32_t> fused;  // tensor indices
+    std::vector<uint32_t> tpb;    // their tiles per block
+    uint32_t nblocks = 0;         // their blocks: the first entries of `order`
+    std::vector<uint32_t> order;  // staged block -> caller's block
+};
+
+FusedPlan plan_fused(int32_t route, const hh_hctt_tensor *tensors, uint32_t ntensors, const uint64_t *pos,
+                     const uint64_t *out_off, const uint32_t *out_cap, uint32_t nblocks) {
+    FusedPlan P;
+    if (route == HH_PIPE_TWO_LAUNCH || ntensors == 0 || nblocks == 0) return P;
+    std::vector<std::vector<uint32_t>> mine(ntensors);
+    std::vector<char> ok(ntensors, 1);
+    for (uint32_t b = 0; b < nblocks; b++) {
+        const uint64_t lo = out_off[b], hi = lo + out_cap[b];
+        // the tensors whose tile bytes [pos[i], pos[i + 1]) the block's
+        // output range meets
+        uint32_t i = (uint32_t)(std::upper_bound(pos, pos + ntensors + 1, lo) - pos);
+        i = i > 0 ? i - 1 : 0;
+        if (lo >= pos[ntensors]) continue;  // past every tensor
+        if (hi <= pos[i + 1] && out_cap[b] > 0) {
+            mine[i].push_back(b);
+        } else {
+            for (uint32_t j = i; j < ntensors && pos[j] < (hi > lo ? hi : lo + 1); j++) ok[j] = 0;
+        }
+    }
+    const uint32_t fmax = hh::fused_block_max();
+    std::vector<char> taken(nblocks, 0);
+    for (uint32_t i = 0; i < ntensors; i++) {
+        const hh_hctt_tensor &T = tensors[i];
+        const uint64_t tb = hh_hctt_tile_bytes(T.k);
+        const uint64_t nt = (uint64_t)(T.rows / 64) * (T.cols / 64);
+        if (!ok[i] || nt == 0 || mine[i].empty() || T.tiles_len != nt * tb) continue;
+        if (route == HH_PIPE_AUTO && T.k < 1024u) continue;
+        std::vector<uint32_t> &m = mine[i];
+        std::sort(m.begin(), m.end(), [&](uint32_t a, uint32_t c) { return out_off[a] < out_off[c]; });
+        const uint64_t run = out_cap[m[0]];
+        if (run % tb || run > fmax) continue;
+        const uint64_t tpb = run / tb;
+        if ((uint64_t)m.size() != (nt + tpb - 1) / tpb) continue;
+        bool exact = true;
+        for (size_t j = 0; j < m.size() && exact; j++) {
+            const uint64_t want = j + 1 < m.size() ? run : (nt - j * tpb) * tb;
+            exact = out_off[m[j]] == pos[i] + j * run && out_cap[m[j]] == want;
+        }
+        if (!exact) continue;
+        P.fused.push_back(i);
+        P.tpb.push_back((uint32_t)tpb);
+        for (uint32_t b : m) {
+            P.order.push_back(b);
+            taken[b] = 1;
+        }
+    }
+    if (P.fused.empty()) {
+        P.order.clear();
+        return P;
+    }
+    P.nblocks = (uint32_t)P.order.size();
+    for (uint32_t b = 0; b < nblocks; b++)
+        if (!taken[b]) P.order.push_back(b);
+    return P;
+}
 
 }  // namespace
 
@@ -513,6 +592,13 @@ int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, co
     }
     if (ntiles_total > 0xffffffffull) return HH_ERR_UNSUPPORTED;
     if (nblocks && !lz4_out) return HH_ERR_INVALID_ARGUMENT;
+    // the tensors' packed tile offsets in the LZ4 output, and which of them
+    // the fused launch takes (only when that output is the tile scratch)
+    std::vector<uint64_t> pos(ntensors + 1, 0);
+    for (uint32_t i = 0; i < ntensors; i++) pos[i + 1] = pos[i] + tensors[i].tiles_len;
+    const FusedPlan plan = d_lz4_out ? FusedPlan{}
+                                     : plan_fused(p->ctx->pipeline_route, tensors, ntensors, pos.data(), h_out_off,
+                                                  h_out_cap, nblocks);
     hh::DeviceGuard guard(p->ctx->device);
     if (guard.status() != hipSuccess) return from_hip(guard.status());
     Slot &s = p->slots[p->next_ticket % p->slots.size()];
@@ -534,13 +620,27 @@ int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, co
         if (!direct) p->copier->copy(s.h_stage, h_data, len);
     }
     uint64_t lz4_bytes = 0;
-    if (nblocks) {
+    if (nblocks && plan.order.empty()) {
         std::memcpy(s.h_stage + tab, h_in_off, 8 * (size_t)nblocks);
         std::memcpy(s.h_stage + tab + 8 * (size_t)nblocks, h_out_off, 8 * (size_t)nblocks);
         std::memcpy(s.h_stage + tab + 16 * (size_t)nblocks, h_in_len, 4 * (size_t)nblocks);
         std::memcpy(s.h_stage + tab + 20 * (size_t)nblocks, h_out_cap, 4 * (size_t)nblocks);
-        for (uint32_t b = 0; b < nblocks; b++) lz4_bytes += h_out_cap[b];
+    } else if (nblocks) {
+        // the fused tensors' blocks first (plan order)
+        uint64_t *io = reinterpret_cast<uint64_t *>(s.h_stage + tab);
+        uint64_t *oo = io + nblocks;
+        uint32_t *il = reinterpret_cast<uint32_t *>(oo + nblocks);
+        uint32_t *oc = il + nblocks;
+        for (uint32_t j = 0; j < nblocks; j++) {
+            const uint32_t b = plan.order[j];
+            io[j] = h_in_off[b];
+            oo[j] = h_out_off[b];
+            il[j] = h_in_len[b];
+            oc[j] = h_out_cap[b];
+        }
     }
+    for (uint32_t b = 0; b < nblocks; b++) lz4_bytes += h_out_cap[b];
+    s.order = plan.order;
     // copy stream: H2D once the device slot's previous decode is done
     hipError_t e = hipStreamWaitEvent(p->copy, s.consumed, 0);
     if (e == hipSuccess) e = hipEventRecord(s.h2d_start, p->copy);
@@ -558,31 +658,45 @@ int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, co
         e = hipStreamWaitEvent(p->compute, reinterpret_cast<hipEvent_t>(after_event), 0);
     if (e == hipSuccess) e = hipEventRecord(s.dec_start, p->compute);
     if (e != hipSuccess) return from_hip(e);
-    if (nblocks) {
-        const uint8_t *t = s.d_in + tab;
-        const hh::Lz4Batch B = {s.d_in,
-                                len,
-                                reinterpret_cast<const uint64_t *>(t),
-                                reinterpret_cast<const uint32_t *>(t + 16 * (size_t)nblocks),
-                                lz4_out,
-                                d_lz4_out ? lz4_cap : tiles_total,
-                                reinterpret_cast<const uint64_t *>(t + 8 * (size_t)nblocks),
-                                reinterpret_cast<const uint32_t *>(t + 20 * (size_t)nblocks),
-                                nblocks,
-                                s.d_status};
-        e = hh::launch_lz4_batch(B, hh::lz4_decoder_for_tiles(p->ctx, tensors, ntensors), p->compute);
+    // the tensors the two launches decode
+    std::vector<hh_hctt_tensor> rest, fused;
+    {
+        std::vector<char> is_fused(ntensors, 0);
+        for (uint32_t i : plan.fused) is_fused[i] = 1;
+        for (uint32_t i = 0; i < ntensors; i++) {
+            hh_hctt_tensor t = tensors[i];
+            t.d_tiles = lz4_out + pos[i];
+            (is_fused[i] ? fused : rest).push_back(t);
+        }
+    }
+    const uint8_t *t = s.d_in + tab;
+    const uint64_t *d_in_off = reinterpret_cast<const uint64_t *>(t);
+    const uint64_t *d_out_off = reinterpret_cast<const uint64_t *>(t + 8 * (size_t)nblocks);
+    const uint32_t *d_in_len = reinterpret_cast<const uint32_t *>(t + 16 * (size_t)nblocks);
+    const uint32_t *d_out_cap = reinterpret_cast<const uint32_t *>(t + 20 * (size_t)nblocks);
+    // fused launch first: the LZ4 launch's long sequence chains then overlap
+    // its last workgroups
+    if (plan.nblocks) {
+        e = hh::launch_hctt_lz4_fused(
+            fused.data(), (uint32_t)fused.size(), plan.tpb.data(), s.d_in, len, d_in_off, d_in_len, s.d_status,
+            out_dtype, p->ctx->d_basis, p->ctx->num_cus, p->ctx->fused_poll_limit,
+            hh::lz4_decoder_for_tiles(p->ctx, fused.data(), (uint32_t)fused.size()) == HH_LZ4_SEQ, p->compute);
         if (e != hipSuccess) return from_hip(e);
     }
-    hh_hctt_tensor local[8];
-    uint64_t off = 0;
-    for (uint32_t i = 0; i < ntensors; i += 8) {
-        const uint32_t n = ntensors - i < 8 ? ntensors - i : 8;
-        for (uint32_t j = 0; j < n; j++) {
-            local[j] = tensors[i + j];
-            local[j].d_tiles = lz4_out + off;
-            off += local[j].tiles_len;
-        }
-        rc = hh_hctt_decode_batch(p->ctx, local, n, out_dtype, p->compute);
+    const uint32_t nb2 = nblocks - plan.nblocks;
+    if (nb2) {
+        const uint32_t f = plan.nblocks;
+        // the tile scratch: a short block's tail zeroed, as in the fused launch
+        const hh::Lz4Batch B = {s.d_in, len, d_in_off + f, d_in_len + f, lz4_out,
+                                d_lz4_out ? lz4_cap : tiles_total, d_out_off + f, d_out_cap + f, nb2,
+                                s.d_status + f, d_lz4_out ? 0u : 1u};
+        e = hh::launch_lz4_batch(B, hh::lz4_decoder_for_tiles(p->ctx, rest.data(), (uint32_t)rest.size()),
+                                 p->compute);
+        if (e != hipSuccess) return from_hip(e);
+    }
+    for (size_t i = 0; i < rest.size(); i += 8) {
+        const uint32_t n = rest.size() - i < 8 ? (uint32_t)(rest.size() - i) : 8u;
+        rc = hh_hctt_decode_batch(p->ctx, rest.data() + i, n, out_dtype, p->compute);
         if (rc != HH_OK) return rc;
     }
     e = hipEventRecord(s.consumed, p->compute);

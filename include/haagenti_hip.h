@@ -115,9 +115,21 @@ int32_t hh_context_synchronize(hh_context *ctx);
  * HH_OPT_DCT_ROUTE picks the whole-matrix transform of hh_idct_2d,
  * hh_dct_2d and the HCT3 decode entries (hh_dct_route): HH_DCT_AUTO (the
  * default) takes the FFT route when both sides allow it and the larger is
- * at least 1024, the dense MFMA products otherwise.  Returns
- * HH_ERR_INVALID_ARGUMENT for an unknown option or value. */
-typedef enum hh_option { HH_OPT_LZ4_DECODER = 1, HH_OPT_FUSED_POLL_LIMIT = 2, HH_OPT_DCT_ROUTE = 3 } hh_option;
+ * at least 1024, the dense MFMA products otherwise.
+ * HH_OPT_PIPELINE_ROUTE picks how hh_pipeline_submit decodes a unit's
+ * tensors (hh_pipeline_route): HH_PIPE_AUTO (the default) decodes each
+ * tensor with k >= 1024 whose blocks hold whole tiles in the fused launch
+ * (hh_hctt_decode_lz4_fused) and the others through the LZ4 launch and the
+ * tile launch; HH_PIPE_TWO_LAUNCH takes the two launches for every tensor;
+ * HH_PIPE_FUSED the fused launch for every tensor whose blocks allow it.
+ * Returns HH_ERR_INVALID_ARGUMENT for an unknown option or value. */
+typedef enum hh_option {
+    HH_OPT_LZ4_DECODER = 1,
+    HH_OPT_FUSED_POLL_LIMIT = 2,
+    HH_OPT_DCT_ROUTE = 3,
+    HH_OPT_PIPELINE_ROUTE = 4
+} hh_option;
+typedef enum hh_pipeline_route { HH_PIPE_AUTO = 0, HH_PIPE_TWO_LAUNCH = 1, HH_PIPE_FUSED = 2 } hh_pipeline_route;
 typedef enum hh_dct_route {
     HH_DCT_AUTO = 0,
     HH_DCT_DENSE = 1, /* split-f16 MFMA products against cached bases, O(n^3) */
@@ -414,7 +426,13 @@ int32_t hh_pipeline_next_staging(hh_pipeline *p, uint8_t **h_ptr, size_t *cap);
  * (hh_pipeline_wait / hh_pipeline_finish) or its stream event passed
  * (hh_pipeline_stream_wait).  Every tensor is checked (shape, k, tile
  * bytes, output alignment) before anything is enqueued; an invalid one
- * fails the call with nothing enqueued. */
+ * fails the call with nothing enqueued.
+ * Route: with d_lz4_out NULL, a tensor whose blocks cut its packed tile
+ * bytes into runs of tiles_per_block whole tiles (ascending, the last run
+ * the rest, at most HH_FUSED_BLOCK_BYTES each) may be decoded by the fused
+ * launch, its tile bytes then never written to the scratch
+ * (HH_OPT_PIPELINE_ROUTE; by default the tensors with k >= 1024).  Outputs,
+ * tile statuses and block records are the same either way. */
 int32_t hh_pipeline_submit(hh_pipeline *p, const uint8_t *h_data, size_t len, const uint64_t *h_in_off,
                            const uint32_t *h_in_len, const uint64_t *h_out_off, const uint32_t *h_out_cap,
                            uint32_t nblocks, uint8_t *d_lz4_out, uint64_t lz4_out_cap,

@@ -282,3 +282,90 @@ def test_pipeline_blocks_across_tile_boundaries():
         rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
         assert np.abs(got - ref).max() <= TOL * rms
     pipe.close()
+
+
+def test_pipeline_routes_agree_bit_for_bit():
+    # one unit of mixed retention through the three routes of
+    # hh_pipeline_submit (HH_OPT_PIPELINE_ROUTE): two launches for every
+    # tensor; the fused launch for k >= 1024 (auto); the fused launch for
+    # every tensor.  Outputs, tile statuses and block records agree bit for
+    # bit, also with damaged blocks: tensor b's first block cut to one byte
+    # (UnexpectedEof) and its second to half (a stream that ends cleanly
+    # decodes short: the rest of its tile bytes read as zeros on every
+    # route), and tensor c's first block cut by 7 bytes.  Under auto the
+    # fused launch takes a and c, whose blocks come first in the staged
+    # table; wait() still names the first failing block in the caller's
+    # order.
+    Hm, Pm = H(), P()
+    T = G.torch()
+    shapes = [("a", 128, 256), ("b", 192, 128), ("c", 64, 512), ("d", 128, 128)]
+    ks = [1228, 410, 2048, 700]
+    L = LU.encode_layer(Hm, shapes, ks, seed=93, block_bytes=4096)
+    soff = np.cumsum([0] + [t["tiles"].size for t in L["tensors"]])
+    tens = np.searchsorted(soff[1:], L["out_off"], side="right")
+    b0, b1 = (int(x) for x in np.nonzero(tens == 1)[0][:2])   # tensor b (k = 410): its two blocks
+    c0 = int(np.nonzero(tens == 2)[0][0])                       # tensor c (k = 2048), later in the table
+    assert b0 < b1 < c0
+    il = L["in_len"].copy()
+    il[b0] = 1
+    il[b1] //= 2
+    il[c0] -= 7
+    cfg = Pm.default_config()
+    cfg.staging_buffer_size = 1 << 20
+    cfg.tile_scratch_size = 1 << 20
+    cfg.max_blocks = 64
+    ctx = G.ctx()
+    pipe = Pm.DecompressionPipeline(ctx, None, cfg)
+    got = {}
+    try:
+        for route in ("two-launch", "auto", "fused"):
+            ctx.set_pipeline_route(route)
+            for dt, tdt in ((Hm.F32, T.float32), (Hm.BF16, T.bfloat16)):
+                for tables in ((L["in_off"], L["in_len"], L["out_off"], L["out_cap"]),
+                               (L["in_off"], il, L["out_off"], L["out_cap"])):
+                    outs = [T.full((r * c,), 7, dtype=tdt, device="cuda") for _, r, c in shapes]
+                    tst = [T.full(((r // 64) * (c // 64),), -1, dtype=T.int32, device="cuda") for _, r, c in shapes]
+                    desc = [(t["tiles"].size, t["rows"], t["cols"], t["k"], o, s)
+                            for t, o, s in zip(L["tensors"], outs, tst)]
+                    tk = pipe.submit(L["blob"].copy(), *tables, tensors=desc, dtype=dt)
+                    failed = None
+                    try:
+                        pipe.wait(tk)
+                    except Hm.HaagentiError as ex:
+                        failed = (ex.code, ex.block, ex.status.detail, ex.status.position, ex.status.required)
+                    key = (dt, tables[1] is il)
+                    res = ([o.view(T.int16 if tdt == T.bfloat16 else T.int32).cpu().numpy() for o in outs],
+                           [s.cpu().numpy() for s in tst], failed)
+                    print(f"[routes] {route} dtype {dt} damaged {key[1]}: failed {failed}", flush=True)
+                    if key not in got:
+                        got[key] = res
+                        continue
+                    ref = got[key]
+                    assert res[2] == ref[2]
+                    for x, y in zip(res[0], ref[0]):
+                        assert np.array_equal(x, y)
+                    for x, y in zip(res[1], ref[1]):
+                        assert np.array_equal(x, y)
+    finally:
+        ctx.set_pipeline_route("auto")
+    # the clean unit decodes every tile, within the tolerance of the oracle
+    assert got[(Hm.F32, False)][2] is None
+    assert all((s == 0).all() for s in got[(Hm.F32, False)][1])
+    for t, o in zip(L["tensors"], got[(Hm.F32, False)][0]):
+        _, ref = O.hctt_decode_tensor(t["tiles"], t["rows"], t["cols"], t["k"])
+        rms = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+        assert np.abs(o.view(np.float32).reshape(t["rows"], t["cols"]) - ref).max() <= TOL * rms
+    # the damaged unit: wait() names block b0 with the oracle's record
+    code, block = got[(Hm.F32, True)][2][:2]
+    assert block == b0
+    a = int(L["in_off"][b0])
+    _, e = O.lz4_decompress_block(L["blob"][a:a + int(il[b0])].tobytes(), int(L["out_cap"][b0]))
+    assert code == e.kind
+    # every tile of b (both its blocks damaged) and c's first two tiles
+    # (its first block) report CORRUPTED_DATA with zero output; a and d decode
+    st, out = got[(Hm.F32, True)][1], got[(Hm.F32, True)][0]
+    assert (st[0] == 0).all() and (st[3] == 0).all()
+    assert (st[1] == Hm.CORRUPTED_DATA).all() and (out[1] == 0).all()
+    assert (st[2][:2] == Hm.CORRUPTED_DATA).all() and (st[2][2:] == 0).all()
+    assert (out[2].reshape(64, 512)[:, :128] == 0).all()
+    pipe.close()
