@@ -257,7 +257,10 @@ int32_t hh_hctt_decode_batch(hh_context *ctx, const hh_hctt_tensor *tensors, uin
  * 282-293) does for one layer's tensors.  A block that fails leaves its
  * range of d_scratch zeroed, so every tile it covers fails the bitmap count
  * (tile status HH_ERR_CORRUPTED_DATA, output zeros) whatever the scratch held
- * before; d_status names the block once the stream completes. */
+ * before; d_status names the block once the stream completes.  A block that
+ * decodes short (HH_OK, fewer bytes than its capacity) zeroes the rest of
+ * its range, so the tiles there fail the same way (as in
+ * hh_hctt_decode_lz4_fused and the no-alloc entry). */
 int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in_total,
                                  const uint64_t *d_in_off, const uint32_t *d_in_len,
                                  uint8_t *d_scratch, const uint64_t *d_out_off,
