@@ -9,13 +9,14 @@ coefficients (k = 1228) as a bitmap + INT4 with f16 scales, LZ4-compressed
 in blocks of 13 whole tiles (15,652 bytes: the reference HctWriter's default
 block size, 16 KiB, rounded down to whole tiles;
 crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes 32 such layers
-back to back into bf16 tensors: per layer one hh_hctt_decode_lz4_fused call,
-i.e. one launch that decodes the layer's LZ4 blocks into LDS and their tiles
-(dequant + scatter + inverse DCT on MFMA) to bf16.  Inputs are resident in
-HBM before timing starts.  The step time brackets all 32 layers, with nothing
-recorded between the launches; the roofline's average launch is the step
-time over the layers (launch gaps included, so it cannot exceed a layer's
-share of the step).  --path two-launch decodes each layer with
+back to back into bf16 tensors: per two layers (--layers-per-launch) one
+hh_hctt_decode_lz4_fused call, i.e. one launch that decodes the layers' LZ4
+blocks into LDS and their tiles (dequant + scatter + inverse DCT on MFMA) to
+bf16 (two layers share a launch's start-up, pipeline fill and drain).
+Inputs are resident in HBM before timing starts.  The step time brackets all
+32 layers, with nothing recorded between the launches; the roofline's average
+launch is the step time over the launches (launch gaps included, so it
+cannot exceed a launch's share of the step).  --path two-launch decodes each layer with
 hh_hctt_decode_lz4_batch (an LZ4 launch into a scratch buffer, then the tile
 launch); its per-kernel times come from HIP events around the launches of
 every 8th layer of the timed steps (--kernel-sample).
@@ -108,10 +109,20 @@ def traffic_for(workload):
         return None
 
 
-def roofline(workload, kernel, algo_bytes, avg_s, extra=None, traffic_key=None):
+def fused_traffic(lpl):
+    """Traffic of a fused launch over `lpl` layers: measured for that many layers when
+    profiles/traffic.json holds it, else the one-layer measurement scaled by `lpl`."""
+    key = f"llama3-8b-layer:fused-x{lpl}"
+    if lpl > 1 and traffic_for(key) is not None:
+        return {"traffic_key": key}
+    return {"traffic_key": "llama3-8b-layer:fused", "traffic_scale": lpl}
+
+
+def roofline(workload, kernel, algo_bytes, avg_s, extra=None, traffic_key=None, traffic_scale=1):
     achieved = algo_bytes / avg_s / 1e9
+    traffic = traffic_for(traffic_key or workload)  # measured per launch of one unit (e.g. one layer)
     r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(traffic_key or workload),
+         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None if traffic is None else traffic * traffic_scale,
          "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
          "algorithmic_bytes_per_launch": int(algo_bytes)}
     if extra:
@@ -287,14 +298,32 @@ def wl_llama3_8b_layer(args, torch, H, O):
     tabs = [dict(in_off=devtab(torch, L["in_off"]), in_len=devtab(torch, L["in_len"]),
                  out_off=devtab(torch, L["out_off"]), out_cap=devtab(torch, L["out_cap"]),
                  n=L["in_off"].size) for L in layers_host]
-    d_comp, outs = [], []
+    fused = args.path == "fused"
+    # fused path: layers_per_launch consecutive layers per launch (their
+    # compressed blocks in one device buffer, the block offsets shifted)
+    lpl = args.layers_per_launch if fused else 1
+    groups = [list(range(g, min(g + lpl, args.layers))) for g in range(0, args.layers, lpl)]
+    d_comp, outs, gdata = [], [], []
     for l in range(args.layers):
-        L = layers_host[l % args.distinct]
-        d_comp.append(torch.from_numpy(L["blob"].copy()).cuda())
         outs.append([torch.empty(r * c, dtype=torch.bfloat16, device="cuda") for _, r, c in L8B])
+    if lpl == 1:
+        for l in range(args.layers):
+            d_comp.append(torch.from_numpy(layers_host[l % args.distinct]["blob"].copy()).cuda())
+    else:
+        for grp in groups:
+            Ls = [layers_host[l % args.distinct] for l in grp]
+            base = np.cumsum([0] + [L["blob"].size for L in Ls[:-1]]).astype(np.uint64)
+            gdata.append(dict(
+                d=torch.from_numpy(np.concatenate([L["blob"] for L in Ls])).cuda(),
+                in_off=devtab(torch, np.concatenate([L["in_off"] + b for L, b in zip(Ls, base)])),
+                in_len=devtab(torch, np.concatenate([L["in_len"] for L in Ls])),
+                n=sum(int(L["in_off"].size) for L in Ls),
+                desc=[(t["rows"], t["cols"], k, outs[l][i]) for l, L in zip(grp, Ls)
+                      for i, t in enumerate(L["tensors"])]))
     scratch = [torch.empty(layers_host[0]["scratch_bytes"], dtype=torch.uint8, device="cuda")
                for _ in range(2)]
-    status = torch.zeros(max(t["n"] for t in tabs) * 32, dtype=torch.uint8, device="cuda")
+    status = torch.zeros(max([t["n"] for t in tabs] + [g["n"] for g in gdata]) * 32, dtype=torch.uint8,
+                         device="cuda")
     torch.cuda.synchronize()
     # per-kernel HIP events bracket the launches of every kernel_sample-th
     # layer of the timed steps (an event record between two launches costs
@@ -303,7 +332,12 @@ def wl_llama3_8b_layer(args, torch, H, O):
     t_lz4, t_tile = (Timed(torch, stream, args.steps * len(sampled)),
                      Timed(torch, stream, args.steps * len(sampled)))
 
-    fused = args.path == "fused"
+    def run_group(gi):
+        # layers_per_launch layers in one fused launch
+        G = gdata[gi]
+        rc = ctx.hctt_decode_lz4_fused(G["d"], G["d"].numel(), G["in_off"], G["in_len"], G["n"], status,
+                                       G["desc"], tiles_per_block, dtype=H.BF16, stream=sp)
+        assert rc == H.OK
 
     def run_layer(l, timed):
         L = layers_host[l % args.distinct]
@@ -336,12 +370,16 @@ def wl_llama3_8b_layer(args, torch, H, O):
         t_tile.stop(e)
 
     def step(timed=False):
+        if lpl > 1:
+            for gi in range(len(groups)):
+                run_group(gi)
+            return
         for l in range(args.layers):
             run_layer(l, timed)
 
     step()                                   # correctness pass (checked below)
     torch.cuda.synchronize()
-    codes = status.cpu().numpy().view(np.int32)[0::8][:tabs[-1]["n"]]
+    codes = status.cpu().numpy().view(np.int32)[0::8][:(gdata[-1]["n"] if gdata else tabs[-1]["n"])]
     assert (codes == 0).all(), "LZ4 block errors"
     check = None
     if O is not None:
@@ -389,16 +427,19 @@ def wl_llama3_8b_layer(args, torch, H, O):
                          f"bf16 bytes like the GPU line; {secs:.1f} s"}
     return line("llama3-8b-layer", value, ms_step, args, "f16-split-mfma/f32",
                 f"synthetic (N(0,0.02) weights, seeded; {args.distinct} distinct layers replicated)",
-                {"layers": args.layers, "elements_per_layer": n_elem, "rho": RHO_8B, "k": k,
+                {"layers": args.layers, "layers_per_launch": lpl, "elements_per_layer": n_elem, "rho": RHO_8B, "k": k,
                  "tile": 64, "tile_bytes": tb, "lz4_block_tiles": tiles_per_block,
                  "out_dtype": "bf16", "hct_bytes_per_layer": in_tile,
                  "lz4_bytes_per_layer": comp_bytes},
-                (roofline("llama3-8b-layer:fused", "hctt_lz4_fused_kernel<bf16>", comp_bytes + out_bytes_layer,
-                          tile_s) if fused else
+                (roofline("llama3-8b-layer:fused", "hctt_lz4_fused_kernel<bf16>",
+                          lpl * (comp_bytes + out_bytes_layer), lpl * tile_s,
+                          **fused_traffic(lpl)) if fused else
                  roofline("llama3-8b-layer", "hctt_decode_kernel<bf16>", in_tile + out_bytes_layer, tile_s)),
                 cpu,
-                ({"path": "fused", "kernels_us": {"hctt_lz4_fused_kernel": round(tile_s * 1e6, 2)},
-                  "avg_launch_is": "step time / layers (back-to-back launches, no events between them)",
+                ({"path": "fused", "kernels_us": {"hctt_lz4_fused_kernel": round(lpl * tile_s * 1e6, 2)},
+                  "per_layer_us": round(tile_s * 1e6, 2),
+                  "avg_launch_is": "step time / launches (back-to-back launches of layers_per_launch layers, "
+                                   "no events between them)",
                   "spot_check_max_err_over_rms": check} if fused else
                  {"path": "two-launch",
                   "kernels_us": {"lz4_kernel": round(lz4_s * 1e6, 2),
@@ -992,6 +1033,9 @@ def main():
                     help="untimed steps first (the clocks settle within ~50 ms of load)")
     ap.add_argument("--workload", default="llama3-8b-layer", choices=sorted(WORKLOADS))
     ap.add_argument("--layers", type=int, default=32, help="llama3-8b-layer: layers per step")
+    ap.add_argument("--layers-per-launch", type=int, default=2,
+                    help="llama3-8b-layer, fused path: consecutive layers decoded by one hh_hctt_decode_lz4_fused "
+                         "call (their 7 tensors each; one launch for up to 16 tensors)")
     ap.add_argument("--stream-layers", type=int, default=80, help="llama70b-stream: layers")
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
@@ -1001,7 +1045,7 @@ def main():
     ap.add_argument("--kernel-sample", type=int, default=8,
                     help="llama3-8b-layer: per-kernel events on every n-th layer of the timed steps")
     ap.add_argument("--path", choices=["fused", "two-launch"], default="fused",
-                    help="llama3-8b-layer: one fused LZ4 + tile launch per layer (hh_hctt_decode_lz4_fused) "
+                    help="llama3-8b-layer: fused LZ4 + tile launches (hh_hctt_decode_lz4_fused) "
                          "or the LZ4 and tile launches through a scratch buffer (hh_hctt_decode_lz4_batch)")
     ap.add_argument("--hct3-size", type=int, default=4096, help="hct3-4096: side of the square tensor")
     ap.add_argument("--dct-route", default="auto", choices=["auto", "dense", "fft"],
@@ -1020,6 +1064,10 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the decode runs on "
               "a single MI355X; across GPUs each would decode its own tensors or 64-aligned slabs, "
               "with nothing exchanged).", file=sys.stderr)
+        sys.exit(2)
+    if args.layers_per_launch not in (1, 2) or args.layers % args.layers_per_launch:
+        print("--layers-per-launch is 1 or 2 (a launch takes up to 16 tensors, 7 per layer) and divides "
+              "--layers", file=sys.stderr)
         sys.exit(2)
     import torch
     import haagenti_amd as H

@@ -168,7 +168,7 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
-constexpr int kMaxTensors = 8;
+constexpr int kMaxTensors = 16;
 static_assert((kMaxTensors & (kMaxTensors - 1)) == 0 && kMaxTensors <= 64, "tensor_of reads one start per lane");
 // Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs with
 // at most 2 KiB of tile bytes prefetched (168 registers, no spills; the LDS
@@ -696,7 +696,7 @@ constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's
 constexpr uint32_t kFusedMaxBufs = 8;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
-constexpr uint32_t kFusedMaxRange = 4096;  // slots per workgroup (the bitmaps' size)
+constexpr uint32_t kFusedMaxRange = 2048;  // slots per workgroup (the bitmaps' size)
 // tiles a wave claims with one atomic (2 measured 2 % slower on the
 // Llama-3-8B layer: the block claims, checked once per claim, came later)
 constexpr uint32_t kTileClaim = 1;

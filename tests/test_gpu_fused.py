@@ -234,14 +234,15 @@ def assert_same(T, dtype, fo, fs, bo, bs):
 
 
 def test_many_tensors_small_blocks_f16():
-    # ten tensors (two launches of at most eight), blocks of one and of three
-    # tiles, f16 output
+    # twenty tensors (two launches of at most sixteen), blocks of one and of
+    # three tiles, f16 output
     Hm = H()
     T = G.torch()
     rng = np.random.default_rng(51)
     shapes = [("t%d" % i, r, c) for i, (r, c) in enumerate(
         [(64, 64), (128, 64), (64, 192), (192, 128), (64, 64), (256, 64), (128, 128), (64, 320), (320, 64),
-         (128, 192)])]
+         (128, 192), (64, 128), (192, 64), (64, 64), (128, 256), (64, 448), (256, 128), (64, 64), (192, 192),
+         (128, 64), (64, 256)])]
     ks = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, len(shapes))]
     for tpb in (1, 3):
         L = encode_fixed(Hm, shapes, ks, seed=52 + tpb, tpb=tpb)
