@@ -21,12 +21,14 @@
 //
 // Precision.  Each retained coefficient (q - 8) * scale is held exactly as
 // an f16 pair hi + lo (the scale split into its top 8 and low 3 significant
-// bits, each product with q - 8 exact), and GEMM1 runs all four passes
-// hi*hi + hi*lo + lo*hi + lo*lo against M = M_hi + M_lo (~2^-22 relative).
-// GEMM1's output S is split the same way by rounding (S_hi = f16(S),
-// S_lo = f16(S - S_hi)) and GEMM2 runs three passes (the dropped
-// S_lo * M_lo is ~2^-24 relative).  Accumulation is f32; the max-abs error
-// is ~1e-6 x RMS against a bar of 1e-3 x RMS.  Coefficients are prescaled
+// bits, each product with q - 8 exact), and GEMM1 runs three passes
+// hi*hi + hi*lo + lo*hi against M = M_hi + M_lo (the dropped lo*lo is below
+// 2^-8 * 2^-11 = 2^-19 relative).  GEMM1's output S is split the same way by
+// rounding (S_hi = f16(S), S_lo = f16(S - S_hi)) and GEMM2 runs three
+// passes (the dropped S_lo * M_lo is ~2^-24 relative).  Accumulation is
+// f32; the max-abs error is ~4e-6 x RMS against a bar of 1e-3 x RMS (each
+// MFMA pass costs about as much as a tenth of the tile's vector work, so
+// the fourth GEMM1 pass, worth ~2e-6 x RMS, is left out).  Coefficients are prescaled
 // by 2^E per tile (E from the largest f16 scale exponent, so that
 // |C 2^E| < 4) and M by 2^8, which puts GEMM1's output directly in the
 // range of GEMM2's f16 operands; only scales below ~2^-12 of the tile's
@@ -425,7 +427,6 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                 acc[up][vp] = mfma(ahi[vp], mh, acc[up][vp]);
                 acc[up][vp] = mfma(ahi[vp], ml, acc[up][vp]);
                 acc[up][vp] = mfma(alo[vp], mh, acc[up][vp]);
-                acc[up][vp] = mfma(alo[vp], ml, acc[up][vp]);
             }
         }
     }
