@@ -494,11 +494,13 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
             *(u32x4 HH_GLOBAL *)(otile + (size_t)(rows_per * it) * opitch + loff) = v;
         }
     };
+    // GEMM2 for both column blocks first (four accumulator chains in
+    // flight), then their output stages
+    floatx16 x2all[2][2];
 #pragma unroll
     for (int jb = 0; jb < 2; jb++) {
-        floatx16 x2[2];
-        x2[0] = floatx16{};
-        x2[1] = floatx16{};
+        x2all[jb][0] = floatx16{};
+        x2all[jb][1] = floatx16{};
 #pragma unroll
         for (int up = 0; up < 2; up++) {
 #pragma unroll
@@ -514,11 +516,15 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
                 }
                 const u32x4 mh = mtab[((0 * 2 + up) * 2 + s) * 64 + lane];
                 const u32x4 ml = mtab[((1 * 2 + up) * 2 + s) * 64 + lane];
-                x2[up] = mfma(shi, mh, x2[up]);
-                x2[up] = mfma(shi, ml, x2[up]);
-                x2[up] = mfma(slo, mh, x2[up]);
+                x2all[jb][up] = mfma(shi, mh, x2all[jb][up]);
+                x2all[jb][up] = mfma(shi, ml, x2all[jb][up]);
+                x2all[jb][up] = mfma(slo, mh, x2all[jb][up]);
             }
         }
+    }
+#pragma unroll
+    for (int jb = 0; jb < 2; jb++) {
+        const floatx16 *x2 = x2all[jb];
         if constexpr (PRIO)
             if (jb == 1) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
