@@ -111,6 +111,39 @@ def test_llama3_8b_layer_fused_equals_two_launch_path():
         del fo, bo
 
 
+_TWO_LAYERS = {}
+
+
+def test_two_llama3_8b_layers_in_one_launch():
+    # the bench's default step: two layers' 14 tensors in one fused launch
+    # (their blocks in one buffer, the second layer's offsets shifted), bit
+    # for bit the same outputs, tile statuses and block records as one
+    # launch per layer
+    Hm = H()
+    T = G.torch()
+    k = Hm.hctt_retain_count(0.3)
+    tpb = 16384 // Hm.hctt_tile_bytes(k)
+    if not _TWO_LAYERS:
+        _TWO_LAYERS["L"] = [LU.encode_layer(Hm, LU.L8B, [k] * 7, seed=s) for s in (21, 22)]
+    La, Lb = _TWO_LAYERS["L"]
+    both = dict(blob=np.concatenate([La["blob"], Lb["blob"]]),
+                in_off=np.concatenate([La["in_off"], Lb["in_off"] + np.uint64(La["blob"].size)]),
+                in_len=np.concatenate([La["in_len"], Lb["in_len"]]),
+                tensors=La["tensors"] + Lb["tensors"])
+    assert len(both["tensors"]) == 14
+    fo, st, fs = fused(both, Hm.BF16, tpb)
+    assert (st["code"] == 0).all()
+    na = La["in_off"].size
+    for i, L in enumerate((La, Lb)):
+        lo, lst, ls = fused(L, Hm.BF16, tpb)
+        assert np.array_equal(lst, st[i * na:i * na + L["in_off"].size])
+        for j in range(7):
+            assert T.equal(lo[j].view(T.int16), fo[7 * i + j].view(T.int16)), (i, j)
+            assert T.equal(ls[j], fs[7 * i + j]), (i, j)
+        del lo, ls
+    del fo, fs
+
+
 def test_mixed_retention_fixed_blocks_vs_oracle():
     Hm = H()
     rng = np.random.default_rng(41)
