@@ -810,16 +810,20 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
     auto done_w = [](uint32_t x) { return kFusedDoneOff + 4u * x; };
 
     // block lb -> tensor, first tile, tile count
-    auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt) {
-        // the count of tensor first blocks after the first at or below lb
-        // (the unused entries past blk_start[n] are all-ones; no branches,
-        // so the loads overlap)
-        ti = 0;
-#pragma unroll
-        for (uint32_t j = 1; j < (uint32_t)kMaxTensors; j++) ti += lb >= uniform(F.blk_start[j]) ? 1u : 0u;
-        const uint32_t tpb_i = uniform(F.tpb[ti]);
-        t0 = (lb - uniform(F.blk_start[ti])) * tpb_i;
-        nt = min(tpb_i, uniform(B.start[ti + 1]) - uniform(B.start[ti]) - t0);
+    auto locate = [&](uint32_t lb, uint32_t &ti, uint32_t &t0, uint32_t &nt, uint32_t &tb) {
+        // lane j holds tensor j's first block, tiles per block, first and
+        // last tile and tile bytes (one round of LDS reads); the tensor is
+        // the count of first blocks after the first at or below lb (the
+        // unused entries past blk_start[n] are all-ones), by a ballot, and
+        // its fields come from lane ti (wave-uniform; every lane active)
+        const uint32_t j = (uint32_t)opaque_lane() & (kMaxTensors - 1);
+        const uint32_t sj = F.blk_start[j], pj = F.tpb[j], s0 = B.start[j], s1 = B.start[j + 1], bj = B.tb[j];
+        ti = (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(lb >= sj) & (((1ull << kMaxTensors) - 1ull) & ~1ull));
+        const uint32_t tpb_i = (uint32_t)__builtin_amdgcn_readlane((int)pj, (int)ti);
+        t0 = (lb - (uint32_t)__builtin_amdgcn_readlane((int)sj, (int)ti)) * tpb_i;
+        nt = min(tpb_i, (uint32_t)__builtin_amdgcn_readlane((int)s1, (int)ti) -
+                            (uint32_t)__builtin_amdgcn_readlane((int)s0, (int)ti) - t0);
+        tb = (uint32_t)__builtin_amdgcn_readlane((int)bj, (int)ti);
     };
     // The workgroup's blocks: launch blocks g, g + G, g + 2 G, ... (G
     // workgroups), its q-th block lb(q) = g + q G, all of whose tiles it
@@ -858,8 +862,8 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 ((hh_block_status *)Fk.status)[Fk.blk_base + lb_of(q)] = st;
             }
             for (uint32_t q = 0; q < Q; q++) {
-                uint32_t ti, t0, nt;
-                locate(lb_of(q), ti, t0, nt);
+                uint32_t ti, t0, nt, tbq;
+                locate(lb_of(q), ti, t0, nt, tbq);
                 int32_t *ts = B.status[ti];
                 if (ts != nullptr)
                     for (uint32_t j = (uint32_t)l; j < nt; j += 64u) ts[t0 + j] = HH_ERR_DEVICE;
@@ -917,14 +921,14 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 return false;
         }
         const uint32_t lb = lb_of(q);
-        uint32_t ti, t0, nt;
-        locate(lb, ti, t0, nt);
+        uint32_t ti, t0, nt, tbq;
+        locate(lb, ti, t0, nt, tbq);
         const uint64_t stamp = (uint64_t)(q + 1u) << 32;
         if (ln == 0) {
             __hip_atomic_store((lds_word *)(size_t)done_w(x), nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_store((lds_dword *)(size_t)state_w(x), stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        const uint32_t tb = uniform(B.tb[ti]);
+        const uint32_t tb = tbq;
         const uint32_t cap = nt * tb;
         uint8_t *rbuf = smem + Fk.buf_off + x * kFusedBuf;
         const uint32_t gb = Fk.blk_base + lb;
@@ -1050,8 +1054,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
                 break;
             }
             if (q != cq) {
-                locate(lb_of(q), cti, ct0, cnt);
-                ctb = uniform(B.tb[cti]);
+                locate(lb_of(q), cti, ct0, cnt, ctb);
                 cq = q;
                 cpub = 0;
             }
@@ -1139,8 +1142,8 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         const uint32_t f = uniform(__hip_atomic_load((lds_word *)(size_t)bit_w(kFusedFailOff, q), __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
         if ((f & bit_m(q)) == 0u) continue;
-        uint32_t bti, bt0, bnt;
-        locate(lb_of(q), bti, bt0, bnt);
+        uint32_t bti, bt0, bnt, btb;
+        locate(lb_of(q), bti, bt0, bnt, btb);
         const uint32_t cols = B.cols[bti], tpr = B.tiles_per_row[bti];
         uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[bti];
         for (uint32_t j = wave; j < bnt; j += nw) {
