@@ -9,10 +9,10 @@ coefficients (k = 1228) as a bitmap + INT4 with f16 scales, LZ4-compressed
 in blocks of 13 whole tiles (15,652 bytes: the reference HctWriter's default
 block size, 16 KiB, rounded down to whole tiles;
 crates/haagenti-hct/src/tensor.rs:74,536).  One step decodes 32 such layers
-back to back into bf16 tensors: per two layers (--layers-per-launch) one
+back to back into bf16 tensors: per four layers (--layers-per-launch) one
 hh_hctt_decode_lz4_fused call, i.e. one launch that decodes the layers' LZ4
 blocks into LDS and their tiles (dequant + scatter + inverse DCT on MFMA) to
-bf16 (two layers share a launch's start-up, pipeline fill and drain).
+bf16 (four layers share a launch's start-up, pipeline fill and drain).
 Inputs are resident in HBM before timing starts.  The step time brackets all
 32 layers, with nothing recorded between the launches; the roofline's average
 launch is the step time over the launches (launch gaps included, so it
@@ -1033,9 +1033,9 @@ def main():
                     help="untimed steps first (the clocks settle within ~50 ms of load)")
     ap.add_argument("--workload", default="llama3-8b-layer", choices=sorted(WORKLOADS))
     ap.add_argument("--layers", type=int, default=32, help="llama3-8b-layer: layers per step")
-    ap.add_argument("--layers-per-launch", type=int, default=2,
+    ap.add_argument("--layers-per-launch", type=int, default=4,
                     help="llama3-8b-layer, fused path: consecutive layers decoded by one hh_hctt_decode_lz4_fused "
-                         "call (their 7 tensors each; one launch for up to 16 tensors)")
+                         "call (their 7 tensors each; one launch for up to 32 tensors)")
     ap.add_argument("--stream-layers", type=int, default=80, help="llama70b-stream: layers")
     ap.add_argument("--distinct", type=int, default=2, help="distinct encoded layers")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
@@ -1065,8 +1065,8 @@ def main():
               "a single MI355X; across GPUs each would decode its own tensors or 64-aligned slabs, "
               "with nothing exchanged).", file=sys.stderr)
         sys.exit(2)
-    if args.layers_per_launch not in (1, 2) or args.layers % args.layers_per_launch:
-        print("--layers-per-launch is 1 or 2 (a launch takes up to 16 tensors, 7 per layer) and divides "
+    if args.layers_per_launch not in (1, 2, 4) or args.layers % args.layers_per_launch:
+        print("--layers-per-launch is 1, 2 or 4 (a launch takes up to 32 tensors, 7 per layer) and divides "
               "--layers", file=sys.stderr)
         sys.exit(2)
     import torch

@@ -170,7 +170,7 @@ __device__ __forceinline__ uint32_t lds_load(uint32_t a) { return *(lds_u32 *)(s
 
 // Up to kMaxTensors tensors per launch, passed by value as kernel arguments.
 // Tiles are numbered across the batch; tensor i owns [start[i], start[i+1]).
-constexpr int kMaxTensors = 16;
+constexpr int kMaxTensors = 32;
 static_assert((kMaxTensors & (kMaxTensors - 1)) == 0 && kMaxTensors <= 64, "tensor_of reads one start per lane");
 // Waves per SIMD the tile kernel is compiled for: 3 for 16-bit outputs with
 // at most 2 KiB of tile bytes prefetched (168 registers, no spills; the LDS
@@ -181,12 +181,10 @@ struct TileBatch {
     void *out[kMaxTensors];
     int32_t *status[kMaxTensors];
     uint32_t start[kMaxTensors + 1];
-    uint32_t tiles_per_row[kMaxTensors];
-    float tpr_inv[kMaxTensors];  // 1 / tiles_per_row, rounded to f32 on the host
+    float tpr_inv[kMaxTensors];  // 64 / cols (1 / tiles per row), rounded to f32 on the host
     uint32_t cols[kMaxTensors];
     uint32_t k[kMaxTensors];
     uint32_t tb[kMaxTensors];
-    uint32_t dword_ok[kMaxTensors];
     uint32_t n;
     uint32_t wave_lds;  // per-wave LDS bytes: V/output union + staged tile bytes
     uint32_t vo_bytes;  // size of the V/output union
@@ -460,7 +458,7 @@ __device__ __forceinline__ void tile_body(const TileBatch &B, uint32_t ti, uint3
     const uint32_t i_lo = wbase + (uint32_t)l32 * pitch;
     const uint32_t i_hi = wbase + (uint32_t)(63 - l32) * pitch;
     constexpr uint32_t esz = DT == HH_F32 ? 4u : 2u;
-    const uint32_t tpr = uniform(B.tiles_per_row[ti]);
+    const uint32_t tpr = cols >> 6;
     // t / tpr without a division below 2^22 tiles: (t + 1/2) / tpr lies at
     // least 1/(2 tpr) from an integer, beyond the float product's error
     const uint32_t tr = t < (1u << 22) ? uniform((uint32_t)(((float)t + 0.5f) * B.tpr_inv[ti])) : t / tpr;
@@ -700,10 +698,10 @@ constexpr uint32_t kFusedStageSeq = FusedSeq::kStageLds + FusedSeq::kTabLds;
 constexpr uint32_t kFusedStage = kFusedStageRing > kFusedStageSeq ? kFusedStageRing : kFusedStageSeq;
 static_assert(FusedRing::kSFront == FusedSeq::kSFront, "both decoders' stages start at the same offset");
 constexpr int kFusedMaxWaves = 12;     // 3 per SIMD: 168 registers, tile_body's budget
-constexpr uint32_t kFusedMaxBufs = 8;
+constexpr uint32_t kFusedMaxBufs = 4;
 constexpr uint32_t kFusedLdsMax = 160u * 1024u;
 constexpr uint32_t kSpinLimit = 1u << 24;  // polls of about 64 cycles each
-constexpr uint32_t kFusedMaxRange = 2048;  // slots per workgroup (the bitmaps' size)
+constexpr uint32_t kFusedMaxRange = 512;  // slots per workgroup (the bitmaps' size)
 // tiles a wave claims with one atomic (2 measured 2 % slower on the
 // Llama-3-8B layer: the block claims, checked once per claim, came later)
 constexpr uint32_t kTileClaim = 1;
@@ -739,6 +737,10 @@ constexpr uint32_t kFusedFinalOff = kFusedLeftOff + 4;
 constexpr uint32_t kFusedFailOff = kFusedFinalOff + kFusedMaxRange / 8;
 constexpr uint32_t kFusedFlagWords = (kFusedFailOff + kFusedMaxRange / 8 - kFusedFlagsOff) / 4;
 constexpr uint32_t kFusedWaveOff = kFusedFlagsOff + ((4 * kFusedFlagWords + 15u) & ~15u);
+// 16-bit outputs of tiles with k <= 2176 (every retention up to 0.53): 12
+// waves with a whole-tile park each and three block buffers
+static_assert(kFusedWaveOff + 12u * 64u * kParkPitch<HH_BF16> + 3u * kFusedBuf <= kFusedLdsMax,
+              "twelve waves and three block buffers fit the LDS");
 
 typedef uint32_t __attribute__((address_space(3))) lds_word;
 typedef uint64_t __attribute__((address_space(3))) lds_dword;
@@ -1144,7 +1146,7 @@ __global__ __launch_bounds__(64 * kFusedMaxWaves) void hctt_lz4_fused_kernel(Til
         if ((f & bit_m(q)) == 0u) continue;
         uint32_t bti, bt0, bnt, btb;
         locate(lb_of(q), bti, bt0, bnt, btb);
-        const uint32_t cols = B.cols[bti], tpr = B.tiles_per_row[bti];
+        const uint32_t cols = B.cols[bti], tpr = cols >> 6;
         uint8_t HH_GLOBAL *o = (uint8_t HH_GLOBAL *)B.out[bti];
         for (uint32_t j = wave; j < bnt; j += nw) {
             const uint32_t t = bt0 + j;
@@ -1181,15 +1183,14 @@ hipError_t launch_hctt_decode(const hh_hctt_tensor *tensors, uint32_t n, int dty
             B.out[j] = T.d_out;
             B.status[j] = T.d_tile_status;
             B.start[j] = total;
-            B.tiles_per_row[j] = T.cols / 64;
             B.tpr_inv[j] = 1.0f / (float)(T.cols / 64);
             B.cols[j] = T.cols;
             B.k[j] = T.k;
             B.tb[j] = tb;
-            B.dword_ok[j] = ((tb & 3u) == 0 && ((uintptr_t)T.d_tiles & 3u) == 0) ? 1u : 0u;
+            const bool dword_ok = (tb & 3u) == 0 && ((uintptr_t)T.d_tiles & 3u) == 0;
             total += nt;
             max_k = T.k > max_k ? T.k : max_k;
-            all_dw = all_dw && B.dword_ok[j];
+            all_dw = all_dw && dword_ok;
         }
         if (B.n == 0) continue;
         B.start[B.n] = total;
@@ -1281,7 +1282,6 @@ hipError_t launch_hctt_lz4_fused(const hh_hctt_tensor *tensors, uint32_t n, cons
             B.out[j] = T.d_out;
             B.status[j] = T.d_tile_status;
             B.start[j] = total;
-            B.tiles_per_row[j] = T.cols / 64;
             B.tpr_inv[j] = 1.0f / (float)(T.cols / 64);
             B.cols[j] = T.cols;
             B.k[j] = T.k;

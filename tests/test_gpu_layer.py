@@ -174,15 +174,16 @@ def test_fused_layer_call_reports_a_corrupt_block(cut):
         assert np.abs(x.numpy().reshape(t["rows"], t["cols"]) - ref).max() <= TOL * rms
 
 
-def test_batch_of_more_than_sixteen_tensors_with_empty_ones():
-    # more tensors than one launch takes (16), empty ones among them: every
+def test_batch_of_more_than_thirty_two_tensors_with_empty_ones():
+    # more tensors than one launch takes (32), empty ones among them: every
     # tensor decoded once, each against the oracle, tile statuses all OK
     Hm = H()
     T = G.torch()
     rng = np.random.default_rng(12)
-    shapes = [(64, 128), (0, 64), (128, 64), (64, 64), (0, 0), (64, 192), (128, 128), (64, 64),
-              (192, 64), (64, 0), (64, 256), (128, 192), (64, 64), (128, 64), (64, 320), (192, 128),
-              (0, 128), (64, 64), (256, 64), (64, 128), (128, 128), (64, 192)]
+    half = [(64, 128), (0, 64), (128, 64), (64, 64), (0, 0), (64, 192), (128, 128), (64, 64),
+            (192, 64), (64, 0), (64, 256), (128, 192), (64, 64), (128, 64), (64, 320), (192, 128),
+            (0, 128), (64, 64), (256, 64), (64, 128), (128, 128), (64, 192)]
+    shapes = half + half[::-1]
     descs, refs, outs, tsts = [], [], [], []
     keep = []
     for i, (rows, cols) in enumerate(shapes):
