@@ -269,144 +269,17 @@ def assert_same(T, dtype, fo, fs, bo, bs):
         assert T.equal(sa, sb), i
 
 
-def test_many_tensors_small_blocks_f16():
-    # forty tensors (two launches of at most thirty-two), blocks of one and
-    # of three tiles, f16 output
+@pytest.mark.parametrize("ntensors", [32, 33, 40])
+def test_many_tensors_small_blocks_f16(ntensors):
+    # up to 32 tensors in one launch, more in launches of at most 32; blocks
+    # of one and of three tiles, f16 output
     Hm = H()
     T = G.torch()
     rng = np.random.default_rng(51)
     base = [(64, 64), (128, 64), (64, 192), (192, 128), (64, 64), (256, 64), (128, 128), (64, 320), (320, 64),
             (128, 192), (64, 128), (192, 64), (64, 64), (128, 256), (64, 448), (256, 128), (64, 64), (192, 192),
             (128, 64), (64, 256)]
-    shapes = [("t%d" % i, r, c) for i, (r, c) in enumerate(base + base[::-1])]
-    ks = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, len(shapes))]
-    tpb = min(Hm.FUSED_BLOCK_BYTES // Hm.hctt_tile_bytes(k) for k in ks)
-    L = encode_fixed(Hm, shapes, ks, seed=42, tpb=tpb)
-    fo, st, fs = fused(L, Hm.F32, tpb)
-    assert (st["code"] == 0).all()
-    assert all((s.cpu().numpy() == 0).all() for s in fs)
-    check_against_oracle(L, fo)
-    # the same tiles through the two-launch path: bit-identical
-    bo, codes, scratch, _ = decode(L, Hm.F32)
-    assert (codes == 0).all()
-    T = G.torch()
-    for a, b in zip(fo, bo):
-        assert T.equal(a.view(T.int32), b.view(T.int32))
-
-
-def test_failed_and_short_blocks_poison_only_their_tiles():
-    Hm = H()
-    T = G.torch()
-    shapes = [("a", 256, 512), ("b", 512, 256)]
-    ks = [Hm.hctt_retain_count(0.3), Hm.hctt_retain_count(0.2)]
-    tpb = 5
-    L = encode_fixed(Hm, shapes, ks, seed=43, tpb=tpb)
-    n = L["in_off"].size
-    blob = L["blob"].copy()
-    # block 2: a corrupted offset field is far past the output (CORRUPTED);
-    # block n - 3: the stream ends early (decodes short or fails)
-    bad = [2, n - 3]
-    lens = L["in_len"].copy()
-    o2 = int(L["in_off"][2])
-    blob[o2 + 1:o2 + int(lens[2])] ^= 0x5A
-    lens[n - 3] = max(1, lens[n - 3] // 3)
-    L2 = dict(L, in_len=lens)
-    fo, st, fs = fused(L2, Hm.F32, tpb, blob=blob)
-    # the records are the batched LZ4 kernel's for the same blocks and sizes
-    d_in = G.dev(blob)
-    ref_st = T.zeros(n * 32, dtype=T.uint8, device="cuda")
-    scratch = T.zeros(L["scratch_bytes"], dtype=T.uint8, device="cuda")
-    G.ctx().lz4_decompress_batch(d_in, d_in.numel(), G.dev(L["in_off"]), G.dev(lens), scratch,
-                                 G.dev(L["out_off"]), G.dev(L["out_cap"]), n, ref_st, stream=G.stream())
-    G.sync()
-    ref = np.frombuffer(ref_st.cpu().numpy().tobytes(), dtype=st.dtype)
-    for f in ("code", "detail", "position", "required"):
-        assert np.array_equal(st[f], ref[f]), f
-    short = [b for b in bad if ref["code"][b] != 0 or ref["written"][b] < L["out_cap"][b]]
-    assert len(short) == 2
-    # map blocks to tiles and check the poisoning
-    bo, codes, sc, _ = decode(L, Hm.F32)
-    blk = 0
-    for t, a, b, s in zip(L["tensors"], fo, bo, fs):
-        nt = (t["rows"] // 64) * (t["cols"] // 64)
-        stt = s.cpu().numpy()
-        a_np = a.cpu().numpy().reshape(t["rows"] // 64, 64, t["cols"] // 64, 64)
-        b_np = b.cpu().numpy().reshape(t["rows"] // 64, 64, t["cols"] // 64, 64)
-        tpr = t["cols"] // 64
-        for j in range((nt + tpb - 1) // tpb):
-            g = blk + j
-            good = int(st["written"][g]) if st["code"][g] == 0 else 0
-            tb = Hm.hctt_tile_bytes(t["k"])
-            for tt in range(j * tpb, min(nt, (j + 1) * tpb)):
-                r, c = divmod(tt, tpr)
-                lo, hi = (tt - j * tpb) * tb, (tt - j * tpb + 1) * tb
-                if hi <= good:      # every byte of the tile produced
-                    assert stt[tt] == 0
-                    assert np.array_equal(a_np[r, :, c, :].view(np.int32), b_np[r, :, c, :].view(np.int32))
-                elif lo >= good:    # none: all zero bytes
-                    assert g in bad
-                    assert stt[tt] == Hm.CORRUPTED_DATA, (t["name"], g, tt)
-                    assert (a_np[r, :, c, :] == 0).all()
-        blk += (nt + tpb - 1) // tpb
-
-
-def test_argument_errors():
-    Hm = H()
-    k = Hm.hctt_retain_count(0.3)
-    L = encode_fixed(Hm, [("a", 128, 128)], [k], seed=44, tpb=2)
-    assert L["in_off"].size == 2
-    T = G.torch()
-    d_in = G.dev(L["blob"])
-    st = T.zeros(64, dtype=T.uint8, device="cuda")
-    o = T.empty(128 * 128, dtype=T.float32, device="cuda")
-    args = (d_in, d_in.numel(), G.dev(L["in_off"]), G.dev(L["in_len"]))
-    assert G.ctx().hctt_decode_lz4_fused(*args, 3, st, [(128, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
-    assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], 14) == Hm.UNSUPPORTED
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(100, 128, k, o)], 2) == Hm.INVALID_ARGUMENT
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(64, (1 << 24) + 64, k, o)], 2) == Hm.INVALID_ARGUMENT
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], 2) == Hm.OK
-    # the per-tensor entry (hh_hctt_decode_lz4_fused_tpb): a zero count, a
-    # block over HH_FUSED_BLOCK_BYTES, a block total that does not match
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], [0]) == Hm.INVALID_ARGUMENT
-    assert G.ctx().hctt_decode_lz4_fused(*args, 1, st, [(128, 128, k, o)], [14]) == Hm.UNSUPPORTED
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o), (64, 64, k, o)], [2, 1]) == \
-        Hm.INVALID_ARGUMENT
-    assert G.ctx().hctt_decode_lz4_fused(*args, 2, st, [(128, 128, k, o)], [2]) == Hm.OK
-
-
-def both_paths(L, dtype, tpb, blob=None, lens=None):
-    """The same blocks through the fused call and the two-launch call:
-    outputs, tile statuses and block records (the two-launch path's LZ4
-    records are hh_lz4_decompress_batch's)."""
-    L2 = dict(L)
-    if blob is not None:
-        L2["blob"] = blob
-    if lens is not None:
-        L2["in_len"] = lens
-    fo, st, fs = fused(L2, dtype, tpb)
-    bo, codes, scratch, bs = decode(L2, dtype)
-    del scratch
-    return fo, st, fs, bo, codes, bs
-
-
-def assert_same(T, dtype, fo, fs, bo, bs):
-    Hm = H()
-    view = T.int32 if dtype == Hm.F32 else T.int16
-    for i, (a, b, sa, sb) in enumerate(zip(fo, bo, fs, bs)):
-        assert T.equal(a.view(view), b.view(view)), i
-        assert T.equal(sa, sb), i
-
-
-def test_many_tensors_small_blocks_f16():
-    # twenty tensors (two launches of at most sixteen), blocks of one and of
-    # three tiles, f16 output
-    Hm = H()
-    T = G.torch()
-    rng = np.random.default_rng(51)
-    shapes = [("t%d" % i, r, c) for i, (r, c) in enumerate(
-        [(64, 64), (128, 64), (64, 192), (192, 128), (64, 64), (256, 64), (128, 128), (64, 320), (320, 64),
-         (128, 192), (64, 128), (192, 64), (64, 64), (128, 256), (64, 448), (256, 128), (64, 64), (192, 192),
-         (128, 64), (64, 256)])]
+    shapes = [("t%d" % i, r, c) for i, (r, c) in enumerate((base + base[::-1])[:ntensors])]
     ks = [Hm.hctt_retain_count(float(r)) for r in rng.uniform(0.10, 0.50, len(shapes))]
     for tpb in (1, 3):
         L = encode_fixed(Hm, shapes, ks, seed=52 + tpb, tpb=tpb)
