@@ -288,7 +288,12 @@ int32_t hh_hctt_decode_lz4_batch(hh_context *ctx, const uint8_t *d_in, size_t in
  * the waves is bounded (HH_OPT_FUSED_POLL_LIMIT polls); when one runs out,
  * every block record and every tile status of that workgroup's blocks
  * report HH_ERR_DEVICE and those tiles' outputs are unspecified (the
- * kernel still ends; the next call decodes normally). */
+ * kernel still ends; the next call decodes normally).  One launch takes up
+ * to 32 tensors (more go to further launches of up to 32, in order); a
+ * launch has a fixed cost (its workgroups' start, the first blocks' decode,
+ * the last tiles' drain) of about 10 us on an MI355X, so several layers'
+ * tensors passed in one call, their blocks in one buffer, decode faster
+ * than one call per layer. */
 #define HH_FUSED_BLOCK_BYTES 16352u
 int32_t hh_hctt_decode_lz4_fused(hh_context *ctx, const uint8_t *d_in, size_t in_total,
                                  const uint64_t *d_in_off, const uint32_t *d_in_len, uint32_t nblocks,
